@@ -1,0 +1,204 @@
+"""Config 5 benchmark: bs=1 greedy decode of the int4 Qwen3.5-4B-shaped hybrid on one MI355X.
+
+    python bench.py [--steps 256] [--warmup 8] [--prompt-len 4096] [--no-cpu-baseline]
+
+A step is one greedy decode token (one replay of the captured decode graph). The prompt
+(4096 random ids, seed 1) is prefilled untimed, the cache is snapshotted, ``warmup`` steps
+run and the snapshot is restored, then exactly ``steps`` tokens are timed with HIP events
+between device synchronisations. Weights are random-init in the model's real shapes
+(synthetic data: there is no checkpoint here). One JSON line is printed.
+
+``roofline`` is for the dominant kernel, the tied-head int4 GEMV (one launch = 248320 x 2560
+int4 + scales + x + norm weight + bf16 logits), timed with HIP events on the decode stream
+right after the decode run. ``cpu_baseline`` times the CPU oracle (``oracle/``, plain
+PyTorch, fp32 dequant as the reference does) on one decode step of the same model at the
+same context on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode tok/s bs=1 ctx4k on 1 MI355X; achieved HBM GB/s as % of 8 TB/s"
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prompt-len", type=int, default=4096)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--head-iters", type=int, default=20)
+    return ap.parse_args()
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_head(engine, iters: int) -> float:
+    """Average duration (s) of the tied-head GEMV launch, HIP events on the current stream."""
+    from deltaforge_amd import _native as N
+
+    stream = torch.cuda.current_stream()
+    g = engine.head
+    run = lambda: engine._gemv(g, engine.h, prologue=N.PRO_RMSNORM, norm_w=engine.final_norm,  # noqa: E731
+                               epilogue=N.EPI_LOGITS, out=engine.logits)
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        run()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters / 1e3
+
+
+def cpu_baseline(model, position: int) -> dict:
+    """One decode step of the CPU oracle at ``position`` (bounded sample of the same workload)."""
+    from oracle.int4 import dequantise_int4_k_major
+    from oracle.model import OracleModel
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    params = dict(model.params)
+    head = model.linears["lm_head"]
+    params["embed_tokens.weight"] = dequantise_int4_k_major(head.packed, head.scale, 128).to(torch.bfloat16).t().contiguous()
+    oracle = OracleModel(model.config, params, {n: (w.packed, w.scale, 128) for n, w in model.linears.items()})
+    cache = oracle.new_cache(1, position + 2)
+    gen = torch.Generator().manual_seed(3)
+    for layer in cache.layers:  # a filled cache: values do not change the cost
+        for t in layer.values():
+            t.copy_(torch.randn(t.shape, generator=gen).to(t.dtype) * 0.1)
+    cache.seq_len = position
+    token = torch.tensor([[17]])
+    times = []
+    with torch.no_grad():
+        for _ in range(2):
+            t0 = time.perf_counter()
+            oracle.forward(token, cache, num_logits_to_keep=1)
+            times.append(time.perf_counter() - t0)
+            cache.seq_len = position
+    best = min(times)
+    return {"value": 1.0 / best, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"1 decode step (best of 2) of the same 32-layer int4 model at context {position}, "
+                      f"CPU oracle (plain PyTorch, fp32 dequant per linear), {threads} threads",
+            "seconds_per_token": best}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path has no "
+              "multi-GPU mode: see DESIGN.md on how it would shard).", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    from deltaforge_amd import synth
+    from deltaforge_amd.config import qwen3_5_4b_config
+    from deltaforge_amd.engine import DecodeEngine
+    from deltaforge_amd.harness.bytes_model import HBM_PEAK_BYTES_PER_S, int4_bytes, mean_decode_bytes
+
+    cfg = qwen3_5_4b_config()
+    t0 = time.perf_counter()
+    model = synth.synth_model(cfg, seed=args.seed)
+    log(f"synthetic model drawn in {time.perf_counter() - t0:.1f}s ({model.nbytes() / 1e9:.2f} GB)")
+    engine = DecodeEngine(model, max_seq_len=args.prompt_len + args.steps + args.warmup + 64,
+                          max_new_tokens=args.steps + args.warmup)
+    torch.cuda.synchronize()
+    log(f"engine ready: {engine.weight_bytes() / 1e9:.3f} GB of int4 weights in HBM")
+    prompt = synth.prompt_ids(cfg.vocab_size, args.prompt_len, seed=1)
+    t0 = time.perf_counter()
+    engine.prefill(prompt.cuda())
+    torch.cuda.synchronize()
+    log(f"prefill of {args.prompt_len} tokens (teacher-forced decode steps) in {time.perf_counter() - t0:.1f}s")
+    snap = engine.snapshot()
+    engine.decode(args.warmup)
+    torch.cuda.synchronize()
+    engine.restore(snap)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    engine.decode(args.steps)
+    end.record(stream)
+    torch.cuda.synchronize()
+    seconds = start.elapsed_time(end) / 1e3
+    tok_s = args.steps / seconds
+    bytes_per_token = mean_decode_bytes(cfg, args.prompt_len, args.steps)
+    achieved = bytes_per_token * tok_s
+    log(f"decode: {args.steps} tokens in {seconds * 1e3:.1f} ms -> {tok_s:.1f} tok/s, "
+        f"{achieved / 1e9:.1f} GB/s ({100 * achieved / HBM_PEAK_BYTES_PER_S:.1f}% of 8 TB/s)")
+    tokens = engine.token_log[0, :8].tolist()
+
+    head_s = time_head(engine, args.head_iters)
+    head_bytes = int4_bytes(cfg.hidden_size, cfg.vocab_size) + 2 * cfg.hidden_size * 2 + cfg.vocab_size * 2
+    head_gbps = head_bytes / head_s / 1e9
+    log(f"head GEMV: {head_s * 1e6:.1f} us/launch, {head_gbps:.1f} GB/s")
+
+    baseline = None
+    if not args.no_cpu_baseline:
+        t0 = time.perf_counter()
+        baseline = cpu_baseline(model, args.prompt_len)
+        log(f"cpu baseline: {baseline['seconds_per_token']:.2f} s/token on {baseline['cores']} threads "
+            f"(sample took {time.perf_counter() - t0:.1f}s)")
+        baseline.pop("seconds_per_token")
+
+    out = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(seconds * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "config 5: bs=1 greedy decode of a random-init 32-layer Qwen3.5-4B-shaped hybrid "
+                        "(24 Gated DeltaNet + 8 gated GQA layers), int4 group-128 weights, tied int4 head, "
+                        f"prompt {args.prompt_len} ids (seed 1), {args.steps} timed greedy steps",
+            "batch": 1,
+            "context": args.prompt_len,
+            "weights": "int4 g128 nibbles + bf16 scales; bf16 activations; fp32 accumulation and state",
+            "bytes_per_token": int(bytes_per_token),
+            "achieved_GBps": round(achieved / 1e9, 1),
+            "hbm_fraction": round(achieved / HBM_PEAK_BYTES_PER_S, 4),
+            "first_tokens": tokens,
+        },
+        "roofline": {
+            "kernel": "w4_gemv_kernel<RMSNORM, LOGITS> (tied head, 248320 x 2560)",
+            "bound": "hbm",
+            "achieved": round(head_gbps, 1),
+            "peak": 8000.0,
+            "unit": "GB/s",
+            "frac": round(head_gbps / 8000.0, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": baseline,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,109 @@
+"""ctypes binding of ``libdeltaforge_hip.so`` (declared in ``include/deltaforge_hip.h``).
+
+There is no fallback: if the library is missing or fails to load, every op raises. The
+library is built in-tree by ``python -m deltaforge_amd.build`` (or ``__graft_entry__.build``).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libdeltaforge_hip.so"
+
+STATUS = {0: "ok", 1: "bad argument", 2: "kernel launch failed", 3: "workspace too small"}
+
+PRO_NONE, PRO_RMSNORM, PRO_ADD_RMSNORM, PRO_GATED_RMSNORM = 0, 1, 2, 3
+EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU, EPI_LOGITS = 0, 1, 2, 3
+
+_vp = C.c_void_p
+_i = C.c_int
+_f = C.c_float
+_sz = C.c_size_t
+
+
+class Int4GemvArgs(C.Structure):
+    _fields_ = [
+        ("w", _vp), ("s", _vp), ("x", _vp), ("x2", _vp), ("norm_w", _vp), ("res", _vp),
+        ("out", _vp), ("h_out", _vp), ("part", _vp),
+        ("rows", _i), ("K", _i), ("N", _i), ("ldx", _i), ("ldx2", _i), ("ldo", _i),
+        ("tiles_per_workgroup", _i), ("ksplit", _i), ("groups_per_split", _i),
+        ("prologue", _i), ("epilogue", _i),
+        ("eps", _f),
+    ]
+
+
+class GatedDeltaArgs(C.Structure):
+    _fields_ = [
+        ("qkv", _vp), ("a", _vp), ("b", _vp), ("A_log", _vp), ("dt_bias", _vp), ("conv_w", _vp),
+        ("conv_in", _vp), ("conv_out", _vp), ("conv_ring", _vp), ("position", _vp),
+        ("state", _vp), ("out", _vp),
+        ("batch", _i), ("ld_qkv", _i), ("ld_ab", _i),
+        ("num_k_heads", _i), ("num_v_heads", _i), ("head_k_dim", _i), ("head_v_dim", _i),
+        ("conv_mode", _i),
+    ]
+
+
+class AttnDecodeArgs(C.Structure):
+    _fields_ = [
+        ("q", _vp), ("k", _vp), ("v", _vp), ("q_norm_w", _vp), ("k_norm_w", _vp), ("inv_freq", _vp),
+        ("k_cache", _vp), ("v_cache", _vp), ("position", _vp), ("out", _vp),
+        ("batch", _i), ("ld_q", _i), ("ld_kv", _i), ("num_q_heads", _i), ("num_kv_heads", _i), ("head_dim", _i),
+        ("rotary_dim", _i), ("max_len", _i), ("splits", _i), ("gate", _i), ("eps", _f),
+    ]
+
+
+# name -> (restype, argtypes); the exported surface of include/deltaforge_hip.h
+SIGNATURES = {
+    "df_int4_gemv_plan": (_i, [_i, _i, _i, _i, _i, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i), C.POINTER(_sz)]),
+    "df_int4_gemv_workspace_bytes": (_sz, [_i, _i, _i]),
+    "df_int4_gemv": (_i, [C.POINTER(Int4GemvArgs), _vp, _sz, _vp]),
+    "df_int4_repack": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
+    "df_int4_dequant": (_i, [_vp, _vp, _i, _i, _vp, _vp]),
+    "df_gated_delta_step": (_i, [C.POINTER(GatedDeltaArgs), _vp]),
+    "df_attention_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
+    "df_attention_decode_splits": (_i, [_i, _i, _i]),
+    "df_attention_decode": (_i, [C.POINTER(AttnDecodeArgs), _vp, _sz, _vp]),
+    "df_rms_norm": (_i, [_vp, _vp, _f, _i, _i, _vp, _vp]),
+    "df_add_rms_norm": (_i, [_vp, _vp, _vp, _f, _i, _i, _vp, _vp, _vp]),
+    "df_silu_mul": (_i, [_vp, _vp, _sz, _vp, _vp]),
+    "df_partial_rope": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp]),
+    "df_causal_conv_step": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp]),
+    "df_embed_int4": (_i, [_vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i, _vp, _vp]),
+    "df_argmax_workspace_bytes": (_sz, [_i, _i]),
+    "df_argmax": (_i, [_vp, _i, _i, _vp, _vp, _i, _vp, _i, _vp, _vp, _sz, _vp]),
+}
+
+_LIB: C.CDLL | None = None
+
+
+class NativeError(RuntimeError):
+    """A library entry point returned a non-zero status."""
+
+
+def lib() -> C.CDLL:
+    """Load the HIP library once. Raises if it is missing: there is no CPU fallback."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing; build it with `python -m deltaforge_amd.build`. "
+                "deltaforge_amd has no fallback path."
+            )
+        handle = C.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _LIB = handle
+    return _LIB
+
+
+def check(status: int, op: str) -> None:
+    if status != 0:
+        raise NativeError(f"deltaforge::{op}: {STATUS.get(status, status)} (status {status})")
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a tensor (None for None)."""
+    return None if t is None else t.data_ptr()

@@ -1,0 +1,322 @@
+// Single-token gated GQA attention with split-KV for gfx950.
+//
+// Grid (split, kv_head, batch); 256 threads = 4 waves = the 4 query heads sharing the KV
+// head (reference gqa_decode.py:95: q head h reads KV head h / groups), so every K/V byte is
+// read once per split.
+//
+//   prologue  wave w: q_norm (RMSNorm(1+w) over 256) then partial RoPE of query head
+//             4*kv + w, in the reference's bf16 op order (reference.py:632-643,
+//             137-149, 189-200 with cos/sin = bf16(cos(position * inv_freq))); wave 0 does
+//             the same for the new key, wave 1 stages the new value. The split that owns
+//             `position` writes them into the cache (reference.py:645-650) and uses the
+//             staged copies for that key.
+//   per tile  64 keys: QK on MFMA (16x16x32 bf16, query heads as rows, keys as columns,
+//             fp32 scores x head_dim^-0.5); fp32 online softmax per head; PV on VALU
+//             with each lane owning 4 output dims for all 4 heads.
+//   merge     each split writes (acc[256], m, l) per head; the last workgroup of the KV
+//             head (atomic counter) combines the splits in split order with the
+//             log-sum-exp identity (flash_decode_splitkv.py:135-174), rounds to bf16 and
+//             applies the bf16 output gate (reference.py:558-568, 674-676).
+//
+// Scores and probabilities stay fp32 (the reference rounds both to bf16); this is the
+// more accurate function and is checked against the reference within tolerance.
+#include "common.h"
+#include "deltaforge_hip.h"
+
+namespace df {
+
+constexpr int kHd = 256;
+constexpr int kQPerKv = 4;
+constexpr int kTile = 64;
+
+struct AttnWs {
+  int* counters;
+  float* acc;  // [B][Hq][S][256]
+  float* ml;   // [B][Hq][S][2]
+};
+
+DF_DEVICE AttnWs attn_ws(void* base, int batch, int hq, int hkv, int splits) {
+  AttnWs w;
+  char* p = reinterpret_cast<char*>(base);
+  const size_t counters = ((size_t)batch * hkv * sizeof(int) + 255) & ~(size_t)255;
+  w.counters = reinterpret_cast<int*>(p);
+  w.acc = reinterpret_cast<float*>(p + counters);
+  w.ml = w.acc + (size_t)batch * hq * splits * kHd;
+  return w;
+}
+
+// RMSNorm(1+w) over 256 dims held 4 per lane, then partial RoPE over the first `rot` dims.
+DF_DEVICE void norm_rope4(float x[4], const uint16_t* norm_w, float eps, const float* inv_freq, int rot,
+                          float posf, int lane) {
+  float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(kHd) + eps);
+  float n[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float scaled = x[i] * r;
+    n[i] = round_bf(scaled * (1.0f + bf2f(norm_w[lane * 4 + i])));
+  }
+  const int half = rot / 2;
+  float partner[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) partner[i] = __shfl_xor(n[i], half / 4, 64);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int dim = lane * 4 + i;
+    if (dim < rot) {
+      const float ang = posf * inv_freq[dim % half];
+      const float c = round_bf(cosf(ang)), s = round_bf(sinf(ang));
+      const float rotated = dim < half ? -partner[i] : partner[i];
+      x[i] = round_bf(round_bf(n[i] * c) + round_bf(rotated * s));
+    } else {
+      x[i] = n[i];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, AttnWs ws) {
+  __shared__ __align__(16) uint16_t q_s[kQPerKv][kHd];
+  __shared__ __align__(16) uint16_t knew[kHd];
+  __shared__ __align__(16) uint16_t vnew[kHd];
+  __shared__ float sc[kQPerKv][kTile];
+  __shared__ float alpha_s[kQPerKv];
+  __shared__ float red[kQPerKv][kQPerKv][kHd];
+  __shared__ float ml_s[kQPerKv][2];
+  __shared__ int last_s;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int S = p.splits;
+  const int pos = *p.position;
+  // A position past the cache would write out of bounds; the host cannot see the device
+  // scalar, so every workgroup refuses here (the output is left unwritten).
+  if (pos < 0 || pos >= p.max_len) return;
+  const int nkeys = pos + 1;
+  const int per = (nkeys + S - 1) / S;
+  const int j0 = min(split * per, nkeys);
+  const int j1 = min(j0 + per, nkeys);
+  const float posf = static_cast<float>(pos);
+  const size_t kv_base = ((size_t)b * p.num_kv_heads + kvh) * p.max_len;
+
+  // Prologue: queries, new key, new value.
+  {
+    const int hq = kvh * kQPerKv + wave;
+    const uint16_t* src = p.q + (size_t)b * p.ld_q + (size_t)hq * 2 * kHd + lane * 4;
+    float x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = bf2f(src[i]);
+    norm_rope4(x, p.q_norm_w, p.eps, p.inv_freq, p.rotary_dim, posf, lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q_s[wave][lane * 4 + i] = f2bf(x[i]);
+    if (wave == 0) {
+      const uint16_t* ks = p.k + (size_t)b * p.ld_kv + (size_t)kvh * kHd + lane * 4;
+      float kx[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kx[i] = bf2f(ks[i]);
+      norm_rope4(kx, p.k_norm_w, p.eps, p.inv_freq, p.rotary_dim, posf, lane);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) knew[lane * 4 + i] = f2bf(kx[i]);
+    } else if (wave == 1) {
+      const uint16_t* vsrc = p.v + (size_t)b * p.ld_kv + (size_t)kvh * kHd + lane * 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vnew[lane * 4 + i] = vsrc[i];
+    }
+  }
+  __syncthreads();
+  const bool owner = pos >= j0 && pos < j1;
+  if (owner) {
+    uint16_t* kd = p.k_cache + (kv_base + pos) * kHd;
+    uint16_t* vd = p.v_cache + (kv_base + pos) * kHd;
+    kd[tid] = knew[tid];
+    vd[tid] = vnew[tid];
+  }
+
+  const int col = lane & 15, slot = lane >> 4;
+  const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
+  float m_run = -INFINITY, l_run = 0.0f;  // for head `wave`
+  float acc[kQPerKv][4];
+#pragma unroll
+  for (int h = 0; h < kQPerKv; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[h][i] = 0.0f;
+
+  for (int t0 = j0; t0 < j1; t0 += kTile) {
+    // QK: wave covers keys t0 + 16*wave + col.
+    {
+      const int key = t0 + wave * 16 + col;
+      const bool live = key < j1;
+      const int krow = min(key, p.max_len - 1);
+      const uint16_t* kp = p.k_cache + (kv_base + krow) * kHd + slot * 8;
+      df_f32x4 d4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        uint4 bw = make_uint4(0u, 0u, 0u, 0u);
+        if (live) {
+          bw = key == pos ? *reinterpret_cast<const uint4*>(knew + d * 32 + slot * 8)
+                          : *reinterpret_cast<const uint4*>(kp + d * 32);
+        }
+        uint4 aw = make_uint4(0u, 0u, 0u, 0u);
+        if (col < kQPerKv) aw = *reinterpret_cast<const uint4*>(&q_s[col][d * 32 + slot * 8]);
+        d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, aw),
+                                                     __builtin_bit_cast(df_bf16x8, bw), d4, 0, 0, 0);
+      }
+      if (slot == 0) {
+#pragma unroll
+        for (int i = 0; i < kQPerKv; ++i) sc[i][wave * 16 + col] = live ? d4[i] * scale : -INFINITY;
+      }
+    }
+    __syncthreads();
+    // Online softmax for head `wave`.
+    {
+      const float s = sc[wave][lane];
+      const float tmax = wave_max(s);
+      const float m_new = fmaxf(m_run, tmax);
+      float pr = 0.0f, alpha = 1.0f;
+      if (m_new != -INFINITY) {
+        pr = s == -INFINITY ? 0.0f : expf(s - m_new);
+        alpha = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+      }
+      l_run = l_run * alpha + wave_sum(pr);
+      m_run = m_new;
+      sc[wave][lane] = pr;
+      if (lane == 0) alpha_s[wave] = alpha;
+    }
+    __syncthreads();
+    // PV: wave handles keys t0 + 16*wave .. +15 for all heads; lane owns dims 4*lane..+3.
+    {
+#pragma unroll
+      for (int h = 0; h < kQPerKv; ++h) {
+        const float a = alpha_s[h];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[h][i] *= a;
+      }
+      for (int jj = 0; jj < 16; ++jj) {
+        const int key = t0 + wave * 16 + jj;
+        if (key >= j1) break;
+        uint2 raw;
+        if (key == pos) raw = *reinterpret_cast<const uint2*>(vnew + lane * 4);
+        else raw = *reinterpret_cast<const uint2*>(p.v_cache + (kv_base + key) * kHd + lane * 4);
+        const float v0 = __uint_as_float(raw.x << 16), v1 = __uint_as_float(raw.x & 0xFFFF0000u);
+        const float v2 = __uint_as_float(raw.y << 16), v3 = __uint_as_float(raw.y & 0xFFFF0000u);
+#pragma unroll
+        for (int h = 0; h < kQPerKv; ++h) {
+          const float pr = sc[h][wave * 16 + jj];
+          acc[h][0] += pr * v0;
+          acc[h][1] += pr * v1;
+          acc[h][2] += pr * v2;
+          acc[h][3] += pr * v3;
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // Combine the four waves' PV partials; publish this split's (acc, m, l) per head.
+#pragma unroll
+  for (int h = 0; h < kQPerKv; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][h][lane * 4 + i] = acc[h][i];
+  if (lane == 0) {
+    ml_s[wave][0] = m_run;
+    ml_s[wave][1] = l_run;
+  }
+  __syncthreads();
+  const int hq0 = kvh * kQPerKv;
+#pragma unroll
+  for (int h = 0; h < kQPerKv; ++h) {
+    const float total = red[0][h][tid] + red[1][h][tid] + red[2][h][tid] + red[3][h][tid];
+    const size_t row = ((size_t)b * p.num_q_heads + hq0 + h) * S + split;
+    ws.acc[row * kHd + tid] = total;
+    if (tid == 0) {
+      ws.ml[row * 2] = ml_s[h][0];
+      ws.ml[row * 2 + 1] = ml_s[h][1];
+    }
+  }
+  if (S > 1) {
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+      const int prev = atomicAdd(ws.counters + b * p.num_kv_heads + kvh, 1);
+      last_s = prev == S - 1;
+    }
+    __syncthreads();
+    if (!last_s) return;
+    __threadfence();
+  } else {
+    __syncthreads();
+  }
+
+  // Merge splits (deterministic order), normalise, round, gate.
+#pragma unroll 1
+  for (int h = 0; h < kQPerKv; ++h) {
+    const size_t row0 = ((size_t)b * p.num_q_heads + hq0 + h) * S;
+    float mstar = -INFINITY;
+    for (int s = 0; s < S; ++s) {
+      if (ws.ml[(row0 + s) * 2 + 1] > 0.0f) mstar = fmaxf(mstar, ws.ml[(row0 + s) * 2]);
+    }
+    float num = 0.0f, den = 0.0f;
+    for (int s = 0; s < S; ++s) {
+      const float l = ws.ml[(row0 + s) * 2 + 1];
+      if (l > 0.0f) {
+        const float w = expf(ws.ml[(row0 + s) * 2] - mstar);
+        num += w * ws.acc[(row0 + s) * kHd + tid];
+        den += w * l;
+      }
+    }
+    const float o = round_bf(num / den);
+    const float gx = bf2f(p.q[(size_t)b * p.ld_q + (size_t)(hq0 + h) * 2 * kHd + kHd + tid]);
+    const float gate = round_bf(p.gate == 0 ? sigmoid(gx) : silu(gx));
+    p.out[(size_t)b * p.num_q_heads * kHd + (size_t)(hq0 + h) * kHd + tid] = f2bf(o * gate);
+  }
+  if (S > 1 && tid == 0) ws.counters[b * p.num_kv_heads + kvh] = 0;
+}
+
+}  // namespace df
+
+using namespace df;
+
+extern "C" {
+
+size_t df_attention_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                           int splits) {
+  const size_t counters = ((size_t)batch * num_kv_heads * sizeof(int) + 255) & ~(size_t)255;
+  return counters + (size_t)batch * num_q_heads * splits * (head_dim + 2) * sizeof(float);
+}
+
+int df_attention_decode_splits(int batch, int num_kv_heads, int max_keys) {
+  // Aim for ~1024 workgroups, at least one 64-key tile per split, at most 256 splits.
+  if (batch < 1 || num_kv_heads < 1 || max_keys < 1) return 1;
+  int s = 1024 / (batch * num_kv_heads);
+  const int tiles = (max_keys + kTile - 1) / kTile;
+  if (s > tiles) s = tiles;
+  if (s > 256) s = 256;
+  return s < 1 ? 1 : s;
+}
+
+int df_attention_decode(const DfAttnDecodeArgs* args, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
+  if (!args) return DF_BAD_ARGUMENT;
+  const DfAttnDecodeArgs& a = *args;
+  if (a.head_dim != kHd || a.num_kv_heads < 1 || a.num_q_heads != a.num_kv_heads * kQPerKv || a.batch < 1 ||
+      a.splits < 1 || a.rotary_dim % 8 || a.rotary_dim > kHd || a.rotary_dim < 8 || a.max_len < 1 ||
+      !a.q || !a.k || !a.v || !a.q_norm_w || !a.k_norm_w || !a.inv_freq || !a.k_cache || !a.v_cache ||
+      !a.position || !a.out || (a.gate != 0 && a.gate != 1))
+    return DF_BAD_ARGUMENT;
+  if (a.ld_q % 4 || a.ld_kv % 4) return DF_BAD_ARGUMENT;
+  if (!workspace ||
+      workspace_bytes < df_attention_decode_workspace_bytes(a.batch, a.num_q_heads, a.num_kv_heads, kHd, a.splits))
+    return DF_WORKSPACE_TOO_SMALL;
+  AttnWs ws;
+  {
+    char* p = reinterpret_cast<char*>(workspace);
+    const size_t counters = ((size_t)a.batch * a.num_kv_heads * sizeof(int) + 255) & ~(size_t)255;
+    ws.counters = reinterpret_cast<int*>(p);
+    ws.acc = reinterpret_cast<float*>(p + counters);
+    ws.ml = ws.acc + (size_t)a.batch * a.num_q_heads * a.splits * kHd;
+  }
+  hipLaunchKernelGGL(attn_decode_kernel, dim3(a.splits, a.num_kv_heads, a.batch), dim3(256), 0, stream, a, ws);
+  DF_RETURN_LAUNCH_STATUS();
+}
+
+}  // extern "C"

@@ -1,0 +1,191 @@
+/* C ABI of the MI355X (gfx950) decode kernels for the Qwen3.5-4B int4 path.
+ *
+ * Plain pointers, sizes and a hipStream_t; no torch types. Every entry point is
+ * asynchronous on `stream`, allocates nothing, and returns a DfStatus (0 = OK).
+ * bf16 tensors are passed as uint16_t bit patterns. Scratch ("workspace") is
+ * always caller-owned.
+ *
+ * Each declaration names the reference interface it replaces
+ * (LoveManna/deltaforge, src/deltaforge/...).
+ */
+#ifndef DELTAFORGE_HIP_H
+#define DELTAFORGE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- int4 dequantise-GEMV family ------------------------------------------------ */
+
+enum DfPrologue {
+  DF_PRO_NONE = 0,           /* x as given                                             */
+  DF_PRO_RMSNORM = 1,        /* RMSNorm(1+w) of x over K (reference.py:92-96)          */
+  DF_PRO_ADD_RMSNORM = 2,    /* RMSNorm(1+w) of bf16(x + x2) (reference.py:730-735)   */
+  DF_PRO_GATED_RMSNORM = 3   /* per-128 GatedRMSNorm(x, gate=x2) (reference.py:115-121) */
+};
+
+enum DfEpilogue {
+  DF_EPI_STORE = 0,          /* out = bf16(y)                                          */
+  DF_EPI_RESIDUAL = 1,       /* out = bf16(res + bf16(y)) (reference.py:730, 735)      */
+  DF_EPI_SWIGLU = 2,         /* out = bf16(bf16(silu(gate)) * up) over alternating
+                                16-column gate / up tiles (reference.py:692-693)      */
+  DF_EPI_LOGITS = 3          /* as STORE; the tied LM head's own kernel instance       */
+};
+
+typedef struct DfInt4GemvArgs {
+  const uint8_t* w;          /* tiled nibbles from df_int4_repack                     */
+  const uint16_t* s;         /* tiled bf16 scales from df_int4_repack                 */
+  const uint16_t* x;         /* [rows][ldx] bf16 activations                          */
+  const uint16_t* x2;        /* ADD: residual [rows][ldx2]; GATED: gate z [rows][ldx2] */
+  const uint16_t* norm_w;    /* RMSNORM/ADD: [K]; GATED: [128]                        */
+  const uint16_t* res;       /* RESIDUAL: [rows][ldo] (may alias out)                 */
+  uint16_t* out;             /* [rows][ldo]                                           */
+  uint16_t* h_out;           /* ADD: optional [rows][K] copy of bf16(x + x2)          */
+  float* part;               /* set by the library from the workspace                 */
+  int rows, K, N;            /* rows <= 16; K % 256 == 0; N % 64 == 0                 */
+  int ldx, ldx2, ldo;        /* row strides (elements) of x, x2 and out/res           */
+  int tiles_per_workgroup;   /* 1, 2, 4 or 8 sixteen-column tiles per workgroup       */
+  int ksplit, groups_per_split;  /* K split across workgroups (1 = none)              */
+  int prologue, epilogue;
+  float eps;
+} DfInt4GemvArgs;
+
+/* Choose the launch shape for a GEMV and report the workspace it needs (0 when the
+ * K range is not split across workgroups). Replaces the launch heuristic of
+ * kernels/tiled_gemv.py:291-311. */
+int df_int4_gemv_plan(int rows, int K, int N, int epilogue, int target_waves,
+                      int* tiles_per_workgroup, int* ksplit, int* groups_per_split,
+                      size_t* workspace_bytes);
+size_t df_int4_gemv_workspace_bytes(int rows, int N, int ksplit);
+
+/* y = x @ dequant(W) with an optional fused prologue/epilogue. Every weight is
+ * bf16((nibble - 8) * scale), accumulated in fp32.
+ * Replaces torch_dequant_gemv_int4 (kernels/visible_int4_head.py:187-199) and
+ * tiled_gemv_int4 (kernels/tiled_gemv.py:915-953); with DF_PRO_ADD_RMSNORM it is the
+ * tied head with its final residual + RMSNorm (reference.py:735, 810, 764-777).
+ * With ksplit > 1 a second kernel sums the fp32 partials held in the workspace;
+ * calls sharing a workspace must not overlap. No atomics: results are deterministic. */
+int df_int4_gemv(const DfInt4GemvArgs* args, void* workspace, size_t workspace_bytes,
+                 hipStream_t stream);
+
+/* Canonical K-major int4 (packed [K/2][N] uint8, scale [K/128][N] bf16) -> device tiling.
+ * Replaces the install-time quantise/repack of kernels/tiled_gemv.py:242-278. */
+int df_int4_repack(const uint8_t* packed, const uint16_t* scale, int K, int N,
+                   uint8_t* w_tiled, uint16_t* s_tiled, hipStream_t stream);
+
+/* W[k][n] = bf16((nibble - 8) * scale) from the tiled layout, [K][N] bf16.
+ * Replaces dequantise_int4_k_major(...).to(bf16) (kernels/tiled_gemv.py:281-288). */
+int df_int4_dequant(const uint8_t* w_tiled, const uint16_t* s_tiled, int K, int N,
+                    uint16_t* out, hipStream_t stream);
+
+/* ---- Gated DeltaNet decode step ------------------------------------------------- */
+
+typedef struct DfGatedDeltaArgs {
+  const uint16_t* qkv;       /* [B][ld_qkv] in_proj_qkv output (pre-conv)              */
+  const uint16_t* a;         /* [B][ld_ab] in_proj_a output                            */
+  const uint16_t* b;         /* [B][ld_ab] in_proj_b output                            */
+  const uint16_t* A_log;     /* [Hv]                                                   */
+  const uint16_t* dt_bias;   /* [Hv]                                                   */
+  const uint16_t* conv_w;    /* [C][4]                                                 */
+  const uint16_t* conv_in;   /* mode 0: [B][C][3] history (oldest first)               */
+  uint16_t* conv_out;        /* mode 0: [B][C][3] new history (must not alias conv_in) */
+  uint16_t* conv_ring;       /* mode 1: [B][C][4] ring, slot = position % 4            */
+  const int* position;       /* mode 1: device scalar, the token's position            */
+  float* state;              /* [B][Hv][Dk][Dv] fp32, updated in place                 */
+  uint16_t* out;             /* [B][Hv][Dv] bf16                                       */
+  int batch, ld_qkv, ld_ab;
+  int num_k_heads, num_v_heads, head_k_dim, head_v_dim;
+  int conv_mode;
+} DfGatedDeltaArgs;
+
+/* One token of GatedDeltaNet's middle: 4-tap causal conv + SiLU, q/k L2-norm, q scale,
+ * beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias), then the gated delta rule.
+ * Replaces GatedDeltaNet._causal_conv + recurrent_gated_delta_rule at seq_len 1
+ * (reference.py:496-545; kernels/inline_causal_conv.py:98-129;
+ * kernels/gated_delta_step.py:109-186). Requires Dk == Dv == 128, 4 taps. */
+int df_gated_delta_step(const DfGatedDeltaArgs* args, hipStream_t stream);
+
+/* ---- GQA attention decode (split-KV) -------------------------------------------- */
+
+typedef struct DfAttnDecodeArgs {
+  const uint16_t* q;         /* [B][ld_q] q_proj output: per head [query D | gate D]   */
+  const uint16_t* k;         /* [B][ld_kv] new key   (Hkv x D) before k_norm/RoPE      */
+  const uint16_t* v;         /* [B][ld_kv] new value (Hkv x D)                         */
+  const uint16_t* q_norm_w;  /* [D] (1+w)                                              */
+  const uint16_t* k_norm_w;  /* [D] (1+w)                                              */
+  const float* inv_freq;     /* [rotary/2] fp32 (as the model stores it)               */
+  uint16_t* k_cache;         /* [B][Hkv][max_len][D]                                   */
+  uint16_t* v_cache;         /* [B][Hkv][max_len][D]                                   */
+  const int* position;       /* device scalar: keys already cached (= new position)    */
+  uint16_t* out;             /* [B][Hq*D] gated attention output                       */
+  int batch, ld_q, ld_kv, num_q_heads, num_kv_heads, head_dim, rotary_dim, max_len;
+  int splits;                /* fixed grid; empty splits are allowed                   */
+  int gate;                  /* 0 sigmoid, 1 swish (reference.py:558-568)              */
+  float eps;
+} DfAttnDecodeArgs;
+
+size_t df_attention_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads,
+                                           int head_dim, int splits);
+int df_attention_decode_splits(int batch, int num_kv_heads, int max_keys);
+
+/* q/k RMSNorm + partial RoPE, KV-cache write at `position`, split-KV online-softmax
+ * decode over position+1 keys, deterministic log-sum-exp merge, and the output gate.
+ * Replaces GatedAttention.forward's seq_len==1 path between the projections
+ * (reference.py:621-676; kernels/flash_decode_splitkv.py:177-331;
+ * kernels/gqa_decode.py:322-335). head_dim 256, 4 q heads per KV head. */
+int df_attention_decode(const DfAttnDecodeArgs* args, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
+/* ---- elementwise ops of the slot surface ---------------------------------------- */
+
+/* rms_norm (kernels/fused_rmsnorm_residual.py:201-226; reference.py:92-96). */
+int df_rms_norm(const uint16_t* x, const uint16_t* w, float eps, int rows, int n,
+                uint16_t* out, hipStream_t stream);
+/* add_rms_norm -> (residual + x, rms_norm(residual + x))
+ * (kernels/fused_rmsnorm_residual.py:164-198). */
+int df_add_rms_norm(const uint16_t* x, const uint16_t* residual, const uint16_t* w, float eps,
+                    int rows, int n, uint16_t* resid_out, uint16_t* out, hipStream_t stream);
+/* silu_mul: bf16(bf16(silu(gate)) * up) (kernels/fused_swiglu.py:51-80). */
+int df_silu_mul(const uint16_t* gate, const uint16_t* up, size_t n, uint16_t* out,
+                hipStream_t stream);
+/* partial_rope over (rows = B*H*S) rows of head_dim; cos/sin [B*S][rotary] bf16,
+ * row r uses cos row (r / (H*S)) * S + r % S (kernels/fused_rope.py:97-158). */
+int df_partial_rope(const uint16_t* x, const uint16_t* cos, const uint16_t* sin, int batch,
+                    int heads, int seq, int head_dim, int rotary_dim, uint16_t* out,
+                    hipStream_t stream);
+/* causal_conv step at seq_len 1, history [B][C][3] updated in place
+ * (kernels/inline_causal_conv.py:98-129; kernels/fused_causal_conv.py:136-181). */
+int df_causal_conv_step(const uint16_t* x, uint16_t* conv_cache, const uint16_t* weight,
+                        int batch, int channels, uint16_t* out, hipStream_t stream);
+
+/* ---- decode-loop glue ----------------------------------------------------------- */
+
+/* Tied embedding row from the int4 head: out[b][k] = bf16((nibble - 8) * scale) of
+ * vocab column t (reference.py:804 with the tied, int4-quantised table), where
+ * t = tokens[b], or, when prompt != NULL, t = prompt[b * prompt_len + *position]
+ * (teacher-forced prefill; positions outside the prompt write nothing). */
+int df_embed_int4(const int64_t* tokens, const int64_t* prompt, int prompt_len,
+                  const int* position, int batch, const uint8_t* w_tiled,
+                  const uint16_t* s_tiled, int hidden, int vocab, uint16_t* out,
+                  hipStream_t stream);
+
+size_t df_argmax_workspace_bytes(int rows, int n);
+/* Greedy next token: first index of the max of each bf16 logits row (torch's tie rule;
+ * model.py:145-147 `logits[:, -1].argmax`). After all rows are reduced, the last
+ * workgroup writes tokens[row] (int64); if token_log != NULL (needs step) it also writes
+ * token_log[row * log_stride + *step]; then, once, *position += advance (if position)
+ * and *step += 1 (if step). The workspace must be zero-filled once before first use;
+ * the kernel leaves it ready for the next call. rows <= 256. */
+int df_argmax(const uint16_t* logits, int rows, int n, int64_t* tokens, int64_t* token_log,
+              int log_stride, int* position, int advance, int* step, void* workspace,
+              size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DELTAFORGE_HIP_H */
