@@ -13,8 +13,8 @@
 //   per tile  64 keys: QK on MFMA (16x16x32 bf16, query heads as rows, keys as columns,
 //             fp32 scores x head_dim^-0.5); fp32 online softmax per head; PV on VALU
 //             with each lane owning 4 output dims for all 4 heads.
-//   merge     each split writes (acc[256], m, l) per head; the last workgroup of the KV
-//             head (atomic counter) combines the splits in split order with the
+//   merge     each split writes (acc[256], m, l) per head with write-through stores; the
+//             last workgroup of the KV head (atomic counter) combines the splits in split order with the
 //             log-sum-exp identity (flash_decode_splitkv.py:135-174), rounds to bf16 and
 //             applies the bf16 output gate (reference.py:558-568, 674-676).
 //
@@ -28,6 +28,7 @@ namespace df {
 constexpr int kHd = 256;
 constexpr int kQPerKv = 4;
 constexpr int kTile = 64;
+constexpr int kMaxSplits = 256;
 
 struct AttnWs {
   int* counters;
@@ -227,44 +228,70 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
   for (int h = 0; h < kQPerKv; ++h) {
     const float total = red[0][h][tid] + red[1][h][tid] + red[2][h][tid] + red[3][h][tid];
     const size_t row = ((size_t)b * p.num_q_heads + hq0 + h) * S + split;
-    ws.acc[row * kHd + tid] = total;
+    store_through(ws.acc + row * kHd + tid, total);
     if (tid == 0) {
-      ws.ml[row * 2] = ml_s[h][0];
-      ws.ml[row * 2 + 1] = ml_s[h][1];
+      store_through(ws.ml + row * 2, ml_s[h][0]);
+      store_through(ws.ml + row * 2 + 1, ml_s[h][1]);
     }
   }
   if (S > 1) {
-    __threadfence();
+    publish_wait();
     __syncthreads();
-    if (tid == 0) {
-      const int prev = atomicAdd(ws.counters + b * p.num_kv_heads + kvh, 1);
-      last_s = prev == S - 1;
-    }
+    if (tid == 0) last_s = arrive(ws.counters + b * p.num_kv_heads + kvh) == S - 1;
     __syncthreads();
     if (!last_s) return;
-    __threadfence();
   } else {
     __syncthreads();
   }
 
-  // Merge splits (deterministic order), normalise, round, gate.
+  // Merge splits (deterministic order), normalise, round, gate. All (m, l) pairs are loaded
+  // at once into LDS; wave h turns head h's into split weights w_s = exp(m_s - m*) (0 for an
+  // empty split) and the denominator; then each thread (one output dim) sums its S partials
+  // with independent loads.
+  float* wgt = &red[0][0][0];     // reuse: [2 * kQPerKv][kMaxSplits] = 2048 of the 4096 floats
+  float* den_s = &red[3][0][0];   // past them
+  for (int e = tid; e < kQPerKv * S; e += 256) {
+    const int h = e / S, s = e % S;
+    const size_t row = ((size_t)b * p.num_q_heads + hq0 + h) * S + s;
+    const float m = load_through(ws.ml + row * 2), l = load_through(ws.ml + row * 2 + 1);
+    wgt[h * kMaxSplits + s] = l > 0.0f ? m : -INFINITY;
+    wgt[(kQPerKv + h) * kMaxSplits + s] = l;
+  }
+  __syncthreads();
+  {
+    const int h = wave;
+    float mstar = -INFINITY;
+    for (int s = lane; s < S; s += 64) mstar = fmaxf(mstar, wgt[h * kMaxSplits + s]);
+    mstar = wave_max(mstar);
+    float den = 0.0f;
+    for (int s = lane; s < S; s += 64) {
+      const float m = wgt[h * kMaxSplits + s];
+      const float w = m == -INFINITY ? 0.0f : expf(m - mstar);
+      den += w * wgt[(kQPerKv + h) * kMaxSplits + s];
+      wgt[h * kMaxSplits + s] = w;
+    }
+    den = wave_sum(den);
+    if (lane == 0) den_s[h] = den;
+  }
+  __syncthreads();
 #pragma unroll 1
   for (int h = 0; h < kQPerKv; ++h) {
-    const size_t row0 = ((size_t)b * p.num_q_heads + hq0 + h) * S;
-    float mstar = -INFINITY;
-    for (int s = 0; s < S; ++s) {
-      if (ws.ml[(row0 + s) * 2 + 1] > 0.0f) mstar = fmaxf(mstar, ws.ml[(row0 + s) * 2]);
+    const float* accp = ws.acc + (((size_t)b * p.num_q_heads + hq0 + h) * S) * kHd + tid;
+    const float* w = wgt + h * kMaxSplits;
+    float num0 = 0.0f, num1 = 0.0f, num2 = 0.0f, num3 = 0.0f;
+    int s = 0;
+    for (; s + 4 <= S; s += 4) {
+      const float a0 = load_through(accp + (size_t)(s + 0) * kHd);
+      const float a1 = load_through(accp + (size_t)(s + 1) * kHd);
+      const float a2 = load_through(accp + (size_t)(s + 2) * kHd);
+      const float a3 = load_through(accp + (size_t)(s + 3) * kHd);
+      num0 += w[s] * a0;
+      num1 += w[s + 1] * a1;
+      num2 += w[s + 2] * a2;
+      num3 += w[s + 3] * a3;
     }
-    float num = 0.0f, den = 0.0f;
-    for (int s = 0; s < S; ++s) {
-      const float l = ws.ml[(row0 + s) * 2 + 1];
-      if (l > 0.0f) {
-        const float w = expf(ws.ml[(row0 + s) * 2] - mstar);
-        num += w * ws.acc[(row0 + s) * kHd + tid];
-        den += w * l;
-      }
-    }
-    const float o = round_bf(num / den);
+    for (; s < S; ++s) num0 += w[s] * load_through(accp + (size_t)s * kHd);
+    const float o = round_bf(((num0 + num1) + (num2 + num3)) / den_s[h]);
     const float gx = bf2f(p.q[(size_t)b * p.ld_q + (size_t)(hq0 + h) * 2 * kHd + kHd + tid]);
     const float gate = round_bf(p.gate == 0 ? sigmoid(gx) : silu(gx));
     p.out[(size_t)b * p.num_q_heads * kHd + (size_t)(hq0 + h) * kHd + tid] = f2bf(o * gate);
@@ -299,7 +326,7 @@ int df_attention_decode(const DfAttnDecodeArgs* args, void* workspace, size_t wo
   if (!args) return DF_BAD_ARGUMENT;
   const DfAttnDecodeArgs& a = *args;
   if (a.head_dim != kHd || a.num_kv_heads < 1 || a.num_q_heads != a.num_kv_heads * kQPerKv || a.batch < 1 ||
-      a.splits < 1 || a.rotary_dim % 8 || a.rotary_dim > kHd || a.rotary_dim < 8 || a.max_len < 1 ||
+      a.splits < 1 || a.splits > kMaxSplits || a.rotary_dim % 8 || a.rotary_dim > kHd || a.rotary_dim < 8 || a.max_len < 1 ||
       !a.q || !a.k || !a.v || !a.q_norm_w || !a.k_norm_w || !a.inv_freq || !a.k_cache || !a.v_cache ||
       !a.position || !a.out || (a.gate != 0 && a.gate != 1))
     return DF_BAD_ARGUMENT;

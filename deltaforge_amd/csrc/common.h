@@ -46,6 +46,29 @@ DF_DEVICE float wave_max(float v) {
   return v;
 }
 
+// Cross-workgroup hand-off without an L2 write-back. On gfx950 each XCD has its own L2, so
+// plain stores are not visible to a workgroup on another XCD until a device-scope release
+// (buffer_wbl2), which serialises across workgroups (~50 ns each). Hand-off data is instead
+// written with system-scope stores (sc0 sc1: write-through to memory) and read with
+// system-scope loads (sc0 sc1: miss the caches); `publish_wait` makes the writer's stores
+// complete before it signals (the relaxed agent-scope counter RMW that follows).
+DF_DEVICE void store_through(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+DF_DEVICE void store_through(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+DF_DEVICE float load_through(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+DF_DEVICE int load_through(const int* p) {
+  return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+DF_DEVICE void publish_wait() { __builtin_amdgcn_s_waitcnt(0); }
+DF_DEVICE int arrive(int* counter) {
+  return __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Block-wide sum for blockDim.x == 64 * waves; `scratch` holds >= waves floats.
 template <int WAVES>
 DF_DEVICE float block_sum(float v, float* scratch) {

@@ -37,6 +37,7 @@ constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxRows = 16;
 constexpr int kDepth = 8;  // groups in flight per wave
+constexpr int kNormChunks = 3;  // RMSNorm prologue: K <= kNormChunks * kThreads * 8 = 12288
 
 typedef __bf16 df_bf16x2 __attribute__((ext_vector_type(2)));
 typedef float df_f32x2 __attribute__((ext_vector_type(2)));
@@ -124,44 +125,102 @@ DF_DEVICE void gemv_prologue(const DfInt4GemvArgs& p, uint16_t* xs, int xs_ld, f
     }
   } else if constexpr (PRO == DF_PRO_RMSNORM || PRO == DF_PRO_ADD_RMSNORM) {
     // RMSNorm with the (1 + w) scale over the whole row (reference.py:92-96); with ADD the
-    // row is first bf16(x + residual) (reference.py:735 feeding the next norm).
+    // row is first bf16(x + residual) (reference.py:735 feeding the next norm). Each thread
+    // owns up to kNormChunks 8-element chunks of the row, loaded once (16-byte loads) and
+    // kept in registers between the sum of squares and the scaling.
     const bool write_h =
         (PRO == DF_PRO_ADD_RMSNORM) && p.h_out && blockIdx.x == 0 && blockIdx.y == 0;
+    const int nchunks = p.K / 8;
     for (int m = 0; m < p.rows; ++m) {
       const uint16_t* xr = p.x + (size_t)m * p.ldx;
       const uint16_t* rr = p.x2 + (size_t)m * p.ldx2;
+      uint32_t v[kNormChunks][4];  // the row as packed bf16 (bf16(x + r) is exact in bf16)
       float ss = 0.0f;
-      for (int k = tid; k < p.K; k += kThreads) {
-        float v = bf2f(xr[k]);
-        if constexpr (PRO == DF_PRO_ADD_RMSNORM) v = round_bf(v + bf2f(rr[k]));
-        ss += v * v;
-        if (write_h) p.h_out[(size_t)m * p.K + k] = f2bf(v);
+#pragma unroll
+      for (int j = 0; j < kNormChunks; ++j) {
+        const int c = tid + j * kThreads;
+        if (c < nchunks) {
+          const uint4 raw = load16(xr + c * 8);
+          v[j][0] = raw.x, v[j][1] = raw.y, v[j][2] = raw.z, v[j][3] = raw.w;
+          if constexpr (PRO == DF_PRO_ADD_RMSNORM) {
+            const uint4 rraw = load16(rr + c * 8);
+            const uint32_t rw[4] = {rraw.x, rraw.y, rraw.z, rraw.w};
+#pragma unroll
+            for (int e2 = 0; e2 < 4; ++e2) {
+              const uint16_t lo = f2bf(bf2f(static_cast<uint16_t>(v[j][e2])) + bf2f(static_cast<uint16_t>(rw[e2])));
+              const uint16_t hi = f2bf(bf2f(static_cast<uint16_t>(v[j][e2] >> 16)) +
+                                       bf2f(static_cast<uint16_t>(rw[e2] >> 16)));
+              v[j][e2] = lo | (static_cast<uint32_t>(hi) << 16);
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float val = bf2f(static_cast<uint16_t>(v[j][e >> 1] >> (16 * (e & 1))));
+            ss += val * val;
+          }
+          if (write_h)
+            *reinterpret_cast<uint4*>(p.h_out + (size_t)m * p.K + c * 8) = make_uint4(v[j][0], v[j][1], v[j][2], v[j][3]);
+        }
       }
       ss = block_sum<kWaves>(ss, red);
       const float r = 1.0f / sqrtf(ss / static_cast<float>(p.K) + p.eps);
-      for (int kk = tid; kk < kc; kk += kThreads) {
-        const int k = k0 + kk;
-        float v = bf2f(xr[k]);
-        if constexpr (PRO == DF_PRO_ADD_RMSNORM) v = round_bf(v + bf2f(rr[k]));
-        const float scaled = v * r;
-        xs[m * xs_ld + kk] = f2bf(scaled * (1.0f + bf2f(p.norm_w[k])));
+#pragma unroll
+      for (int j = 0; j < kNormChunks; ++j) {
+        const int c = tid + j * kThreads;
+        const int k = c * 8;
+        if (c < nchunks && k >= k0 && k < k0 + kc) {
+          const uint4 wraw = load16(p.norm_w + k);
+          const uint32_t ww[4] = {wraw.x, wraw.y, wraw.z, wraw.w};
+          uint32_t o[4];
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) {
+            uint16_t pr[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const float scaled = bf2f(static_cast<uint16_t>(v[j][e2] >> (16 * h))) * r;
+              pr[h] = f2bf(scaled * (1.0f + bf2f(static_cast<uint16_t>(ww[e2] >> (16 * h)))));
+            }
+            o[e2] = pr[0] | (static_cast<uint32_t>(pr[1]) << 16);
+          }
+          *reinterpret_cast<uint4*>(xs + m * xs_ld + (k - k0)) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
       }
     }
   } else {  // DF_PRO_GATED_RMSNORM: one 128-group == one value head (reference.py:115-121)
-    const int lane = tid & 63, wave = tid >> 6;
-    const int ng = kc / kGroup, g0 = k0 / kGroup;
-    for (int pair = wave; pair < p.rows * ng; pair += kWaves) {
-      const int m = pair / ng, gi = pair % ng;
-      const size_t base = (size_t)m * p.ldx + (size_t)(g0 + gi) * kGroup + lane * 2;
-      const size_t zbase = (size_t)m * p.ldx2 + (size_t)(g0 + gi) * kGroup + lane * 2;
-      const float v0 = bf2f(p.x[base]), v1 = bf2f(p.x[base + 1]);
-      const float ss = wave_sum(v0 * v0 + v1 * v1);
-      const float r = 1.0f / sqrtf(ss / 128.0f + p.eps);
-      const float z0 = bf2f(p.x2[zbase]), z1 = bf2f(p.x2[zbase + 1]);
-      const float t0 = round_bf(bf2f(p.norm_w[lane * 2]) * round_bf(v0 * r));
-      const float t1 = round_bf(bf2f(p.norm_w[lane * 2 + 1]) * round_bf(v1 * r));
-      xs[m * xs_ld + gi * kGroup + lane * 2] = f2bf(t0 * silu(z0));
-      xs[m * xs_ld + gi * kGroup + lane * 2 + 1] = f2bf(t1 * silu(z1));
+    // 8 elements per thread; a head is 16 consecutive lanes, reduced with lane shuffles.
+    for (int m = 0; m < p.rows; ++m) {
+      for (int c = tid; c < kc / 8; c += kThreads) {
+        const int k = k0 + c * 8;
+        const uint4 xraw = load16(p.x + (size_t)m * p.ldx + k);
+        const uint4 zraw = load16(p.x2 + (size_t)m * p.ldx2 + k);
+        const uint4 wraw = load16(p.norm_w + (k % kGroup));
+        const uint32_t xw[4] = {xraw.x, xraw.y, xraw.z, xraw.w};
+        const uint32_t zw[4] = {zraw.x, zraw.y, zraw.z, zraw.w};
+        const uint32_t ww[4] = {wraw.x, wraw.y, wraw.z, wraw.w};
+        float v[8];
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          v[e] = bf2f(static_cast<uint16_t>(xw[e >> 1] >> (16 * (e & 1))));
+          ss += v[e] * v[e];
+        }
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) ss += __shfl_xor(ss, off, 64);
+        const float r = 1.0f / sqrtf(ss / 128.0f + p.eps);
+        uint32_t o[4];
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          uint16_t pr[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int e = e2 * 2 + h;
+            const float t = round_bf(bf2f(static_cast<uint16_t>(ww[e2] >> (16 * h))) * round_bf(v[e] * r));
+            pr[h] = f2bf(t * silu(bf2f(static_cast<uint16_t>(zw[e2] >> (16 * h)))));
+          }
+          o[e2] = pr[0] | (static_cast<uint32_t>(pr[1]) << 16);
+        }
+        *reinterpret_cast<uint4*>(xs + m * xs_ld + c * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+      }
     }
   }
   __syncthreads();
@@ -448,6 +507,14 @@ int df_int4_gemv(const DfInt4GemvArgs* args, void* workspace, size_t workspace_b
   if (a.prologue != DF_PRO_NONE && !a.norm_w) return DF_BAD_ARGUMENT;
   if (a.epilogue == DF_EPI_RESIDUAL && !a.res) return DF_BAD_ARGUMENT;
   if (reinterpret_cast<uintptr_t>(a.x) % 16 || reinterpret_cast<uintptr_t>(a.w) % 16) return DF_BAD_ARGUMENT;
+  // The norm prologues read x2 and the norm weight with 16-byte loads.
+  if (a.prologue != DF_PRO_NONE && reinterpret_cast<uintptr_t>(a.norm_w) % 16) return DF_BAD_ARGUMENT;
+  if ((a.prologue == DF_PRO_ADD_RMSNORM || a.prologue == DF_PRO_GATED_RMSNORM) &&
+      (reinterpret_cast<uintptr_t>(a.x2) % 16 || a.ldx2 % 8))
+    return DF_BAD_ARGUMENT;
+  if ((a.prologue == DF_PRO_RMSNORM || a.prologue == DF_PRO_ADD_RMSNORM) && a.K > kNormChunks * kThreads * 8)
+    return DF_BAD_ARGUMENT;
+  if (a.h_out && reinterpret_cast<uintptr_t>(a.h_out) % 16) return DF_BAD_ARGUMENT;
   if (a.ksplit > 1) {
     if (!workspace || workspace_bytes < df_int4_gemv_workspace_bytes(a.rows, a.N, a.ksplit))
       return DF_WORKSPACE_TOO_SMALL;

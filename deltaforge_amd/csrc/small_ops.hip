@@ -119,7 +119,7 @@ __global__ void embed_int4_kernel(const int64_t* __restrict__ tokens, const int6
 
 // argmax with torch's tie rule (first index of the maximum). Each workgroup reduces a
 // chunk of one row to (value, index); the last workgroup reduces the chunks in order.
-constexpr int kArgmaxChunk = 4096;
+constexpr int kArgmaxChunk = 1024;
 
 DF_DEVICE void argmax_merge(float& v, int& i, float ov, int oi) {
   if (ov > v || (ov == v && oi < i)) {
@@ -141,7 +141,17 @@ __global__ __launch_bounds__(256) void argmax_kernel(const uint16_t* __restrict_
   float v = -INFINITY;
   int idx = 0x7FFFFFFF;
   const int end = min(n, (chunk + 1) * kArgmaxChunk);
-  for (int k = chunk * kArgmaxChunk + threadIdx.x; k < end; k += 256) argmax_merge(v, idx, bf2f(lr[k]), k);
+  float vals[kArgmaxChunk / 256];
+#pragma unroll
+  for (int j = 0; j < kArgmaxChunk / 256; ++j) {
+    const int k = chunk * kArgmaxChunk + j * 256 + threadIdx.x;
+    vals[j] = k < end ? bf2f(lr[k]) : -INFINITY;
+  }
+#pragma unroll
+  for (int j = 0; j < kArgmaxChunk / 256; ++j) {
+    const int k = chunk * kArgmaxChunk + j * 256 + threadIdx.x;
+    if (k < end) argmax_merge(v, idx, vals[j], k);
+  }
   for (int off = 32; off > 0; off >>= 1) {
     const float ov = __shfl_xor(v, off, 64);
     const int oi = __shfl_xor(idx, off, 64);
@@ -155,21 +165,36 @@ __global__ __launch_bounds__(256) void argmax_kernel(const uint16_t* __restrict_
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int w = 1; w < 4; ++w) argmax_merge(v, idx, sv[w], si[w]);
-    pv[row * chunks + chunk] = v;
-    pi[row * chunks + chunk] = idx;
-    __threadfence();
-    last = atomicAdd(counter, 1) == rows * chunks - 1;
+    store_through(pv + row * chunks + chunk, v);
+    store_through(pi + row * chunks + chunk, idx);
+    publish_wait();
+    last = arrive(counter) == rows * chunks - 1;
   }
   __syncthreads();
   if (!last) return;
-  __threadfence();
-  if (threadIdx.x < rows) {
-    const int r = threadIdx.x;
+  // Final reduction per row: every thread takes chunk partials at once, then lanes and
+  // waves merge (the tie rule keeps the lowest index, so the order does not matter).
+  for (int r = 0; r < rows; ++r) {
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
-    for (int c = 0; c < chunks; ++c) argmax_merge(bv, bi, pv[r * chunks + c], pi[r * chunks + c]);
-    tokens[r] = bi;
-    if (log && step) log[(size_t)r * log_stride + *step] = bi;
+    for (int c = threadIdx.x; c < chunks; c += 256)
+      argmax_merge(bv, bi, load_through(pv + r * chunks + c), load_through(pi + r * chunks + c));
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      argmax_merge(bv, bi, ov, oi);
+    }
+    __syncthreads();
+    if (lane == 0) {
+      sv[wave] = bv;
+      si[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w = 1; w < 4; ++w) argmax_merge(bv, bi, sv[w], si[w]);
+      tokens[r] = bi;
+      if (log && step) log[(size_t)r * log_stride + *step] = bi;
+    }
   }
   __syncthreads();
   if (threadIdx.x == 0) {

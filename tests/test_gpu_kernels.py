@@ -113,14 +113,14 @@ def test_config4_mlp_block(rows):
     close(act, want_act, what=f"gate/up+swiglu rows={rows}", flip_frac=1e-4)
     act_cpu = act.cpu()
     close(out, inp["x"] + dequant_gemv(act_cpu, down.packed, down.scale, 128), what=f"down+residual rows={rows}")
-    # The whole block against the oracle's own chain: 1-ulp flips of the bf16 intermediates
-    # (different fp32 summation order) propagate into the 9216-term down projection, so the
-    # composite is held to 4 bf16 ulps of each output (and the per-op bars above are exact).
+    # The whole block against the oracle's own chain: a 1-ulp flip of one bf16 intermediate
+    # (different fp32 summation order) reaches every output through the 9216-term down
+    # projection as an absolute error, so the composite is held normwise: max error within
+    # 1e-2 of the output's largest magnitude (the per-op bars above are elementwise).
     want = oracle_ops.mlp_block(inp["x"], inp["norm_w"], (gate.packed, gate.scale), (up.packed, up.scale),
                                 (down.packed, down.scale)).float()
-    ulp = torch.exp2(torch.floor(torch.log2(want.abs().clamp_min(1e-30))) - 7)
-    err = (out.float().cpu() - want).abs()
-    assert bool((err <= 4 * ulp + ATOL).all()), f"mlp block rows={rows}: max {float((err / ulp).max()):.1f} ulps"
+    err = float((out.float().cpu() - want).abs().max())
+    assert err <= ATOL + RTOL * float(want.abs().max()), f"mlp block rows={rows}: max abs err {err:.4g}"
 
 
 # -- gated delta --------------------------------------------------------------------------
