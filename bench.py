@@ -8,11 +8,14 @@ run and the snapshot is restored, then exactly ``steps`` tokens are timed with H
 between device synchronisations. Weights are random-init in the model's real shapes
 (synthetic data: there is no checkpoint here). One JSON line is printed.
 
-``roofline`` is for the dominant kernel, the tied-head int4 GEMV (one launch = 248320 x 2560
-int4 + scales + x + norm weight + bf16 logits), timed with HIP events on the decode stream
-right after the decode run. ``cpu_baseline`` times the CPU oracle (``oracle/``, plain
-PyTorch, fp32 dequant as the reference does) on one decode step of the same model at the
-same context on the host cores.
+``roofline`` is for the kernel with the largest share of decode time, the fused
+RMSNorm + gate/up int4 GEMV + SwiGLU (one launch = 2560 x 18432 int4 + bf16 scales + h + norm
+weight + the 9216 bf16 activations it writes). It is timed with HIP events around a captured
+graph of the 32 layers' launches (so the weights stream from HBM, as in decode) on the stream
+the graph runs on. ``--roofline-only`` runs just that graph plus a plain 256 MiB device copy,
+for the ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` passes that calibrate HBM traffic.
+``cpu_baseline`` times the CPU oracle (``oracle/``, plain PyTorch, fp32 dequant as the
+reference does) on one decode step of the same model at the same context on the host cores.
 """
 
 from __future__ import annotations
@@ -39,7 +42,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--prompt-len", type=int, default=4096)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--head-iters", type=int, default=20)
+    ap.add_argument("--roofline-reps", type=int, default=10)
+    ap.add_argument("--roofline-only", action="store_true")
     return ap.parse_args()
 
 
@@ -47,24 +51,62 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_head(engine, iters: int) -> float:
-    """Average duration (s) of the tied-head GEMV launch, HIP events on the current stream."""
+GATE_UP_KERNEL = "w4_gemv_kernel<RMSNORM, SWIGLU> (post-attention norm + gate/up 2560 x 18432 + SwiGLU)"
+# HBM bytes one gate/up launch actually moves: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes
+# over ``--roofline-only`` (12049 KiB fetched, 18 KiB written per launch), each scaled by what
+# the counter reads for a plain 256 MiB device copy (x 2.000 for FETCH_SIZE, x 1.000 for
+# WRITE_SIZE). Re-measure when the kernel changes.
+GATE_UP_TRAFFIC_BYTES = 12049 * 1024 * 2 + 18 * 1024
+
+
+def gate_up_bytes(cfg) -> int:
+    """Algorithmic HBM bytes of one gate/up launch: int4 weights, bf16 scales, the bf16 h row
+    and norm weight read, the bf16 activation row written."""
+    from deltaforge_amd.harness.bytes_model import int4_bytes
+
+    k, n = cfg.hidden_size, 2 * cfg.intermediate_size
+    return int4_bytes(k, n) + 2 * k * 2 + cfg.intermediate_size * 2
+
+
+def time_gate_up(engine, reps: int) -> float:
+    """Average duration (s) of one gate/up launch: a graph of every layer's launch (weights
+    stream from HBM as in decode), replayed ``reps`` times between HIP events."""
     from deltaforge_amd import _native as N
 
-    stream = torch.cuda.current_stream()
-    g = engine.head
-    run = lambda: engine._gemv(g, engine.h, prologue=N.PRO_RMSNORM, norm_w=engine.final_norm,  # noqa: E731
-                               epilogue=N.EPI_LOGITS, out=engine.logits)
-    for _ in range(3):
-        run()
+    def enqueue():
+        for layer in engine.layers:
+            engine._gemv(layer.gate_up, engine.h, prologue=N.PRO_RMSNORM, norm_w=layer.post_norm,
+                         epilogue=N.EPI_SWIGLU, out=engine.act)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        enqueue()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        enqueue()
+    graph.replay()
     torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
-    for _ in range(iters):
-        run()
+    for _ in range(reps):
+        graph.replay()
     end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / iters / 1e3
+    return start.elapsed_time(end) / 1e3 / (reps * len(engine.layers))
+
+
+def copy_calibration(mib: int = 256) -> None:
+    """A plain device copy of ``mib`` MiB (reads and writes exactly that much) for scaling the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE counters."""
+    a = torch.empty(mib * 1024 * 1024 // 2, dtype=torch.bfloat16, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"calibration copy: {mib} MiB read + {mib} MiB written per launch (3 launches)")
 
 
 def cpu_baseline(model, position: int) -> dict:
@@ -111,7 +153,7 @@ def main() -> int:
     from deltaforge_amd import synth
     from deltaforge_amd.config import qwen3_5_4b_config
     from deltaforge_amd.engine import DecodeEngine
-    from deltaforge_amd.harness.bytes_model import HBM_PEAK_BYTES_PER_S, int4_bytes, mean_decode_bytes
+    from deltaforge_amd.harness.bytes_model import HBM_PEAK_BYTES_PER_S, mean_decode_bytes
 
     cfg = qwen3_5_4b_config()
     t0 = time.perf_counter()
@@ -121,6 +163,11 @@ def main() -> int:
                           max_new_tokens=args.steps + args.warmup)
     torch.cuda.synchronize()
     log(f"engine ready: {engine.weight_bytes() / 1e9:.3f} GB of int4 weights in HBM")
+    if args.roofline_only:
+        gu_s = time_gate_up(engine, args.roofline_reps)
+        log(f"gate/up GEMV: {gu_s * 1e6:.2f} us/launch, {gate_up_bytes(cfg) / gu_s / 1e9:.1f} GB/s")
+        copy_calibration()
+        return 0
     prompt = synth.prompt_ids(cfg.vocab_size, args.prompt_len, seed=1)
     t0 = time.perf_counter()
     engine.prefill(prompt.cuda())
@@ -147,10 +194,9 @@ def main() -> int:
         f"{achieved / 1e9:.1f} GB/s ({100 * achieved / HBM_PEAK_BYTES_PER_S:.1f}% of 8 TB/s)")
     tokens = engine.token_log[0, :8].tolist()
 
-    head_s = time_head(engine, args.head_iters)
-    head_bytes = int4_bytes(cfg.hidden_size, cfg.vocab_size) + 2 * cfg.hidden_size * 2 + cfg.vocab_size * 2
-    head_gbps = head_bytes / head_s / 1e9
-    log(f"head GEMV: {head_s * 1e6:.1f} us/launch, {head_gbps:.1f} GB/s")
+    gu_s = time_gate_up(engine, args.roofline_reps)
+    gu_gbps = gate_up_bytes(cfg) / gu_s / 1e9
+    log(f"gate/up GEMV: {gu_s * 1e6:.2f} us/launch, {gu_gbps:.1f} GB/s")
 
     baseline = None
     if not args.no_cpu_baseline:
@@ -186,13 +232,15 @@ def main() -> int:
             "first_tokens": tokens,
         },
         "roofline": {
-            "kernel": "w4_gemv_kernel<RMSNORM, LOGITS> (tied head, 248320 x 2560)",
+            "kernel": GATE_UP_KERNEL,
             "bound": "hbm",
-            "achieved": round(head_gbps, 1),
+            "achieved": round(gu_gbps, 1),
             "peak": 8000.0,
             "unit": "GB/s",
-            "frac": round(head_gbps / 8000.0, 4),
-            "traffic": None,
+            "frac": round(gu_gbps / 8000.0, 4),
+            "traffic": GATE_UP_TRAFFIC_BYTES,
+            "us_per_launch": round(gu_s * 1e6, 3),
+            "bytes_per_launch": gate_up_bytes(cfg),
         },
         "cpu_baseline": baseline,
     }

@@ -1,0 +1,222 @@
+"""The drop-in boundary on the CPU: the C ABI's exported surface, the registry's invariants,
+the custom ops' error order and fake kernels, and champion installation.
+
+Nothing here launches a kernel; the GPU parity of the same ops is in test_gpu_boundary.py.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from deltaforge_amd import _native as N
+from deltaforge_amd.config import mid_config
+from deltaforge_amd.kernels import (
+    REGISTRY,
+    REPLACEABLE_OPS,
+    KernelRegistry,
+    KernelStatus,
+    RegistryError,
+    hip_ops,
+)
+from deltaforge_amd.model import INSTALLERS, InstallerMissing, apply_champions, greedy_decode
+
+ROOT = Path(__file__).resolve().parents[1]
+BF16 = torch.bfloat16
+
+
+def header_symbols() -> set[str]:
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"^\s*(?:int|size_t|void)\s+(df_\w+)\s*\(", text, flags=re.M))
+    return names
+
+
+@pytest.fixture(scope="module")
+def built_library() -> ctypes.CDLL:
+    if not N.LIB_PATH.exists():
+        from deltaforge_amd import build
+
+        build.build()
+    return ctypes.CDLL(str(N.LIB_PATH))
+
+
+def test_library_exports_every_header_symbol(built_library):
+    names = header_symbols()
+    assert len(names) >= 17, names
+    missing = [n for n in sorted(names) if not hasattr(built_library, n)]
+    assert not missing, f"declared in include/ but not exported: {missing}"
+    # and the ctypes table binds exactly the declared surface
+    assert set(N.SIGNATURES) <= names, set(N.SIGNATURES) - names
+
+
+def test_python_binding_loads(built_library):
+    lib = N.lib()  # no device call happens at load time
+    for name in N.SIGNATURES:
+        assert getattr(lib, name).restype is not None or True
+
+
+# -- registry -----------------------------------------------------------------------------
+
+
+def test_replaceable_ops_are_the_reference_slots():
+    # reference kernels/__init__.py:56-80
+    assert REPLACEABLE_OPS == {
+        "rms_norm", "rms_norm_residual", "swiglu_mlp", "qkv_projection_rope", "gated_delta_rule",
+        "gqa_attention", "kv_cache_update", "decode_step", "causal_conv", "decode_cache",
+    }
+
+
+def test_one_champion_per_op_and_promote_swaps_atomically():
+    reg = KernelRegistry()
+    reg.register("a", impl=lambda: None, replaces="rms_norm", status=KernelStatus.CHAMPION)
+    with pytest.raises(RegistryError):
+        reg.register("b", impl=lambda: None, replaces="rms_norm", status=KernelStatus.CHAMPION)
+    reg.register("b", impl=lambda: None, replaces="rms_norm")
+    reg.promote("b")
+    assert reg.champion("rms_norm").name == "b"
+    assert reg.get("a").status is KernelStatus.RETIRED
+    with pytest.raises(RegistryError):
+        reg.register("c", impl=lambda: None, replaces="no_such_op")
+    with pytest.raises(RegistryError):
+        reg.register("b", impl=lambda: None, replaces="rms_norm")
+    reg.check_invariants()
+
+
+def test_shipped_champions_cover_the_hot_path():
+    REGISTRY.check_invariants()
+    champs = {op: e.name for op, e in REGISTRY.champions().items()}
+    for op in ("decode_step", "swiglu_mlp", "rms_norm", "rms_norm_residual", "qkv_projection_rope",
+               "causal_conv", "gated_delta_rule", "gqa_attention", "decode_cache"):
+        assert op in champs, op
+    for name in champs.values():
+        assert name in INSTALLERS, f"champion {name} has no installer"
+
+
+def test_apply_champions_refuses_a_champion_without_installer():
+    reg = KernelRegistry()
+    reg.register("orphan", impl=lambda: None, replaces="rms_norm", status=KernelStatus.CHAMPION)
+    with pytest.raises(InstallerMissing):
+        apply_champions(object(), reg, installers={})
+
+
+def test_apply_champions_installs_the_decode_loop():
+    from deltaforge_amd.synth import synth_model
+
+    model = synth_model(mid_config(num_layers=4), seed=0)
+    applied = apply_champions(model)
+    assert set(applied) == {e.name for e in REGISTRY.champions().values()}
+    assert callable(model.decode_loop)
+    with pytest.raises(ValueError):
+        greedy_decode(model, torch.zeros((1, 4), dtype=torch.int64), 0)
+
+
+def test_greedy_decode_without_loop_fails_loudly():
+    class Bare:
+        pass
+
+    with pytest.raises(InstallerMissing):
+        greedy_decode(Bare(), torch.zeros((1, 4), dtype=torch.int64), 2)
+
+
+# -- custom ops: errors before device, no fallback, fakes ----------------------------------
+
+
+def _int4(k=256, n=64, device="cpu"):
+    packed = torch.zeros((k // 2, n), dtype=torch.uint8, device=device)
+    scale = torch.ones((k // 128, n), dtype=BF16, device=device)
+    return packed, scale
+
+
+def test_tiled_gemv_int4_shape_errors_come_first():
+    packed, scale = _int4()
+    with pytest.raises(ValueError):
+        hip_ops.tiled_gemv_int4(torch.zeros((1, 128), dtype=BF16), packed, scale, 128)  # wrong K
+    with pytest.raises(ValueError):
+        hip_ops.tiled_gemv_int4(torch.zeros((1, 256), dtype=BF16), packed, scale, 64)  # wrong group
+    with pytest.raises(ValueError):
+        hip_ops.tiled_gemv_int4(torch.zeros((1, 256), dtype=torch.float32), packed, scale, 128)
+    with pytest.raises(ValueError):
+        hip_ops.tiled_gemv_int4(torch.zeros((1, 256), dtype=BF16), packed, scale.float(), 128)
+    with pytest.raises(RuntimeError, match="no PyTorch fallback"):
+        hip_ops.tiled_gemv_int4(torch.zeros((1, 256), dtype=BF16), packed, scale, 128)
+
+
+@pytest.mark.parametrize(
+    "call",
+    [
+        lambda: hip_ops.silu_mul(torch.zeros(8, dtype=BF16), torch.zeros(8, dtype=BF16)),
+        lambda: hip_ops.rms_norm(torch.zeros((2, 8), dtype=BF16), torch.zeros(8, dtype=BF16), 1e-6),
+        lambda: hip_ops.add_rms_norm(torch.zeros((2, 8), dtype=BF16), torch.zeros((2, 8), dtype=BF16),
+                                     torch.zeros(8, dtype=BF16), 1e-6),
+        lambda: hip_ops.apply_partial_rope(torch.zeros((1, 2, 1, 8), dtype=BF16), torch.zeros((1, 1, 4), dtype=BF16),
+                                           torch.zeros((1, 1, 4), dtype=BF16)),
+        lambda: hip_ops.fused_causal_conv_step(torch.zeros((1, 8, 1), dtype=BF16), torch.zeros((1, 8, 3), dtype=BF16),
+                                               torch.zeros((8, 1, 4), dtype=BF16)),
+    ],
+)
+def test_cpu_tensors_raise_without_fallback(call):
+    with pytest.raises(RuntimeError, match="no PyTorch fallback"):
+        call()
+
+
+@pytest.mark.parametrize(
+    "call",
+    [
+        lambda: hip_ops.silu_mul(torch.zeros(8, dtype=BF16), torch.zeros(9, dtype=BF16)),
+        lambda: hip_ops.rms_norm(torch.zeros((2, 8), dtype=BF16), torch.zeros(7, dtype=BF16), 1e-6),
+        lambda: hip_ops.apply_partial_rope(torch.zeros((1, 2, 1, 8), dtype=BF16), torch.zeros((1, 1, 3), dtype=BF16),
+                                           torch.zeros((1, 1, 3), dtype=BF16)),
+        lambda: hip_ops.fused_causal_conv_step(torch.zeros((1, 8, 2), dtype=BF16), torch.zeros((1, 8, 3), dtype=BF16),
+                                               torch.zeros((8, 1, 4), dtype=BF16)),
+    ],
+)
+def test_bad_shapes_raise_value_error_before_the_device_check(call):
+    with pytest.raises(ValueError):
+        call()
+
+
+def test_delta_and_attention_ops_validate_before_device():
+    c = mid_config(num_layers=4)
+    hv, hk, dk = c.linear_num_value_heads, c.linear_num_key_heads, 128
+    ch = 2 * hk * dk + hv * dk
+    state = torch.zeros((1, hv, dk, dk), dtype=torch.float32)
+    args = dict(mixed_qkv=torch.zeros((1, ch), dtype=BF16), a=torch.zeros((1, hv), dtype=BF16),
+                b=torch.zeros((1, hv), dtype=BF16), A_log=torch.zeros(hv, dtype=BF16), dt_bias=torch.zeros(hv, dtype=BF16),
+                conv_weight=torch.zeros((ch, 1, 4), dtype=BF16), conv_cache=torch.zeros((1, ch, 3), dtype=BF16),
+                state=state, num_k_heads=hk)
+    with pytest.raises(RuntimeError, match="no PyTorch fallback"):
+        hip_ops.gated_delta_decode(**args)
+    with pytest.raises(ValueError):
+        hip_ops.gated_delta_decode(**{**args, "state": state.to(BF16)})
+    hq, hkv, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
+    att = dict(q_gate=torch.zeros((1, hq * 2 * d), dtype=BF16), k=torch.zeros((1, hkv * d), dtype=BF16),
+               v=torch.zeros((1, hkv * d), dtype=BF16), q_norm_w=torch.zeros(d, dtype=BF16),
+               k_norm_w=torch.zeros(d, dtype=BF16), inv_freq=torch.zeros(32, dtype=torch.float32),
+               k_cache=torch.zeros((1, hkv, 16, d), dtype=BF16), v_cache=torch.zeros((1, hkv, 16, d), dtype=BF16),
+               position=torch.zeros(1, dtype=torch.int32), num_q_heads=hq, sigmoid_gate=True, eps=1e-6)
+    with pytest.raises(RuntimeError, match="no PyTorch fallback"):
+        hip_ops.gated_attention_decode(**att)
+    with pytest.raises(ValueError):
+        hip_ops.gated_attention_decode(**{**att, "num_q_heads": hq + 1})
+
+
+def test_fake_kernels_give_the_output_shapes():
+    m = "meta"
+    packed, scale = _int4(512, 128, m)
+    assert hip_ops.tiled_gemv_int4(torch.empty((3, 5, 512), dtype=BF16, device=m), packed, scale, 128).shape == (3, 5, 128)
+    assert hip_ops.silu_mul(torch.empty(8, dtype=BF16, device=m), torch.empty(8, dtype=BF16, device=m)).shape == (8,)
+    r, y = hip_ops.add_rms_norm(*(torch.empty((2, 8), dtype=BF16, device=m) for _ in range(2)),
+                                torch.empty(8, dtype=BF16, device=m), 1e-6)
+    assert r.shape == y.shape == (2, 8)
+    st = torch.empty((2, 4, 128, 128), dtype=torch.float32, device=m)
+    out = hip_ops.gated_delta_decode(torch.empty((2, 2048), dtype=BF16, device=m), torch.empty((2, 4), dtype=BF16, device=m),
+                                     torch.empty((2, 4), dtype=BF16, device=m), torch.empty(4, dtype=BF16, device=m),
+                                     torch.empty(4, dtype=BF16, device=m), torch.empty((2048, 1, 4), dtype=BF16, device=m),
+                                     torch.empty((2, 2048, 3), dtype=BF16, device=m), st, 4)
+    assert out.shape == (2, 4, 128)
