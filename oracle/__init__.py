@@ -12,11 +12,17 @@ import it, and only as the *checker* (or as the timed CPU baseline). The product
 
 How each part is pinned (a function with no independent pin would say "parity unpinned"):
 
-* ``int4``: numpy bit-level restatement vs the torch expression, brute force over all 256
-  byte values x scales; the reference tests' own invariants (K-major pairing, round trip).
-* ``model``: golden vectors written by ``tests/golden/make_golden.py`` from the reference
-  itself (tiny and mid configs, prefill + decode logits and cache state, one GatedDeltaNet
-  step, one GatedAttention step, int4 dequant-GEMV), plus the reference tests' known
-  answers and invariants (RMSNorm known answer, rotate_half, RoPE identity at position 0,
-  delta-rule step == whole == chunked, beta = 0, conv history shift).
+* ``int4``: the reference's own quantiser bytes, dequant and dequant-GEMV output
+  (``tests/golden/int4_gemv.safetensors``, written by the reference), a brute force over all
+  256 byte values x scales in integer/float64 arithmetic, the K-major pairing, and the
+  quantiser's range and round trip (``tests/test_oracle_invariants.py``).
+* ``model``: bit-identical (rtol = atol = 0) to vectors the reference itself wrote with
+  ``tests/golden/make_golden.py`` -- tiny and mid configs, dense and int4, prefill logits
+  at every position, each greedy step's logits and token, conv history, fp32 recurrent
+  state and KV cache (``tests/test_oracle_golden.py``) -- plus the reference tests' known
+  answers and invariants: RMSNorm (1 + w), gated RMSNorm closed form, rotate_half, RoPE
+  identity at position 0 and the untouched tail, conv history shift, delta rule against a
+  float64 closed form, step == whole == chunks, beta = 0, causality.
+* ``ops`` (per-config slices used as GPU checkers): each equals, bit for bit, the
+  golden-pinned ``OracleModel`` layer it is cut from (``tests/test_oracle_invariants.py``).
 """
