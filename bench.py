@@ -135,9 +135,16 @@ def cpu_baseline(model, position: int) -> dict:
             times.append(time.perf_counter() - t0)
             cache.seq_len = position
     best = min(times)
+    cpu = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), cpu)
+    except OSError:
+        pass
     return {"value": 1.0 / best, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"1 decode step (best of 2) of the same 32-layer int4 model at context {position}, "
-                      f"CPU oracle (plain PyTorch, fp32 dequant per linear), {threads} threads",
+                      f"CPU oracle (plain PyTorch, fp32 dequant per linear), {threads} threads "
+                      f"(os.cpu_count() = {os.cpu_count()}) on {cpu}",
             "seconds_per_token": best}
 
 
