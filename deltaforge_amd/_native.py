@@ -53,6 +53,29 @@ class AttnDecodeArgs(C.Structure):
     ]
 
 
+class PersistLayer(C.Structure):
+    _fields_ = [
+        ("kind", _i),
+        ("in_norm", _vp), ("post_norm", _vp),
+        ("proj_w", _vp), ("proj_s", _vp), ("out_w", _vp), ("out_s", _vp),
+        ("gu_w", _vp), ("gu_s", _vp), ("down_w", _vp), ("down_s", _vp),
+        ("conv_w", _vp), ("A_log", _vp), ("dt_bias", _vp), ("gnorm_w", _vp),
+        ("conv_ring", _vp), ("state", _vp),
+        ("q_norm", _vp), ("k_norm", _vp), ("k_cache", _vp), ("v_cache", _vp),
+    ]
+
+
+class PersistModel(C.Structure):
+    _fields_ = [
+        ("hidden", _i), ("inter", _i), ("vocab", _i), ("num_layers", _i), ("max_len", _i), ("gate_kind", _i),
+        ("eps", _f),
+        ("layers", _vp), ("head_w", _vp), ("head_s", _vp), ("final_norm", _vp), ("inv_freq", _vp),
+        ("position", _vp), ("tokens", _vp), ("prompt", _vp), ("prompt_len", _i),
+        ("token_log", _vp), ("log_capacity", _i), ("step", _vp), ("logits", _vp),
+        ("trace", _vp), ("trace_step", _i), ("trace_capacity", _i),
+    ]
+
+
 # name -> (restype, argtypes); the exported surface of include/deltaforge_hip.h
 SIGNATURES = {
     "df_int4_gemv_plan": (_i, [_i, _i, _i, _i, _i, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i), C.POINTER(_sz)]),
@@ -72,6 +95,8 @@ SIGNATURES = {
     "df_embed_int4": (_i, [_vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i, _vp, _vp]),
     "df_argmax_workspace_bytes": (_sz, [_i, _i]),
     "df_argmax": (_i, [_vp, _i, _i, _vp, _vp, _i, _vp, _i, _vp, _vp, _sz, _vp]),
+    "df_decode_persistent_workspace_bytes": (_sz, [_i]),
+    "df_decode_persistent": (_i, [C.POINTER(PersistModel), _i, _i, _vp, _sz, _vp]),
 }
 
 _LIB: C.CDLL | None = None

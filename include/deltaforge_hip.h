@@ -184,6 +184,86 @@ int df_argmax(const uint16_t* logits, int rows, int n, int64_t* tokens, int64_t*
               int log_stride, int* position, int advance, int* step, void* workspace,
               size_t workspace_bytes, hipStream_t stream);
 
+/* ---- persistent decode: many bs=1 tokens in one cooperative launch ------------------
+ *
+ * The whole decode step of greedy_decode (model.py:108-148 driving ReferenceModel.forward,
+ * reference.py:779-817) for one sequence, run as 8-way tensor parallelism over the 8 XCDs
+ * of one MI355X: 256 workgroups, 32 per XCD. Per layer, XCD x owns value heads 4x..4x+3
+ * (key heads 2x, 2x+1) of Gated DeltaNet, query heads 2x, 2x+1 (KV head x/2) of gated
+ * attention, 1/8 of the gate/up columns and the matching K slices of out_proj / o_proj /
+ * down; only those row-parallel outputs and the argmax cross XCDs. Head geometry is
+ * Qwen3.5-4B's (16/32 heads of 128 for DeltaNet, 16/4 heads of 256 for attention,
+ * rotary 64, 4-tap conv); hidden % 512 == 0, inter % 1024 == 0, vocab % 128 == 0,
+ * hidden <= 4096.
+ *
+ * Weights are the tiled layout of df_int4_repack. The input projections' columns are in
+ * XCD-major order:
+ *   DeltaNet in_proj, 1552 columns per XCD x: q[2x], q[2x+1], k[2x], k[2x+1] (128 each),
+ *     v[4x..4x+3], z[4x..4x+3] (128 each), a[4x..4x+3], b[4x..4x+3], 8 zero columns.
+ *   attention q|k|v proj, 1536 columns per XCD x: for h in 2x, 2x+1 the 512 q_proj
+ *     columns of head h (query 256 | gate 256), then k_proj and v_proj of KV head x/2.
+ * gate/up is interleaved by 16-column tile (gate, up, gate, up ...); the others are in
+ * natural order. */
+typedef struct DfPersistLayer {
+  int kind;                        /* 0 = Gated DeltaNet, 1 = gated attention             */
+  const uint16_t* in_norm;         /* [hidden] input_layernorm (1 + w)                   */
+  const uint16_t* post_norm;       /* [hidden] post_attention_layernorm (1 + w)          */
+  const uint8_t* proj_w;           /* input projection, XCD-major columns (see above)    */
+  const uint16_t* proj_s;
+  const uint8_t* out_w;            /* out_proj / o_proj: K = 4096, N = hidden            */
+  const uint16_t* out_s;
+  const uint8_t* gu_w;             /* gate|up interleaved: K = hidden, N = 2 * inter     */
+  const uint16_t* gu_s;
+  const uint8_t* down_w;           /* K = inter, N = hidden                              */
+  const uint16_t* down_s;
+  const uint16_t* conv_w;          /* DeltaNet: [8192][4] conv taps                      */
+  const uint16_t* A_log;           /* [32]                                               */
+  const uint16_t* dt_bias;         /* [32]                                               */
+  const uint16_t* gnorm_w;         /* [128] GatedRMSNorm weight                          */
+  uint16_t* conv_ring;             /* [8192][4] history ring, slot position % 4          */
+  float* state;                    /* [32][128][128] fp32 recurrent state                */
+  const uint16_t* q_norm;          /* attention: [256] (1 + w)                           */
+  const uint16_t* k_norm;          /* [256]                                              */
+  uint16_t* k_cache;               /* [4][max_len][256]                                  */
+  uint16_t* v_cache;
+} DfPersistLayer;
+
+typedef struct DfPersistModel {
+  int hidden, inter, vocab, num_layers, max_len;
+  int gate_kind;                   /* output gate: 0 sigmoid, 1 silu                     */
+  float eps;
+  const DfPersistLayer* layers;    /* DEVICE array [num_layers]                          */
+  const uint8_t* head_w;           /* tied head, natural columns: K = hidden, N = vocab  */
+  const uint16_t* head_s;
+  const uint16_t* final_norm;      /* [hidden]                                           */
+  const float* inv_freq;           /* [32] bf16-rounded inverse frequencies, as fp32     */
+  int* position;                   /* tokens already cached (read at launch, advanced)   */
+  int64_t* tokens;                 /* [1] token the next step embeds (argmax written back) */
+  const int64_t* prompt;           /* [prompt_len], teacher-forced steps read prompt[pos] */
+  int prompt_len;
+  int64_t* token_log;              /* generated tokens, token_log[*step] per greedy step */
+  int log_capacity;
+  int* step;                       /* next token_log index                               */
+  uint16_t* logits;                /* [vocab] bf16 logits of the last step (or NULL)     */
+  uint64_t* trace;                 /* optional: s_memrealtime (100 MHz) stamps of one    */
+  int trace_step;                  /* step's phases (start, staged, end), as seen by     */
+  int trace_capacity;              /* workgroup (XCD 0, rank 0); NULL disables           */
+} DfPersistModel;
+
+/* Workspace for df_decode_persistent, zero-filled once before first use and kept (it
+ * carries the launch-to-launch epoch). Its first four int32 are {epoch, abort, error,
+ * reserved}: after a launch, a nonzero `abort` means a wait timed out (`error` says
+ * which) and the outputs are invalid. */
+size_t df_decode_persistent_workspace_bytes(int hidden);
+
+/* Run `steps` decode steps from *position. teacher_forced: the token of each step is
+ * prompt[position] (prefill; token_log untouched); else the previous step's argmax
+ * (greedy; appended to token_log). Either way the last argmax is left in tokens[0] and
+ * position advances by `steps`. Needs all 256 workgroups co-resident (cooperative
+ * launch); returns DF_LAUNCH_FAILED if the device cannot host them. */
+int df_decode_persistent(const DfPersistModel* model, int steps, int teacher_forced, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
