@@ -44,6 +44,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--roofline-reps", type=int, default=10)
     ap.add_argument("--roofline-only", action="store_true")
+    ap.add_argument("--engine", choices=("persistent", "graph"), default="persistent",
+                    help="persistent: one cooperative launch per decode run (df_decode_persistent); "
+                         "graph: the per-op kernels replayed as one HIP graph per step")
     return ap.parse_args()
 
 
@@ -57,6 +60,9 @@ GATE_UP_KERNEL = "w4_gemv_kernel<RMSNORM, SWIGLU> (post-attention norm + gate/up
 # the counter reads for a plain 256 MiB device copy (x 2.000 for FETCH_SIZE, x 1.000 for
 # WRITE_SIZE). Re-measure when the kernel changes.
 GATE_UP_TRAFFIC_BYTES = 12049 * 1024 * 2 + 18 * 1024
+# HBM bytes per decode token of the persistent kernel from the same calibrated PMC passes
+# (None until measured).
+PERSISTENT_TRAFFIC_BYTES_PER_TOKEN = None
 
 
 def gate_up_bytes(cfg) -> int:
@@ -148,6 +154,45 @@ def cpu_baseline(model, position: int) -> dict:
             "seconds_per_token": best}
 
 
+def run_decode(engine, args, persistent: bool) -> tuple[float, list[int]]:
+    """Prefill (untimed), warm up on a snapshot, restore, then time exactly ``args.steps``
+    greedy tokens with HIP events on the stream the decode runs on. Returns (seconds, first tokens)."""
+    prompt = synth_prompt(engine.config, args.prompt_len)
+    t0 = time.perf_counter()
+    engine.prefill(prompt.cuda())
+    if persistent:
+        engine.check()
+    torch.cuda.synchronize()
+    log(f"prefill of {args.prompt_len} tokens (teacher-forced decode steps) in {time.perf_counter() - t0:.1f}s")
+    snap = engine.snapshot()
+    engine.decode(args.warmup)
+    if persistent:
+        engine.check()
+    torch.cuda.synchronize()
+    engine.restore(snap)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    engine.decode(args.steps)
+    end.record(stream)
+    torch.cuda.synchronize()
+    if persistent:
+        engine.check()
+    return start.elapsed_time(end) / 1e3, engine.token_log[0, :8].tolist()
+
+
+def synth_prompt(cfg, n: int) -> torch.Tensor:
+    from deltaforge_amd import synth
+
+    return synth.prompt_ids(cfg.vocab_size, n, seed=1)
+
+
+PERSISTENT_KERNEL = "df::pd::decode_kernel (every layer of every decode step in one cooperative launch)"
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -161,49 +206,63 @@ def main() -> int:
     from deltaforge_amd.config import qwen3_5_4b_config
     from deltaforge_amd.engine import DecodeEngine
     from deltaforge_amd.harness.bytes_model import HBM_PEAK_BYTES_PER_S, mean_decode_bytes
+    from deltaforge_amd.persistent import PersistentDecoder
 
     cfg = qwen3_5_4b_config()
     t0 = time.perf_counter()
     model = synth.synth_model(cfg, seed=args.seed)
     log(f"synthetic model drawn in {time.perf_counter() - t0:.1f}s ({model.nbytes() / 1e9:.2f} GB)")
-    engine = DecodeEngine(model, max_seq_len=args.prompt_len + args.steps + args.warmup + 64,
-                          max_new_tokens=args.steps + args.warmup)
+    persistent = args.engine == "persistent" and not args.roofline_only
+    max_len = args.prompt_len + args.steps + args.warmup + 64
+    if persistent:
+        engine = PersistentDecoder(model, max_seq_len=max_len, max_new_tokens=args.steps + args.warmup)
+    else:
+        engine = DecodeEngine(model, max_seq_len=max_len, max_new_tokens=args.steps + args.warmup)
     torch.cuda.synchronize()
-    log(f"engine ready: {engine.weight_bytes() / 1e9:.3f} GB of int4 weights in HBM")
+    log(f"{args.engine} engine ready: {engine.weight_bytes() / 1e9:.3f} GB of int4 weights in HBM")
     if args.roofline_only:
         gu_s = time_gate_up(engine, args.roofline_reps)
         log(f"gate/up GEMV: {gu_s * 1e6:.2f} us/launch, {gate_up_bytes(cfg) / gu_s / 1e9:.1f} GB/s")
         copy_calibration()
         return 0
-    prompt = synth.prompt_ids(cfg.vocab_size, args.prompt_len, seed=1)
-    t0 = time.perf_counter()
-    engine.prefill(prompt.cuda())
-    torch.cuda.synchronize()
-    log(f"prefill of {args.prompt_len} tokens (teacher-forced decode steps) in {time.perf_counter() - t0:.1f}s")
-    snap = engine.snapshot()
-    engine.decode(args.warmup)
-    torch.cuda.synchronize()
-    engine.restore(snap)
-    torch.cuda.synchronize()
 
-    stream = torch.cuda.current_stream()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(stream)
-    engine.decode(args.steps)
-    end.record(stream)
-    torch.cuda.synchronize()
-    seconds = start.elapsed_time(end) / 1e3
+    seconds, tokens = run_decode(engine, args, persistent)
     tok_s = args.steps / seconds
     bytes_per_token = mean_decode_bytes(cfg, args.prompt_len, args.steps)
     achieved = bytes_per_token * tok_s
     log(f"decode: {args.steps} tokens in {seconds * 1e3:.1f} ms -> {tok_s:.1f} tok/s, "
         f"{achieved / 1e9:.1f} GB/s ({100 * achieved / HBM_PEAK_BYTES_PER_S:.1f}% of 8 TB/s)")
-    tokens = engine.token_log[0, :8].tolist()
 
-    gu_s = time_gate_up(engine, args.roofline_reps)
-    gu_gbps = gate_up_bytes(cfg) / gu_s / 1e9
-    log(f"gate/up GEMV: {gu_s * 1e6:.2f} us/launch, {gu_gbps:.1f} GB/s")
+    if persistent:
+        # the dominant (only) kernel is the persistent decode launch; one launch = `steps` tokens
+        launch_bytes = int(bytes_per_token * args.steps)
+        roofline = {
+            "kernel": PERSISTENT_KERNEL,
+            "bound": "hbm",
+            "achieved": round(launch_bytes / seconds / 1e9, 1),
+            "peak": 8000.0,
+            "unit": "GB/s",
+            "frac": round(launch_bytes / seconds / 8e12, 4),
+            "traffic": PERSISTENT_TRAFFIC_BYTES_PER_TOKEN * args.steps if PERSISTENT_TRAFFIC_BYTES_PER_TOKEN else None,
+            "us_per_launch": round(seconds * 1e6, 1),
+            "bytes_per_launch": launch_bytes,
+            "tokens_per_launch": args.steps,
+        }
+    else:
+        gu_s = time_gate_up(engine, args.roofline_reps)
+        gu_gbps = gate_up_bytes(cfg) / gu_s / 1e9
+        log(f"gate/up GEMV: {gu_s * 1e6:.2f} us/launch, {gu_gbps:.1f} GB/s")
+        roofline = {
+            "kernel": GATE_UP_KERNEL,
+            "bound": "hbm",
+            "achieved": round(gu_gbps, 1),
+            "peak": 8000.0,
+            "unit": "GB/s",
+            "frac": round(gu_gbps / 8000.0, 4),
+            "traffic": GATE_UP_TRAFFIC_BYTES,
+            "us_per_launch": round(gu_s * 1e6, 3),
+            "bytes_per_launch": gate_up_bytes(cfg),
+        }
 
     baseline = None
     if not args.no_cpu_baseline:
@@ -230,6 +289,7 @@ def main() -> int:
             "workload": "config 5: bs=1 greedy decode of a random-init 32-layer Qwen3.5-4B-shaped hybrid "
                         "(24 Gated DeltaNet + 8 gated GQA layers), int4 group-128 weights, tied int4 head, "
                         f"prompt {args.prompt_len} ids (seed 1), {args.steps} timed greedy steps",
+            "engine": args.engine,
             "batch": 1,
             "context": args.prompt_len,
             "weights": "int4 g128 nibbles + bf16 scales; bf16 activations; fp32 accumulation and state",
@@ -238,17 +298,7 @@ def main() -> int:
             "hbm_fraction": round(achieved / HBM_PEAK_BYTES_PER_S, 4),
             "first_tokens": tokens,
         },
-        "roofline": {
-            "kernel": GATE_UP_KERNEL,
-            "bound": "hbm",
-            "achieved": round(gu_gbps, 1),
-            "peak": 8000.0,
-            "unit": "GB/s",
-            "frac": round(gu_gbps / 8000.0, 4),
-            "traffic": GATE_UP_TRAFFIC_BYTES,
-            "us_per_launch": round(gu_s * 1e6, 3),
-            "bytes_per_launch": gate_up_bytes(cfg),
-        },
+        "roofline": roofline,
         "cpu_baseline": baseline,
     }
     print(json.dumps(out), flush=True)

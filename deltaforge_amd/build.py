@@ -30,6 +30,7 @@ HIPCC_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-function",
+    "-Wno-inline-asm",  # m0 is clobbered by the persistent kernel's LDS-DMA asm (nothing else uses it)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",

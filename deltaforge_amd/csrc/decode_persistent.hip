@@ -16,17 +16,30 @@
 // of the hidden vector with write-through stores, each workgroup sums one 1/32 slice of
 // the 8 partials in XCD order, adds the residual and publishes the new hidden vector to
 // its XCD. Every other hand-off stays inside one XCD's L2 (plain stores, agent-scope
-// loads, a per-workgroup epoch flag), which costs ~0.4 us instead of ~3 us across XCDs.
+// loads, a per-workgroup epoch flag).
 //
-// Workgroup = 8 compute waves + 1 control wave. On gfx9 vector loads retire in order, so a
-// wave that has weight loads in flight cannot see a flag or an activation before those
-// weights land. The compute waves therefore only issue weight / state / KV prefetches
-// and then work out of LDS and registers; the control wave polls the hand-offs, stages
-// activations and norm weights into LDS, and does the output stores and the signalling.
-// Each phase's weights are requested before its input hand-off is awaited.
+// Weight stream. Workgroup = 8 compute waves + 1 control wave. Each compute wave owns a
+// fixed sequence of 1 KB weight blocks per token (its share of every GEMV phase of every
+// layer, then of the head) and keeps the next kRing of them in flight or landed in its
+// own LDS ring (LDS DMA), refilling a slot as soon as it has consumed it. The stream runs
+// across phase and layer boundaries, so HBM keeps streaming while workgroups wait on
+// hand-offs; it pauses only before each attention layer's output projection, until that
+// layer's KV-cache loads are consumed. On gfx9 vector memory operations of a wave retire
+// in order (one vmcnt counter), so a compute wave never waits for anything behind its
+// ring: hand-off polls, activation staging, the recurrent state and every hand-off store
+// belong to the control wave, which also signals. Ring slots are read with inline-asm
+// ds_read so the compiler does not insert a vmcnt(0) before them (it cannot tell which
+// slot a DMA targets); the kernel waits explicitly for exactly the block it consumes.
 //
-// Arithmetic is the per-op kernels' (int4_gemv.hip, gated_delta.hip, attention.hip,
-// small_ops.hip), with the reference's rounding points; only fp32 summation orders differ.
+// GEMV arithmetic. A block's B operand is bf16(128 + nibble) (exact, the nibble in the low
+// mantissa bits), built in 7 VALU ops per 8 weights; per 128-group the MFMA gives
+// D = sum x_k (128 + n_k), and y += s * (D - 136 * sum x_k) = s * sum x_k (n_k - 8). This is
+// the reference's sum x_k * ((n_k - 8) * s) with the scale applied once per group instead of
+// rounding each weight to bf16 first: the per-weight bf16 rounding the reference does
+// (relative 2^-9) is not reproduced, which moves outputs by well under the bf16 tolerance.
+//
+// Other arithmetic is the per-op kernels' (gated_delta.hip, attention.hip, small_ops.hip),
+// with the reference's rounding points; only fp32 summation orders differ.
 #include "common.h"
 #include "deltaforge_hip.h"
 #include "int4_block.h"
@@ -40,29 +53,32 @@ constexpr int kNwg = kXcd * kPerXcd;
 constexpr int kCompute = 8;
 constexpr int kCtl = kCompute;                      // wave index of the control wave
 constexpr int kThreads = (kCompute + 1) * 64;       // 576
-constexpr int kCThreads = kCompute * 64;            // 512 compute threads
 constexpr int kMaxHidden = 2560;
-constexpr int kMaxNb = 12;                          // weight blocks per compute wave per phase
-constexpr int kMaxWgTiles = 8;
-constexpr int kDepthH = 8;                          // head pipeline depth (blocks per wave)
+constexpr int kRing = 11;                           // weight blocks in flight per compute wave
+constexpr int kMaxWgTiles = 8;                      // output tiles of a workgroup's GEMV range
+constexpr int kMaxGroups = 24;                      // 128-groups of a GEMV phase's input row
+constexpr int kMaxHeadTiles = 64;                   // head tiles per workgroup
 constexpr int kColparMax = 2304;
 // Gated DeltaNet geometry
 constexpr int kKH = 16, kVH = 32, kDk = 128;
 constexpr int kKeyDim = kKH * kDk;                  // 2048
-constexpr int kConvCh = 2 * kKeyDim + kVH * kDk;    // 8192
 constexpr int kLinCols = 1552;
-constexpr int kLinQ = 0, kLinK = 256, kLinV = 512, kLinZ = 1024, kLinA = 1536, kLinB = 1540;
+constexpr int kLinQ = 0, kLinK = 256, kLinV = 512, kLinZ = 1024, kLinA = 1536;
+constexpr int kDnCh = 2 * kDk + 16;                 // conv channels of one delta unit: q, k, v slice
 // attention geometry
-constexpr int kQH = 16, kKVH = 4, kHd = 256, kRot = 64;
+constexpr int kHd = 256, kRot = 64;
 constexpr int kAttnCols = 1536;
-constexpr int kAttnK = 1024, kAttnV = 1280;
+constexpr int kAttnK = 1024;
 constexpr int kApHead = kHd + 2;                    // acc[256], m, l
 constexpr int kTileKeys = kCompute * 16;            // 128 keys per attention tile
+// factored int4 dot product: B = bf16(128 + n), n - 8 = B - 136
+constexpr uint32_t kBiasPair = 0x43004300u;         // bf16 128.0 in both halves
+constexpr float kBias = 136.0f;
 
 constexpr uint64_t kTimeout = 50000000ull;          // 0.5 s of s_memrealtime (100 MHz)
 constexpr int kRegBase = 4;                         // ctl[4..11]: per-XCD registration tickets
 
-enum Err : int { kErrNone = 0, kErrTimeout = 1, kErrXcd = 2, kErrPosition = 3, kErrToken = 4 };
+enum Err : int { kErrNone = 0, kErrTimeout = 1, kErrXcd = 2, kErrPosition = 3, kErrToken = 4, kErrSchedule = 5 };
 
 struct Ws {
   int* ctl;          // [16]: epoch, abort, error, -, 8 registration tickets, -
@@ -118,12 +134,12 @@ template <class T>
 DF_DEVICE T ld_sys(const T* p) {
   return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
+// Write-through store. The pointer is cast to the global address space: a flat store could
+// target LDS, and the compiler would then make every later LDS access wait for it (vmcnt).
 template <class T>
 DF_DEVICE void st_sys(T* p, T v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __hip_atomic_store((__attribute__((address_space(1))) T*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
-// bf16 pair loads of XCD-local data (bypassing the CU's L1)
-DF_DEVICE uint32_t ld_agent_u32(const uint16_t* p) { return ld_agent(reinterpret_cast<const uint32_t*>(p)); }
 
 DF_DEVICE uint64_t pack_epoch(float v, uint32_t epoch) {
   return (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(v);
@@ -132,64 +148,55 @@ DF_DEVICE uint64_t pack_cand(float v, int index, uint32_t epoch) {
   return (static_cast<uint64_t>(__float_as_uint(v)) << 32) | (static_cast<uint32_t>(index) << 14) | (epoch & 0x3FFFu);
 }
 
-// ---------------------------------------------------------------------------------------
-// per-workgroup context and LDS
-// ---------------------------------------------------------------------------------------
-
-struct Ctx {
-  DfPersistModel M;
-  Ws w;
-  int xcd, r, tid, wave, lane;
-  bool control;
-  uint32_t epoch;   // last epoch this workgroup reached (all workgroups agree on the sequence)
-  int ar;           // row-parallel all-reduce counter (selects the rowpar buffer)
-  int pos;          // position of the token being decoded
-  uint64_t* tr;     // phase trace of the traced step (workgroup (0, 0), control wave), or null
-  int tn;
-};
-
-// Phase trace of the traced step: s_memrealtime << 8 | tag (tags: 1-15 phase starts, 20
-// staged after the hand-off, 30 signalled).
-enum Tag : int { kTProj = 1, kTDelta, kTOut, kTAttn, kTMerge, kTOProj, kTGateUp, kTDown, kTHead, kTEmbed,
-                 kTReduce, kTStaged = 20, kTSignal = 30 };
-DF_DEVICE void stamp(Ctx& c, int tag) {
-  if (c.tr) {
-    if (c.control && c.lane == 0 && c.xcd == 0 && c.r == 0 && c.tn < c.M.trace_capacity)
-      c.tr[c.tn] = (now() << 8) | static_cast<uint64_t>(tag);
-    c.tn += 1;
-  }
-}
-
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) const void gbl_void;
 
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
+// lgkmcnt[11:8] | vmcnt[5:4] at [15:14]).
+template <int N>
+DF_DEVICE void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// ---------------------------------------------------------------------------------------
+// LDS. The weight ring and the GEMV input row are objects of their own: the compiler then
+// knows that reads of the input row and of the workgroup struct cannot alias a ring DMA.
+// ---------------------------------------------------------------------------------------
+
+__shared__ __align__(16) uint4 g_ring_w[kCompute][kRing][64];     // 1 KB blocks
+__shared__ __align__(16) uint32_t g_ring_s[kCompute][kRing][64];  // scale dword of lane i: columns (i & 14), +1
+__shared__ __align__(16) uint16_t g_x[kMaxHidden + 8];            // GEMV input row (bf16)
+
 struct Lds {
-  uint16_t h[kMaxHidden];                        // the hidden vector (bf16)
-  __align__(16) uint16_t x[2][kMaxHidden + 8];   // GEMV activation row; row 1 stays zero
+  __align__(16) uint16_t h[kMaxHidden];          // the hidden vector (bf16)
   __align__(16) uint16_t nw[kMaxHidden];         // staged norm weight
+  float xs[kMaxGroups];                          // 136 * sum of each 128-group of g_x
   float part[kMaxWgTiles][kCompute][16];         // per-wave tile partials
-  float gated_z[512];                            // SiLU inputs of the GatedRMSNorm
   float red[64];
   int ok;
   int token;
+  int nbw;                                       // compute waves' barrier count at the head's last barrier
   struct {                                       // head
-    __align__(16) uint16_t logit[kMaxWgTiles * 8 * 16];  // up to 64 tiles
+    __align__(16) uint16_t logit[kMaxHeadTiles * 16];
     float bv[kCompute];
     int bi[kCompute];
   } hd;
   union {
-    // weight blocks of the current GEMV phase (or the head's ring), written by LDS DMA;
-    // wave w owns wblk[w]
-    struct {
-      __align__(16) uint4 wblk[kCompute][kMaxNb][64];
-      uint32_t sblk[kCompute][kMaxNb][64];       // scale dwords: lane i holds columns 2(i/2 % 8) +0/+1
-    } wq;
+    struct {                                     // out_proj: SiLU inputs of the GatedRMSNorm
+      float z[512];
+    } on;
     struct {                                     // Gated DeltaNet step
-      float qkv_in[272];                         // pre-conv inputs: q 128, k 128, v 16
+      float4 S[kCompute * 64];                   // state slice: row tid/4, columns 4(tid%4)..+3
+      uint2 taps[kDnCh];                         // conv taps (bf16 x4)
+      uint2 hist[kDnCh];                         // conv history ring (bf16 x4, slot position % 4)
+      float qkv_in[kDnCh];                       // pre-conv inputs: q 128, k 128, v 16
       float q[kDk], k[kDk], v[16];
       float sred[kCompute][16];
       float ab8[8];                              // a of the XCD's 4 value heads, then b
+      float gpar[2];                             // A_log, dt_bias of the unit's value head
       float scal[4];
+      uint16_t core[16];
     } dn;
     struct {                                     // attention split
       __align__(16) uint16_t q[2][kHd];
@@ -206,11 +213,10 @@ struct Lds {
       float ml[2][2];
       float red[kCompute][2][kHd];               // 16 KB
     } at;
-    struct {                                     // split merge
+    struct {                                     // split merge (control wave)
       float m[kPerXcd], l[kPerXcd], wgt[kPerXcd];
       float acc[kPerXcd][16];
       float gate[16];
-      float den;
     } mg;
     struct {                                     // all-reduce slice
       float y[kXcd][128];
@@ -218,12 +224,58 @@ struct Lds {
   } u;
 };
 
-// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
-// lgkmcnt[11:8] | vmcnt[5:4] at [15:14]).
-template <int N>
-DF_DEVICE void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+constexpr size_t kLdsBytes = sizeof(Lds) + sizeof(g_ring_w) + sizeof(g_ring_s) + sizeof(g_x);
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
+
+// The layer table is never written during a launch: reading it through the constant
+// address space lets the compiler use scalar loads (a vector load would sit behind the
+// compute wave's weight ring in the in-order vmcnt queue).
+typedef const __attribute__((address_space(4))) DfPersistLayer* LayerPtr;
+DF_DEVICE LayerPtr layer_at(const DfPersistModel& M, int li) { return (LayerPtr)M.layers + li; }
+
+DF_DEVICE uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
+
+// Workgroup barrier that orders LDS only. __syncthreads() is a workgroup-scope release
+// fence, which on gfx950 waits for every outstanding vector memory operation of the wave
+// (vmcnt(0)) and so would drain the compute waves' weight rings at every barrier. Nothing
+// in this kernel passes data between the waves of a workgroup through global memory.
+DF_DEVICE void bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// ---------------------------------------------------------------------------------------
+// per-workgroup context
+// ---------------------------------------------------------------------------------------
+
+struct Ctx {
+  Ws w;
+  int tcap;         // trace capacity
+  int max_len;      // KV-cache rows per head
+  int nb;           // barriers this wave has passed in the current token
+  int xcd, r, tid, wave, lane;
+  bool control;
+  uint32_t epoch;   // last epoch this workgroup reached (all workgroups agree on the sequence)
+  int ar;           // row-parallel all-reduce counter (selects the rowpar buffer)
+  int pos;          // position of the token being decoded
+  uint64_t* tr;     // phase trace of the traced step (workgroup (0, 0), control wave), or null
+  int tn;
+};
+
+// Per-workgroup geometry of the phases.
+struct Geo {
+  int hidden, Gh, inter, inter_x, gu_tiles, rp_lo, rp_hi, ngx, t_lo, t_hi;
+};
+
+// Phase trace of the traced step: s_memrealtime << 8 | tag (tags: 1-15 phase starts, 20
+// staged after the hand-off, 30 signalled).
+enum Tag : int { kTProj = 1, kTDelta, kTOut, kTAttn, kTMerge, kTOProj, kTGateUp, kTDown, kTHead, kTEmbed,
+                 kTReduce, kTStaged = 20, kTSignal = 30 };
+DF_DEVICE void stamp(Ctx& c, int tag) {
+  if (c.tr) {
+    if (c.control && c.lane == 0 && c.xcd == 0 && c.r == 0 && c.tn < c.tcap)
+      c.tr[c.tn] = (now() << 8) | static_cast<uint64_t>(tag);
+    c.tn += 1;
+  }
 }
 
 // Re-derive the thread's coordinates at the start of a phase behind an opaque asm, so the
@@ -240,6 +292,14 @@ DF_DEVICE void fence(Ctx& c, int tag = 0) {
   c.xcd = __builtin_amdgcn_readfirstlane(xcd);
   c.r = __builtin_amdgcn_readfirstlane(r);
   if (tag) stamp(c, tag);
+}
+
+// The control wave and the compute waves run separate code (so neither role's registers or
+// pending loads burden the other) and meet only at these barriers, in the same order; each
+// counts them and the counts are compared once per token.
+DF_DEVICE void sync(Ctx& c) {
+  bar();
+  c.nb += 1;
 }
 
 DF_DEVICE void raise_abort(const Ctx& c, int err) {
@@ -263,77 +323,95 @@ DF_DEVICE bool wait_local(const Ctx& c, uint32_t epoch) {
   }
 }
 
-// All threads: make this workgroup's stores visible, then the control wave publishes `epoch`.
+// Control wave: make its stores complete, then publish `epoch` for this workgroup. Every
+// store another workgroup reads is made by the control wave, so only it waits.
 DF_DEVICE void signal_local(Ctx& c, uint32_t epoch) {
   __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
   stamp(c, kTSignal);
-  if (c.control && c.lane == 0) {
+  if (c.lane == 0) {
     // a plain store lands in this XCD's L2, where the agent-scope polls of the other
     // workgroups of the XCD read it
-    *reinterpret_cast<volatile int*>(c.w.flags + c.xcd * kPerXcd + c.r) = static_cast<int>(epoch);
+    *(volatile __attribute__((address_space(1))) int*)(c.w.flags + c.xcd * kPerXcd + c.r) = static_cast<int>(epoch);
   }
 }
 
 // ---------------------------------------------------------------------------------------
-// block reductions over all 9 waves (LDS only)
+// GEMV input rows
 // ---------------------------------------------------------------------------------------
 
-DF_DEVICE float block_sum9(float v, Lds& L, const Ctx& c) {
-  v = wave_sum(v);
-  __syncthreads();
-  if (c.lane == 0) L.red[c.wave] = v;
-  __syncthreads();
-  float t = 0.0f;
-#pragma unroll
-  for (int i = 0; i <= kCompute; ++i) t += L.red[i];
-  return t;
-}
-
-// x row 0 = RMSNorm(h) * (1 + w) over `hidden` (w staged in L.nw); row 1 zero.
-DF_DEVICE void norm_prologue(Lds& L, const Ctx& c, int hidden, float eps) {
+// Compute waves (2 barriers; the control wave passes 2): g_x = bf16(RMSNorm(h) * (1 + w))
+// over `hidden` (w staged in L.nw) and the group sums L.xs. A wave produces whole 128-groups
+// (2 elements per lane).
+constexpr int kNormBars = 2;
+DF_DEVICE void norm_w(Lds& L, Ctx& c, int hidden, float eps) {
   float ss = 0.0f;
-  for (int k = c.tid; k < hidden; k += kThreads) {
+  for (int k = c.tid; k < hidden; k += kCompute * 64) {
     const float v = bf2f(L.h[k]);
     ss += v * v;
   }
-  ss = block_sum9(ss, L, c);
-  const float r = 1.0f / sqrtf(ss / static_cast<float>(hidden) + eps);
-  for (int k = c.tid; k < hidden; k += kThreads) {
-    const float scaled = bf2f(L.h[k]) * r;
-    L.x[0][k] = f2bf(scaled * (1.0f + bf2f(L.nw[k])));
-    L.x[1][k] = 0;
+  ss = wave_sum(ss);
+  if (c.lane == 0) L.red[c.wave] = ss;
+  sync(c);
+  float tot = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kCompute; ++i) tot += L.red[i];
+  const float r = 1.0f / sqrtf(tot / static_cast<float>(hidden) + eps);
+  const int G = hidden / kGroup;
+  for (int g = c.wave; g < G; g += kCompute) {
+    const int k = g * kGroup + 2 * c.lane;
+    float y[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float scaled = bf2f(L.h[k + e]) * r;
+      const uint16_t b = f2bf(scaled * (1.0f + bf2f(L.nw[k + e])));
+      g_x[k + e] = b;
+      y[e] = bf2f(b);
+    }
+    const float sg = wave_sum(y[0] + y[1]);
+    if (c.lane == 0) L.xs[g] = kBias * sg;
   }
-  __syncthreads();
+  sync(c);
+}
+
+// Control wave: L.xs of `groups` 128-groups of g_x (after it wrote g_x itself).
+DF_DEVICE void group_sums(Lds& L, const Ctx& c, int groups) {
+  for (int g = 0; g < groups; ++g) {
+    const uint32_t pr = *reinterpret_cast<const uint32_t*>(&g_x[g * kGroup + 2 * c.lane]);
+    const float s = wave_sum(bf2f(static_cast<uint16_t>(pr)) + bf2f(static_cast<uint16_t>(pr >> 16)));
+    if (c.lane == 0) L.xs[g] = kBias * s;
+  }
 }
 
 // ---------------------------------------------------------------------------------------
-// GEMV phase over a block range of this XCD's slice
+// GEMV phases and the weight stream
 // ---------------------------------------------------------------------------------------
 
 struct Gemv {
   const uint8_t* w;
   const uint16_t* s;
-  int G;       // groups per tile in the stored matrix
-  int tile0;   // first tile of the XCD slice
-  int g0, ng;  // group slice
+  int G;           // groups per tile in the stored matrix
+  int tile0;       // first tile of the XCD slice
+  int g0, ng;      // group slice
   int b_lo, b_hi;  // this workgroup's block range (relative to the slice, tile-major)
 };
 
-struct WaveBlocks {
-  int lo, n;
-};
-
-// One block (1 KB of nibbles) and its 16 scales into ring slot (wave, slot) by LDS DMA
-// (dword granularity: lane i loads the scale pair holding its column i % 16).
-DF_DEVICE void dma_block(const uint8_t* w, const uint16_t* s, size_t blk, int wave, int slot, int lane, Lds& L) {
-  __builtin_amdgcn_global_load_lds((gbl_void*)(w + blk * kBlockBytes + lane * 16),
-                                   (lds_void*)&L.u.wq.wblk[wave][slot][0], 16, 0, 0);
-  __builtin_amdgcn_global_load_lds((gbl_void*)(s + blk * kTileCols + (lane & 14)),
-                                   (lds_void*)&L.u.wq.sblk[wave][slot][0], 4, 0, 0);
-}
-DF_DEVICE uint16_t block_scale(const Lds& L, int wave, int slot, int lane) {
-  return static_cast<uint16_t>(L.u.wq.sblk[wave][slot][lane] >> (16 * (lane & 1)));
+// Phase k of a layer (0 input projection, 1 out_proj / o_proj, 2 gate|up, 3 down) for
+// workgroup (xcd, r).
+DF_DEVICE Gemv gemv_of(LayerPtr Lp, const Geo& q, int k, int xcd, int r) {
+  Gemv g;
+  if (k == 0) {
+    const int nt = (Lp->kind == 0 ? kLinCols : kAttnCols) / kTileCols;
+    const int B = nt * q.Gh;
+    g = Gemv{Lp->proj_w, Lp->proj_s, q.Gh, xcd * nt, 0, q.Gh, (r * B) / kPerXcd, ((r + 1) * B) / kPerXcd};
+  } else if (k == 1) {
+    g = Gemv{Lp->out_w, Lp->out_s, 4096 / kGroup, 0, xcd * 4, 4, q.rp_lo * 4, q.rp_hi * 4};
+  } else if (k == 2) {
+    const int B = q.gu_tiles * q.Gh;
+    g = Gemv{Lp->gu_w, Lp->gu_s, q.Gh, xcd * q.gu_tiles, 0, q.Gh, (r * B) / kPerXcd, ((r + 1) * B) / kPerXcd};
+  } else {
+    g = Gemv{Lp->down_w, Lp->down_s, q.inter / kGroup, 0, xcd * q.ngx, q.ngx, q.rp_lo * q.ngx, q.rp_hi * q.ngx};
+  }
+  return g;
 }
 
 DF_DEVICE void wave_range(const Gemv& g, int wave, int& lo, int& n) {
@@ -342,53 +420,288 @@ DF_DEVICE void wave_range(const Gemv& g, int wave, int& lo, int& n) {
   n = g.b_lo + (len * (wave + 1)) / kCompute - lo;
 }
 
-// Compute waves: request this wave's blocks (issued before the phase's hand-off wait).
-// Weights and scales go straight to this wave's LDS region (global_load_lds: lane i's
-// bytes land at offset size * i, so a block keeps its register layout).
-DF_DEVICE void gemv_issue(const Gemv& g, const Ctx& c, WaveBlocks& B, Lds& L) {
-  wave_range(g, c.wave, B.lo, B.n);
-#pragma unroll 1
-  for (int i = 0; i < B.n; ++i) {
-    const int b = B.lo + i;
-    const int t = g.tile0 + b / g.ng, gg = g.g0 + b % g.ng;
-    dma_block(g.w, g.s, (size_t)t * g.G + gg, c.wave, i, c.lane, L);
+DF_DEVICE int head_tiles_of_wave(const Geo& q, int wave) {
+  const int n = q.t_hi - q.t_lo - wave;
+  return n > 0 ? (n + kCompute - 1) / kCompute : 0;
+}
+
+// A compute wave's weight stream. The issue cursor is the next block's weight and scale
+// addresses; a segment (one (layer, phase) or the head, of token `istep` of the launch) is
+// a run of blocks whose addresses advance by one block, with a jump of `wjump` blocks after
+// every `ng`-group tile run (row-parallel slices and the head's strided tiles).
+struct Stream {
+  const uint8_t* wp;     // weights of the next block to issue (lane 0's 16 bytes)
+  const uint16_t* sp;    // its 16 scales
+  int g, ng, wjump;      // position in the tile run, groups per run, blocks skipped after a run
+  int left;              // blocks left in the segment
+  int issued, consumed;  // blocks, since the launch began
+  int wslot, rslot;      // ring slots of the next issue / the next consume
+  int state;             // 0 streaming, 1 held before an attention layer's o_proj,
+                         // 2 released, 3 past the launch's last block
+  int li, k, istep;      // segment of the cursor: layer, phase (0..3; 4 = head), token
+};
+
+enum StreamState : int { kStreaming = 0, kHeld = 1, kReleased = 2, kDone = 3 };
+
+// Position the cursor on the first block of the current segment, skipping empty segments;
+// stop at an attention layer's o_proj (until released) and after the last token.
+DF_DEVICE void seg_open(Stream& st, const DfPersistModel& M, const Geo& q, const Ctx& c, int steps) {
+  for (;;) {
+    if (st.k == 4) {
+      const int ntw = head_tiles_of_wave(q, c.wave);
+      if (ntw > 0) {
+        const size_t blk = (size_t)(q.t_lo + c.wave) * q.Gh;
+        st.wp = M.head_w + blk * kBlockBytes;
+        st.sp = M.head_s + blk * kTileCols;
+        st.g = 0;
+        st.ng = q.Gh;
+        st.wjump = (kCompute - 1) * q.Gh;
+        st.left = ntw * q.Gh;
+        return;
+      }
+    } else {
+      LayerPtr Lp = layer_at(M, st.li);
+      if (st.k == 1 && Lp->kind == 1) {
+        if (st.state == kStreaming) {
+          st.state = kHeld;
+          return;
+        }
+        st.state = kStreaming;
+      }
+      const Gemv g = gemv_of(Lp, q, st.k, c.xcd, c.r);
+      int lo, n;
+      wave_range(g, c.wave, lo, n);
+      if (n > 0) {
+        const size_t blk = (size_t)(g.tile0 + lo / g.ng) * g.G + g.g0 + lo % g.ng;
+        st.wp = g.w + blk * kBlockBytes;
+        st.sp = g.s + blk * kTileCols;
+        st.g = lo % g.ng;
+        st.ng = g.ng;
+        st.wjump = g.G - g.ng;
+        st.left = n;
+        return;
+      }
+    }
+    // next segment
+    if (st.k < 3) {
+      st.k += 1;
+    } else if (st.k == 3) {
+      if (st.li + 1 < M.num_layers) {
+        st.li += 1;
+        st.k = 0;
+      } else {
+        st.k = 4;
+      }
+    } else {
+      st.istep += 1;
+      if (st.istep >= steps) {
+        st.state = kDone;
+        return;
+      }
+      st.li = 0;
+      st.k = 0;
+    }
   }
 }
 
-// Compute waves: MFMA over the requested blocks with x row 0 of L.x (the K slice of the
-// phase, index k - 128 * g0); per-tile partials of row 0 go to L.part[tile - first][wave].
-DF_DEVICE void gemv_compute(const Gemv& g, const Ctx& c, const WaveBlocks& B, Lds& L) {
-  wait_vm<0>();  // this wave's weight blocks and scales have landed
-  const int col = c.lane & 15, slot = c.lane >> 4;
-  const uint16_t* xrow = &L.x[col == 0 ? 0 : 1][slot * 32];
-  const int t_first = g.b_lo / g.ng;
-  df_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  int cur = B.n > 0 ? B.lo / g.ng : 0;
-#pragma unroll 1
-  for (int i = 0; i < B.n; ++i) {
-    const int b = B.lo + i;
-    const int t = b / g.ng, gl = b % g.ng;
-    if (t != cur) {
-      if (c.lane < 16) L.part[cur - t_first][c.wave][c.lane] = acc[0];
-      acc = df_f32x4{0.f, 0.f, 0.f, 0.f};
-      cur = t;
+// LDS DMA of 16 (or 4) bytes per lane: lane i's bytes land at lds_base + 16 i (4 i). Written
+// as inline asm so the compiler does not track these loads: it would otherwise treat every
+// later LDS access of the wave as possibly aliasing a pending DMA and wait for all of them
+// (vmcnt(0)), draining the ring. The kernel orders ring reads itself (wait_blocks); the
+// compiler's own vmcnt waits only get stricter, never wrong, for loads it does not count.
+DF_DEVICE void dma16(const void* gaddr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds_base)
+               : "memory", "m0");
+}
+DF_DEVICE void dma4(const void* gaddr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(gaddr), "s"(lds_base)
+               : "memory", "m0");
+}
+
+// Issue the cursor's block into the next ring slot (weights + scales) and advance.
+DF_DEVICE void issue_one(Stream& st, const DfPersistModel& M, const Geo& q, const Ctx& c, int steps) {
+  dma16(st.wp + c.lane * 16, lds_addr(&g_ring_w[c.wave][st.wslot][0]));
+  dma4(st.sp + (c.lane & 14), lds_addr(&g_ring_s[c.wave][st.wslot][0]));
+  st.issued += 1;
+  st.wslot = st.wslot + 1 == kRing ? 0 : st.wslot + 1;
+  int adv = 1;
+  if (++st.g == st.ng) {
+    st.g = 0;
+    adv += st.wjump;
+  }
+  st.wp += (size_t)adv * kBlockBytes;
+  st.sp += (size_t)adv * kTileCols;
+  if (--st.left == 0) {
+    if (st.k < 3) {
+      st.k += 1;
+    } else if (st.k == 3) {
+      if (st.li + 1 < M.num_layers) {
+        st.li += 1;
+        st.k = 0;
+      } else {
+        st.k = 4;
+      }
+    } else {
+      st.istep += 1;
+      if (st.istep >= steps) {
+        st.state = kDone;
+        return;
+      }
+      st.li = 0;
+      st.k = 0;
     }
-    const uint4 wv = L.u.wq.wblk[c.wave][i][c.lane];
-    const GroupScale gs = group_scale(block_scale(L, c.wave, i, c.lane));
-    const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+    seg_open(st, M, q, c, steps);
+  }
+}
+
+DF_DEVICE void fill(Stream& st, const DfPersistModel& M, const Geo& q, const Ctx& c, int steps) {
+  while (st.state == kStreaming && st.issued - st.consumed < kRing) issue_one(st, M, q, c, steps);
+}
+
+// Wait until at most k blocks (2 loads each) issued after the oldest pending one are in flight.
+DF_DEVICE void wait_blocks(int k) {
+  switch (k) {
+    case 0: wait_vm<0>(); break;
+    case 1: wait_vm<2>(); break;
+    case 2: wait_vm<4>(); break;
+    case 3: wait_vm<6>(); break;
+    case 4: wait_vm<8>(); break;
+    case 5: wait_vm<10>(); break;
+    case 6: wait_vm<12>(); break;
+    case 7: wait_vm<14>(); break;
+    case 8: wait_vm<16>(); break;
+    case 9: wait_vm<18>(); break;
+    case 10: wait_vm<20>(); break;
+    default: wait_vm<0>(); break;
+  }
+}
+static_assert(kRing <= 11, "wait_blocks covers k < kRing");
+
+// Wait for the oldest `need` pending blocks (need = 1 or 2); a full ring is the common case.
+DF_DEVICE void wait_oldest(const Stream& st, int need) {
+  const int pending = st.issued - st.consumed;
+  if (need == 1 && pending == kRing) wait_vm<2 * (kRing - 1)>();
+  else if (need == 2 && pending == kRing) wait_vm<2 * (kRing - 2)>();
+  else wait_blocks(pending - need);
+}
+
+DF_DEVICE int next_slot(int s) { return s + 1 == kRing ? 0 : s + 1; }
+
+// One block's weights and scale dword from ring slot `slot` of this wave.
+DF_DEVICE void ring_read1(int slot, const Ctx& c, uint4& wv, uint32_t& sd) {
+  const uint32_t wa = lds_addr(&g_ring_w[c.wave][slot][c.lane]);
+  const uint32_t sa = lds_addr(&g_ring_s[c.wave][slot][c.lane]);
+  asm volatile("ds_read_b128 %0, %2\n\tds_read_b32 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+               : "=&v"(wv), "=&v"(sd)
+               : "v"(wa), "v"(sa)
+               : "memory");
+}
+
+// Two consecutive blocks (slots `slot` and next_slot(slot)) with one LDS wait.
+DF_DEVICE void ring_read2(int slot, const Ctx& c, uint4& w0, uint32_t& s0, uint4& w1, uint32_t& s1) {
+  const int slot1 = next_slot(slot);
+  const uint32_t wa0 = lds_addr(&g_ring_w[c.wave][slot][c.lane]);
+  const uint32_t sa0 = lds_addr(&g_ring_s[c.wave][slot][c.lane]);
+  const uint32_t wa1 = lds_addr(&g_ring_w[c.wave][slot1][c.lane]);
+  const uint32_t sa1 = lds_addr(&g_ring_s[c.wave][slot1][c.lane]);
+  asm volatile(
+      "ds_read_b128 %0, %4\n\tds_read_b32 %1, %5\n\tds_read_b128 %2, %6\n\tds_read_b32 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(w0), "=&v"(s0), "=&v"(w1), "=&v"(s1)
+      : "v"(wa0), "v"(sa0), "v"(wa1), "v"(sa1)
+      : "memory");
+}
+
+// Wait for the oldest pending block and read it.
+DF_DEVICE void take_block(Stream& st, const Ctx& c, uint4& wv, uint32_t& sd) {
+  wait_oldest(st, 1);
+  ring_read1(st.rslot, c, wv, sd);
+  st.consumed += 1;
+  st.rslot = next_slot(st.rslot);
+}
+
+DF_DEVICE void take_blocks2(Stream& st, const Ctx& c, uint4& w0, uint32_t& s0, uint4& w1, uint32_t& s1) {
+  wait_oldest(st, 2);
+  ring_read2(st.rslot, c, w0, s0, w1, s1);
+  st.consumed += 2;
+  st.rslot = next_slot(next_slot(st.rslot));
+}
+
+// (a & mask) | bias in one VALU op (gfx9 VOP3 takes no literals: mask from an SGPR, bias
+// from a VGPR, one constant-bus read).
+DF_DEVICE uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bias) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(bias));
+  return r;
+}
+
+// Two weights k = 2j, 2j+1 of a dword (nibbles at bits 4j and 16 + 4j) as bf16(128 + n).
+DF_DEVICE uint32_t bias_pair(uint32_t w, int j, uint32_t bias) {
+  return and_or(j == 0 ? w : w >> (4 * j), 0x000F000Fu, bias);
+}
+
+// Row 0 of one block's product: lanes 0..15 return s_col * sum_k x_k (n_k - 8) over the
+// block's 128 k (x = the group's input at this lane's k slot; xs = 136 * sum of the group).
+DF_DEVICE float block_dot(const uint4& wv, uint32_t sd, const uint16_t* x, float xs, int lane) {
+  const float s = __uint_as_float((lane & 1) ? (sd & 0xFFFF0000u) : (sd << 16));
+  const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+  const uint32_t bias = kBiasPair;
+  df_f32x4 d4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const uint4 bw = dequant8(words[d], gs);
-      const uint4 aw = *reinterpret_cast<const uint4*>(xrow + gl * kGroup + d * 8);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, aw),
-                                                    __builtin_bit_cast(df_bf16x8, bw), acc, 0, 0, 0);
-    }
+  for (int d = 0; d < 4; ++d) {
+    const uint4 bw = make_uint4(bias_pair(words[d], 0, bias), bias_pair(words[d], 1, bias),
+                                bias_pair(words[d], 2, bias), bias_pair(words[d], 3, bias));
+    const uint4 aw = *reinterpret_cast<const uint4*>(x + d * 8);
+    d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, aw), __builtin_bit_cast(df_bf16x8, bw),
+                                                 d4, 0, 0, 0);
   }
-  if (B.n > 0 && c.lane < 16) L.part[cur - t_first][c.wave][c.lane] = acc[0];
+  return s * (d4[0] - xs);
 }
 
-DF_DEVICE void zero_part(Lds& L, const Ctx& c) {
-  for (int e = c.tid; e < kMaxWgTiles * kCompute * 16; e += kThreads) (&L.part[0][0][0])[e] = 0.0f;
+// Compute waves: consume this wave's blocks of GEMV phase g (input row g_x, group sums
+// L.xs); per-tile partials of row 0 go to L.part[tile - first tile of the workgroup][wave].
+// Blocks are taken two at a time (two independent MFMA chains per iteration).
+DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPersistModel& M, const Geo& q,
+                            int steps, Lds& L) {
+  int lo, n;
+  wave_range(g, c.wave, lo, n);
+  // this wave's partial of every tile starts at zero (only this wave writes its column, and
+  // the control wave read the previous phase's partials before the barrier that began this one)
+  for (int e = c.lane; e < kMaxWgTiles * 16; e += 64) L.part[e / 16][c.wave][e % 16] = 0.0f;
+  const uint16_t* xb = g_x + (c.lane >> 4) * 32;
+  int tr = lo / g.ng - g.b_lo / g.ng;
+  int gl = lo % g.ng;
+  float acc = 0.0f;
+  auto add = [&](float v) {
+    acc += v;
+    if (++gl == g.ng) {
+      if (c.lane < 16) L.part[tr][c.wave][c.lane] = acc;
+      acc = 0.0f;
+      gl = 0;
+      ++tr;
+    }
+  };
+  int i = 0;
+#pragma unroll 1
+  for (; i + 1 < n; i += 2) {
+    uint4 w0, w1;
+    uint32_t s0, s1;
+    take_blocks2(st, c, w0, s0, w1, s1);
+    const int gl1 = gl + 1 == g.ng ? 0 : gl + 1;
+    const float v0 = block_dot(w0, s0, xb + gl * kGroup, L.xs[gl], c.lane);
+    const float v1 = block_dot(w1, s1, xb + gl1 * kGroup, L.xs[gl1], c.lane);
+    fill(st, M, q, c, steps);
+    add(v0);
+    add(v1);
+  }
+  if (i < n) {
+    uint4 w0;
+    uint32_t s0;
+    take_block(st, c, w0, s0);
+    add(block_dot(w0, s0, xb + gl * kGroup, L.xs[gl], c.lane));
+    fill(st, M, q, c, steps);
+  }
+  if (n > 0 && gl != 0 && c.lane < 16) L.part[tr][c.wave][c.lane] = acc;
 }
 
 // Sum of the waves' partials for relative tile t (fixed wave order).
@@ -399,18 +712,9 @@ DF_DEVICE float part_sum(const Lds& L, int t, int col) {
   return v;
 }
 
-// ---------------------------------------------------------------------------------------
-// Phase drivers. Each follows the same barrier schedule on every wave:
-//   compute waves: issue loads | control: wait + stage   -> sync
-//   all: prologue (LDS)                                  -> sync
-//   compute waves: compute                               -> sync
-//   all: epilogue stores; signal
-// ---------------------------------------------------------------------------------------
-
 // ---- control-wave staging: every load of a hand-off is issued before any is used -------
 
 typedef __attribute__((__vector_size__(4 * sizeof(int)))) int df_i4;
-typedef __attribute__((__vector_size__(2 * sizeof(int)))) int df_i2;
 constexpr int kCpPlain = 0, kCpAgent = 16, kCpSystem = 17;  // buffer cache policy: -, sc1, sc0|sc1
 
 DF_DEVICE __amdgpu_buffer_rsrc_t rsrc(const void* p) {
@@ -487,12 +791,12 @@ DF_DEVICE void gather_colpar(const Ctx& c, const Seg (&seg)[NS]) {
   }
 }
 
-// The down projection's input: act = bf16(bf16(silu(g)) * u) over the XCD's inter_x gate|up
-// column pairs (16-column gate tile, then its up tile), straight from the column-parallel
-// slots. Chunk ch (4 columns) of pair ch / 8 is a gate chunk for ch % 8 < 4; its up
-// partner is chunk ch + 4, held 4 lanes up.
+// The down projection's input into g_x: act = bf16(bf16(silu(g)) * u) over the XCD's
+// inter_x gate|up column pairs (16-column gate tile, then its up tile), straight from the
+// column-parallel slots. Chunk ch (4 columns) of pair ch / 8 is a gate chunk for
+// ch % 8 < 4; its up partner is chunk ch + 4, held 4 lanes up.
 template <int K>
-DF_DEVICE void stage_act(const Ctx& c, int inter_x, Lds& L) {
+DF_DEVICE void stage_act(const Ctx& c, int inter_x) {
   const auto r = rsrc(c.w.colpar + (size_t)c.xcd * 2 * kColparMax);
   const int chunks = inter_x / 2;
   uint4 a[K], b[K];
@@ -520,19 +824,19 @@ DF_DEVICE void stage_act(const Ctx& c, int inter_x, Lds& L) {
     if (ch < chunks && (c.lane & 7) < 4) {
       const int j = (ch / 8) * 16 + (ch % 8) * 4;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) L.x[0][j + e] = f2bf(round_bf(silu(v[e])) * u[e]);
+      for (int e = 0; e < 4; ++e) g_x[j + e] = f2bf(round_bf(silu(v[e])) * u[e]);
     }
   }
 }
 
-// Column-parallel epilogue: this workgroup's partial of each tile it touched into its slot
-// (r & 1); tiles wholly inside its range also zero the other slot.
+// Control wave, column-parallel epilogue: this workgroup's partial of each tile it touched
+// into its slot (r & 1); tiles wholly inside its range also zero the other slot.
 DF_DEVICE void colpar_epilogue(const Gemv& g, const Ctx& c, const Lds& L) {
   const int t_first = g.b_lo / g.ng, t_last = (g.b_hi - 1) / g.ng;
   const int nt = t_last - t_first + 1;
   float* cp = c.w.colpar + (size_t)c.xcd * 2 * kColparMax;
   const int mine = c.r & 1;
-  for (int e = c.tid; e < nt * 16; e += kThreads) {
+  for (int e = c.lane; e < nt * 16; e += 64) {
     const int tr = e / 16, col = e % 16;
     const int t = t_first + tr;
     const float v = part_sum(L, tr, col);
@@ -543,91 +847,76 @@ DF_DEVICE void colpar_epilogue(const Gemv& g, const Ctx& c, const Lds& L) {
   }
 }
 
-// Row-parallel epilogue: the XCD's partial of hidden columns [16 t_first, ...) with epoch.
+// Control wave, row-parallel epilogue: the XCD's partial of hidden columns [16 t_first, ...)
+// with epoch.
 DF_DEVICE void rowpar_epilogue(const Gemv& g, const Ctx& c, const Lds& L, int hidden) {
   const int t_first = g.b_lo / g.ng, nt = (g.b_hi - g.b_lo) / g.ng;
   uint64_t* rp = c.w.rowpar + ((size_t)(c.ar & 1) * kXcd + c.xcd) * hidden;
-  for (int e = c.tid; e < nt * 16; e += kThreads) {
+  for (int e = c.lane; e < nt * 16; e += 64) {
     const int tr = e / 16, col = e % 16;
     st_sys(rp + (t_first + tr) * 16 + col, pack_epoch(part_sum(L, tr, col), c.epoch));
   }
 }
 
-// The all-reduce after a row-parallel phase (control wave polls, all waves finish):
-// slice [sl0, sl0 + ns) of y = sum over XCDs (in order); h = bf16(h + bf16(y)); publish
-// the slice to this XCD's copy of h; wait for the XCD; read all of h back into LDS.
+// Control wave, the all-reduce after a row-parallel phase: slice [sl0, sl0 + ns) of y = sum
+// over XCDs (in order); h = bf16(h + bf16(y)); publish the slice to this XCD's copy of h;
+// wait for the XCD; read all of h back into LDS. The caller's next barrier hands h to the
+// compute waves.
 DF_DEVICE bool allreduce_residual(Ctx& c, Lds& L, int hidden) {
   fence(c, kTReduce);
-  const int ns = hidden / kPerXcd;  // <= 128
+  const int ns = hidden / kPerXcd;  // <= 80
   const int sl0 = c.r * ns;
   const uint64_t* rp = c.w.rowpar + (size_t)(c.ar & 1) * kXcd * hidden;
-  if (c.control) {
-    // slice [sl0, sl0 + ns) of the 8 XCD partials: item i = (x = i / ns, column i % ns)
-    constexpr int K = (kXcd * (kMaxHidden / kPerXcd) + 63) / 64;
-    const auto r = rsrc(rp);
-    const int items = kXcd * ns;
-    uint64_t v[K];
-    bool ok = true;
-    const uint64_t t0 = now();
-    for (;;) {
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        const int i = c.lane + 64 * k;
-        if (i < items) v[k] = ld8<kCpSystem>(r, ((i / ns) * hidden + sl0 + i % ns) * 8);
-      }
-      bool ready = true;
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        const int i = c.lane + 64 * k;
-        if (i < items) ready = ready && static_cast<uint32_t>(v[k] >> 32) == c.epoch;
-      }
-      if (__all(ready)) break;
-      if (ld_sys(c.w.ctl + 1)) { ok = false; break; }
-      if (now() - t0 > kTimeout) { raise_abort(c, kErrTimeout); ok = false; break; }
-      __builtin_amdgcn_s_sleep(1);
-    }
-    if (ok) {
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        const int i = c.lane + 64 * k;
-        if (i < items) L.u.rd.y[i / ns][i % ns] = __uint_as_float(static_cast<uint32_t>(v[k]));
-      }
-    }
-    if (c.lane == 0) L.ok = ok;
-  }
-  __syncthreads();
-  if (!L.ok) return false;
-  // h slice update (one thread per column)
-  uint16_t* hx = c.w.hloc + (size_t)c.xcd * hidden;
-  if (c.tid < ns) {
-    float y = 0.0f;
-#pragma unroll
-    for (int x = 0; x < kXcd; ++x) y += L.u.rd.y[x][c.tid];
-    const int k = sl0 + c.tid;
-    const uint16_t hn = f2bf(bf2f(L.h[k]) + round_bf(y));
-    hx[k] = hn;
-  }
+  const uint32_t want = c.epoch;
   c.ar += 1;
   c.epoch += 1;
-  signal_local(c, c.epoch);
-  if (c.control) {
-    const bool ok = wait_local(c, c.epoch);
-    if (ok) stage16<kHidChunks, kCpAgent>(L.h, hx, hidden, c.lane);
-    if (c.lane == 0) L.ok = ok;
+  // slice [sl0, sl0 + ns) of the 8 XCD partials: item i = (x = i / ns, column i % ns)
+  constexpr int K = (kXcd * (kMaxHidden / kPerXcd) + 63) / 64;
+  const auto r = rsrc(rp);
+  const int items = kXcd * ns;
+  uint64_t v[K];
+  bool ok = true;
+  const uint64_t t0 = now();
+  for (;;) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int i = c.lane + 64 * k;
+      if (i < items) v[k] = ld8<kCpSystem>(r, ((i / ns) * hidden + sl0 + i % ns) * 8);
+    }
+    bool ready = true;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int i = c.lane + 64 * k;
+      if (i < items) ready = ready && static_cast<uint32_t>(v[k] >> 32) == want;
+    }
+    if (__all(ready)) break;
+    if (ld_sys(c.w.ctl + 1)) { ok = false; break; }
+    if (now() - t0 > kTimeout) { raise_abort(c, kErrTimeout); ok = false; break; }
+    __builtin_amdgcn_s_sleep(1);
   }
-  __syncthreads();
-  return L.ok;
+  if (!ok) return false;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int i = c.lane + 64 * k;
+    if (i < items) L.u.rd.y[i / ns][i % ns] = __uint_as_float(static_cast<uint32_t>(v[k]));
+  }
+  uint16_t* hx = c.w.hloc + (size_t)c.xcd * hidden;
+  for (int j = c.lane; j < ns; j += 64) {
+    float y = 0.0f;
+#pragma unroll
+    for (int x = 0; x < kXcd; ++x) y += L.u.rd.y[x][j];
+    const int k = sl0 + j;
+    hx[k] = f2bf(bf2f(L.h[k]) + round_bf(y));
+  }
+  signal_local(c, c.epoch);
+  if (!wait_local(c, c.epoch)) return false;
+  stage16<kHidChunks, kCpAgent>(L.h, hx, hidden, c.lane);
+  return true;
 }
 
 // ---------------------------------------------------------------------------------------
 // Gated DeltaNet step for (value head 4x + r/8, value columns 16 (r%8) ..+15)
 // ---------------------------------------------------------------------------------------
-
-struct DnPre {
-  float4 S;          // state row k = tid/4, columns 4 (tid%4) ..+3 of the slice
-  float w[4];        // conv taps of this thread's channel (tid < 272)
-  float h[3];        // its three history values (oldest first)
-};
 
 DF_DEVICE int dn_channel(const Ctx& c, int i) {
   // i in 0..271: q (128), k (128), v slice (16) of this workgroup's unit -> global channel
@@ -638,43 +927,83 @@ DF_DEVICE int dn_channel(const Ctx& c, int i) {
   return 2 * kKeyDim + hv * kDk + vs * 16 + (i - 256);
 }
 
-DF_DEVICE void dn_issue(const Ctx& c, const DfPersistLayer& Lr, DnPre& P) {
+// Control wave: the unit's state slice, conv taps and history, the gate parameters and,
+// after the in_proj hand-off, its pre-conv inputs and gates, all into LDS.
+DF_DEVICE bool dn_stage(Ctx& c, LayerPtr Lp, Lds& L) {
+  auto& D = L.u.dn;
   const int hvl = c.r >> 3, vs = c.r & 7;
   const int hv = 4 * c.xcd + hvl;
-  const int k = c.tid >> 2, c4 = c.tid & 3;
-  P.S = *reinterpret_cast<const float4*>(Lr.state + ((size_t)hv * kDk + k) * kDk + vs * 16 + c4 * 4);
-  if (c.tid < 272) {
-    const int ch = dn_channel(c, c.tid);
-    const uint2 wt = *reinterpret_cast<const uint2*>(Lr.conv_w + (size_t)ch * 4);
-    P.w[0] = __uint_as_float(wt.x << 16);
-    P.w[1] = __uint_as_float(wt.x & 0xFFFF0000u);
-    P.w[2] = __uint_as_float(wt.y << 16);
-    P.w[3] = __uint_as_float(wt.y & 0xFFFF0000u);
-    const uint16_t* ring = Lr.conv_ring + (size_t)ch * 4;
-    // ring slots (pos+1)&3, (pos+2)&3, (pos+3)&3 hold positions pos-3, pos-2, pos-1;
-    // read at agent scope: another workgroup of the XCD writes the q/k slots
-    const uint64_t rv = ld_agent(reinterpret_cast<const uint64_t*>(ring));
-    const uint16_t sl[4] = {static_cast<uint16_t>(rv), static_cast<uint16_t>(rv >> 16),
-                            static_cast<uint16_t>(rv >> 32), static_cast<uint16_t>(rv >> 48)};
-    P.h[0] = bf2f(sl[(c.pos + 1) & 3]);
-    P.h[1] = bf2f(sl[(c.pos + 2) & 3]);
-    P.h[2] = bf2f(sl[(c.pos + 3) & 3]);
+  constexpr int kSt = kCompute;              // float4 of the state slice per lane
+  constexpr int kCh = (kDnCh + 63) / 64;     // conv channels per lane
+  uint4 sv[kSt];
+  const float* state = Lp->state;
+#pragma unroll
+  for (int i = 0; i < kSt; ++i) {
+    const int e = c.lane + 64 * i;  // row e / 4, columns 4 (e % 4)
+    sv[i] = *reinterpret_cast<const uint4*>(state + ((size_t)hv * kDk + (e >> 2)) * kDk + vs * 16 + (e & 3) * 4);
   }
+  uint2 tp[kCh];
+  uint64_t hs[kCh];
+#pragma unroll
+  for (int i = 0; i < kCh; ++i) {
+    const int ch = c.lane + 64 * i;
+    if (ch < kDnCh) {
+      const int gc = dn_channel(c, ch);
+      tp[i] = *reinterpret_cast<const uint2*>(Lp->conv_w + (size_t)gc * 4);
+      // another workgroup of the XCD writes the q/k history slots: read at agent scope
+      hs[i] = ld_agent(reinterpret_cast<const uint64_t*>(Lp->conv_ring + (size_t)gc * 4));
+    }
+  }
+  const float alog = bf2f(Lp->A_log[hv]), dtb = bf2f(Lp->dt_bias[hv]);
+  const bool ok = wait_local(c, c.epoch);
+  if (ok) {
+    const int khl = hvl >> 1;
+    const Seg seg[4] = {{kLinQ + khl * 128, 128, D.qkv_in},
+                        {kLinK + khl * 128, 128, D.qkv_in + 128},
+                        {kLinV + hvl * 128 + vs * 16, 16, D.qkv_in + 256},
+                        {kLinA, 8, D.ab8}};
+    gather_colpar<4, 2>(c, seg);
+  }
+#pragma unroll
+  for (int i = 0; i < kSt; ++i) D.S[c.lane + 64 * i] = __builtin_bit_cast(float4, sv[i]);
+#pragma unroll
+  for (int i = 0; i < kCh; ++i) {
+    const int ch = c.lane + 64 * i;
+    if (ch < kDnCh) {
+      D.taps[ch] = tp[i];
+      D.hist[ch] = __builtin_bit_cast(uint2, hs[i]);
+    }
+  }
+  if (c.lane == 0) {
+    D.gpar[0] = alog;
+    D.gpar[1] = dtb;
+  }
+  return ok;
 }
 
-// After the control wave staged the pre-conv inputs and gates (L.u.dn.qkv_in, ab).
-DF_DEVICE void dn_compute(const Ctx& c, const DfPersistLayer& Lr, DnPre& P, Lds& L) {
+// Compute waves (kDnBars barriers), after dn_stage: conv + SiLU, gates, L2 norms, the delta
+// rule. They write the new state and the conv history themselves (nothing reads them
+// before the next token); the core output goes to L.u.dn.core for the control wave.
+constexpr int kDnBars = 6;
+DF_DEVICE void dn_compute(Ctx& c, LayerPtr Lp, Lds& L) {
 #pragma clang fp contract(off)
   const int hvl = c.r >> 3, vs = c.r & 7;
   const int hv = 4 * c.xcd + hvl;
   auto& D = L.u.dn;
-  // conv + SiLU (fp32 sum in tap order, bf16, SiLU, bf16)
-  if (c.tid < 272) {
+  // conv + SiLU (fp32 sum in tap order, bf16, SiLU, bf16); history slots (pos+1)&3,
+  // (pos+2)&3, (pos+3)&3 hold positions pos-3, pos-2, pos-1
+  if (c.tid < kDnCh) {
+    const uint2 wt = D.taps[c.tid], hr = D.hist[c.tid];
+    const float w0 = __uint_as_float(wt.x << 16), w1 = __uint_as_float(wt.x & 0xFFFF0000u);
+    const float w2 = __uint_as_float(wt.y << 16), w3 = __uint_as_float(wt.y & 0xFFFF0000u);
+    const uint16_t sl[4] = {static_cast<uint16_t>(hr.x), static_cast<uint16_t>(hr.x >> 16),
+                            static_cast<uint16_t>(hr.y), static_cast<uint16_t>(hr.y >> 16)};
+    const float h0 = bf2f(sl[(c.pos + 1) & 3]), h1 = bf2f(sl[(c.pos + 2) & 3]), h2 = bf2f(sl[(c.pos + 3) & 3]);
     const float x = D.qkv_in[c.tid];
-    float acc = P.h[0] * P.w[0];
-    acc = acc + P.h[1] * P.w[1];
-    acc = acc + P.h[2] * P.w[2];
-    acc = acc + x * P.w[3];
+    float acc = h0 * w0;
+    acc = acc + h1 * w1;
+    acc = acc + h2 * w2;
+    acc = acc + x * w3;
     const float y = round_bf(silu(round_bf(acc)));
     if (c.tid < 128) D.q[c.tid] = y;
     else if (c.tid < 256) D.k[c.tid - 128] = y;
@@ -682,19 +1011,16 @@ DF_DEVICE void dn_compute(const Ctx& c, const DfPersistLayer& Lr, DnPre& P, Lds&
     // history: this unit owns its v slice; the (even value head, slice 0) unit owns the
     // key head's q/k channels
     const bool owner = c.tid >= 256 || ((hvl & 1) == 0 && vs == 0);
-    if (owner) {
-      uint16_t* ring = Lr.conv_ring + (size_t)dn_channel(c, c.tid) * 4;
-      ring[c.pos & 3] = f2bf(x);
-    }
+    if (owner) Lp->conv_ring[(size_t)dn_channel(c, c.tid) * 4 + (c.pos & 3)] = f2bf(x);
   }
   if (c.tid == 0) {
     const float a = D.ab8[hvl], b = D.ab8[4 + hvl];
     const float beta = round_bf(sigmoid(b));
-    const float g = -expf(bf2f(Lr.A_log[hv])) * softplus(a + bf2f(Lr.dt_bias[hv]));
+    const float g = -expf(D.gpar[0]) * softplus(a + D.gpar[1]);
     D.scal[0] = expf(g);
     D.scal[1] = beta;
   }
-  __syncthreads();
+  sync(c);
   // L2 norms: wave 0 q, wave 1 k (2 values per lane)
   if (c.wave < 2) {
     float* vec = c.wave == 0 ? D.q : D.k;
@@ -710,22 +1036,20 @@ DF_DEVICE void dn_compute(const Ctx& c, const DfPersistLayer& Lr, DnPre& P, Lds&
     vec[c.lane * 2] = y0;
     vec[c.lane * 2 + 1] = y1;
   }
-  __syncthreads();
+  sync(c);
   const float eg = D.scal[0], beta = D.scal[1];
   const int k = c.tid >> 2, c4 = c.tid & 3;
-  float part[4] = {0.f, 0.f, 0.f, 0.f};
+  float4 S = make_float4(0.f, 0.f, 0.f, 0.f);
   float kr = 0.f, qr = 0.f;
   if (!c.control) {
+    S = D.S[c.tid];
     kr = D.k[k];
     qr = D.q[k];
-    P.S.x = P.S.x * eg;
-    P.S.y = P.S.y * eg;
-    P.S.z = P.S.z * eg;
-    P.S.w = P.S.w * eg;
-    part[0] = P.S.x * kr;
-    part[1] = P.S.y * kr;
-    part[2] = P.S.z * kr;
-    part[3] = P.S.w * kr;
+    S.x = S.x * eg;
+    S.y = S.y * eg;
+    S.z = S.z * eg;
+    S.w = S.w * eg;
+    float part[4] = {S.x * kr, S.y * kr, S.z * kr, S.w * kr};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float v = part[j];
@@ -740,7 +1064,7 @@ DF_DEVICE void dn_compute(const Ctx& c, const DfPersistLayer& Lr, DnPre& P, Lds&
       for (int j = 0; j < 4; ++j) D.sred[c.wave][c4 * 4 + j] = part[j];
     }
   }
-  __syncthreads();
+  sync(c);
   float delta[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -750,14 +1074,14 @@ DF_DEVICE void dn_compute(const Ctx& c, const DfPersistLayer& Lr, DnPre& P, Lds&
     for (int wv = 0; wv < kCompute; ++wv) recalled += D.sred[wv][col];
     delta[j] = (D.v[col] - recalled) * beta;
   }
-  __syncthreads();  // sred is reused below
+  sync(c);  // sred is reused below
   if (!c.control) {
-    P.S.x = P.S.x + kr * delta[0];
-    P.S.y = P.S.y + kr * delta[1];
-    P.S.z = P.S.z + kr * delta[2];
-    P.S.w = P.S.w + kr * delta[3];
-    float o[4] = {P.S.x * qr, P.S.y * qr, P.S.z * qr, P.S.w * qr};
-    *reinterpret_cast<float4*>(Lr.state + ((size_t)hv * kDk + k) * kDk + vs * 16 + c4 * 4) = P.S;
+    S.x = S.x + kr * delta[0];
+    S.y = S.y + kr * delta[1];
+    S.z = S.z + kr * delta[2];
+    S.w = S.w + kr * delta[3];
+    float o[4] = {S.x * qr, S.y * qr, S.z * qr, S.w * qr};
+    *reinterpret_cast<float4*>(Lp->state + ((size_t)hv * kDk + k) * kDk + vs * 16 + c4 * 4) = S;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float v = o[j];
@@ -772,13 +1096,14 @@ DF_DEVICE void dn_compute(const Ctx& c, const DfPersistLayer& Lr, DnPre& P, Lds&
       for (int j = 0; j < 4; ++j) D.sred[c.wave][c4 * 4 + j] = o[j];
     }
   }
-  __syncthreads();
+  sync(c);
   if (c.tid < 16) {
     float o = 0.0f;
 #pragma unroll
     for (int wv = 0; wv < kCompute; ++wv) o += D.sred[wv][c.tid];
-    c.w.core[(size_t)c.xcd * 512 + hvl * kDk + vs * 16 + c.tid] = f2bf(o);
+    D.core[c.tid] = f2bf(o);
   }
+  sync(c);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -813,7 +1138,6 @@ DF_DEVICE void norm_rope4_lds(float x[4], const uint16_t* nw, float eps, const f
 
 struct AtPre {
   uint4 kb[8];   // K rows: this lane's key (t0 + 16 wave + col), dims d*32 + slot*8 ..+7
-  uint2 vb[16];  // V rows: keys t0 + 16 wave + j, dims 4 lane ..+3
 };
 
 DF_DEVICE void at_keys(const Ctx& c, int& j0, int& j1) {
@@ -823,38 +1147,51 @@ DF_DEVICE void at_keys(const Ctx& c, int& j0, int& j1) {
   j1 = min(j0 + per, nkeys);
 }
 
-// Compute waves: prefetch the split's first tile of keys/values (not the new position).
-DF_DEVICE void at_issue_tile(const Ctx& c, const DfPersistLayer& Lr, int t0, int j1, AtPre& P) {
+typedef const __attribute__((address_space(1))) uint16_t* GlobalBf16;
+typedef uint32_t df_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t df_u32x2 __attribute__((ext_vector_type(2)));
+// Loads through global-address-space pointers (never flat: see st_sys).
+DF_DEVICE uint4 gload16(GlobalBf16 p) {
+  const df_u32x4 v = *(const __attribute__((address_space(1))) df_u32x4*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+DF_DEVICE uint2 gload8(GlobalBf16 p) {
+  const df_u32x2 v = *(const __attribute__((address_space(1))) df_u32x2*)p;
+  return make_uint2(v.x, v.y);
+}
+
+// Compute waves: load the K rows of one 128-key tile of the split (not the new position).
+DF_DEVICE void at_issue_k(const Ctx& c, LayerPtr Lp, int t0, int j1, AtPre& P) {
   const int col = c.lane & 15, slot = c.lane >> 4;
-  const int kvh = c.xcd >> 1;
-  const size_t base = (size_t)kvh * c.M.max_len;
+  const size_t base = (size_t)(c.xcd >> 1) * c.max_len;
   const int key = t0 + c.wave * 16 + col;
   if (key < j1 && key != c.pos) {
-    const uint16_t* kp = Lr.k_cache + (base + key) * kHd + slot * 8;
+    GlobalBf16 kp = (GlobalBf16)Lp->k_cache + (base + key) * kHd + slot * 8;
 #pragma unroll
-    for (int d = 0; d < 8; ++d) P.kb[d] = load16(kp + d * 32);
-  }
-#pragma unroll
-  for (int jj = 0; jj < 16; ++jj) {
-    const int kk = t0 + c.wave * 16 + jj;
-    if (kk < j1 && kk != c.pos) P.vb[jj] = *reinterpret_cast<const uint2*>(Lr.v_cache + (base + kk) * kHd + c.lane * 4);
+    for (int d = 0; d < 8; ++d) P.kb[d] = gload16(kp + d * 32);
   }
 }
 
-// One 128-key tile: QK (MFMA), online softmax (waves 0 / 1 for heads 0 / 1), PV.
-DF_DEVICE void at_tile(const Ctx& c, int t0, int j1, const AtPre& P, float acc[2][4], float& m_run,
-                       float& l_run, Lds& L) {
+// Compute waves (kTileBars barriers): one 128-key tile: QK (MFMA), then the V rows are loaded
+// while the online softmax runs (waves 0 / 1 for heads 0 / 1), then PV.
+constexpr int kTileBars = 3;
+DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, float acc[2][4], Lds& L) {
   auto& A = L.u.at;
   const int col = c.lane & 15, slot = c.lane >> 4;
   const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
-  if (!c.control) {
+  // the tile's K loads are the only vector loads in flight (the weight stream is held):
+  // waiting for all of them here also tells the compiler that none is pending afterwards
+  wait_vm<0>();
+  {
     const int key = t0 + c.wave * 16 + col;
     const bool live = key < j1;
     df_f32x4 d4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
+      uint4 kn = *reinterpret_cast<const uint4*>(A.knew + d * 32 + slot * 8);
+      asm volatile("" : "+v"(kn.x), "+v"(kn.y), "+v"(kn.z), "+v"(kn.w));  // a value, not a pointer select into P
       uint4 bw = make_uint4(0u, 0u, 0u, 0u);
-      if (live) bw = key == c.pos ? *reinterpret_cast<const uint4*>(A.knew + d * 32 + slot * 8) : P.kb[d];
+      if (live) bw = key == c.pos ? kn : P.kb[d];
       uint4 aw = make_uint4(0u, 0u, 0u, 0u);
       if (col < 2) aw = *reinterpret_cast<const uint4*>(&A.q[col][d * 32 + slot * 8]);
       d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, aw), __builtin_bit_cast(df_bf16x8, bw),
@@ -865,7 +1202,19 @@ DF_DEVICE void at_tile(const Ctx& c, int t0, int j1, const AtPre& P, float acc[2
       A.sc[1][c.wave * 16 + col] = live ? d4[1] * scale : -INFINITY;
     }
   }
-  __syncthreads();
+  // V rows: keys t0 + 16 wave + j, dims 4 lane ..+3
+  uint2 vb[16];
+  {
+    const size_t base = (size_t)(c.xcd >> 1) * c.max_len;
+    GlobalBf16 vc = (GlobalBf16)Lp->v_cache;
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+      const int kk = t0 + c.wave * 16 + jj;
+      vb[jj] = make_uint2(0u, 0u);
+      if (kk < j1 && kk != c.pos) vb[jj] = gload8(vc + (base + kk) * kHd + c.lane * 4);
+    }
+  }
+  sync(c);
   if (c.wave < 2) {
     const int h = c.wave;
     const float s0 = A.sc[h][c.lane], s1 = A.sc[h][c.lane + 64];
@@ -887,19 +1236,22 @@ DF_DEVICE void at_tile(const Ctx& c, int t0, int j1, const AtPre& P, float acc[2
       A.alpha[h] = alpha;
     }
   }
-  __syncthreads();
-  if (!c.control) {
+  sync(c);
+  wait_vm<0>();  // the V rows (nothing else is in flight)
+  {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const float a = A.alpha[h];
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[h][i] *= a;
     }
+    uint2 vn = *reinterpret_cast<const uint2*>(A.vnew + c.lane * 4);
+    asm volatile("" : "+v"(vn.x), "+v"(vn.y));
 #pragma unroll
     for (int jj = 0; jj < 16; ++jj) {
       const int kk = t0 + c.wave * 16 + jj;
       if (kk < j1) {
-        const uint2 raw = kk == c.pos ? *reinterpret_cast<const uint2*>(A.vnew + c.lane * 4) : P.vb[jj];
+        const uint2 raw = kk == c.pos ? vn : vb[jj];
         const float v0 = __uint_as_float(raw.x << 16), v1 = __uint_as_float(raw.x & 0xFFFF0000u);
         const float v2 = __uint_as_float(raw.y << 16), v3 = __uint_as_float(raw.y & 0xFFFF0000u);
 #pragma unroll
@@ -913,23 +1265,589 @@ DF_DEVICE void at_tile(const Ctx& c, int t0, int j1, const AtPre& P, float acc[2
       }
     }
   }
-  __syncthreads();
-  (void)m_run;
-  (void)l_run;
+  sync(c);
 }
 
 // ---------------------------------------------------------------------------------------
-// the kernel
+// the two roles
+//
+// Barrier schedule per token (C = control wave, W = compute waves; every step below ends
+// at one barrier that both pass):
+//   embed      C: token row into L.h                                   | 1
+//   in_proj    C: stage norm weight                                    | 1
+//              W: RMSNorm -> g_x, group sums                           | kNormBars
+//              W: consume blocks                                       | 1, then C: epilogue, signal
+//   delta      C: state, conv, inputs after the hand-off               | 1
+//              W: conv, gates, delta rule                              | kDnBars, then C: publish core
+//   out_proj   C: hand-off, core / z / norm weight                     | 1
+//              W: GatedRMSNorm -> g_x, group sums                      | 3
+//              W: consume                                              | 1
+//              C: row-parallel partials, all-reduce, h into LDS        | 1
+//   attention  C: hand-off, q/k/v / norm weights; W: first KV tile     | 1
+//              W: q/k norm + RoPE                                      | 1
+//              W: tiles                                                | kTileBars per tile
+//              W: PV partials; sum                                     | 2, then C: publish split
+//   merge      C only
+//   o_proj     C: hand-off, core -> g_x, group sums                    | 1
+//              W: consume                                              | 1
+//              C: row-parallel partials, all-reduce                    | 1
+//   gate|up    as in_proj; down as o_proj with C staging act
+//   head       C: stage norm weight                                    | 1
+//              W: RMSNorm                                              | kNormBars
+//              W: consume head blocks, argmax per wave                 | 1
+//              C: logits, candidate, global argmax                     | 1
+// The control wave works on a phase's outputs (partials, logits) after that phase's last
+// barrier, so the compute waves write shared LDS only after the next barrier.
 // ---------------------------------------------------------------------------------------
+
+// The compute waves' whole launch.
+DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int steps, Lds& L) {
+  const int hidden = M.hidden;
+  const int G = q.Gh;
+  const int pos0 = *M.position;
+  wait_vm<0>();
+  // the weight stream starts with layer 0's input projection
+  Stream st;
+  st.wp = nullptr;
+  st.sp = nullptr;
+  st.g = st.ng = st.wjump = st.left = 0;
+  st.issued = st.consumed = st.wslot = st.rslot = 0;
+  st.li = st.k = st.istep = 0;
+  st.state = kStreaming;
+  seg_open(st, M, q, c, steps);
+  fill(st, M, q, c, steps);
+  auto stop = [&]() { __builtin_amdgcn_s_waitcnt(0); };
+
+  for (int step = 0; step < steps; ++step) {
+    c.pos = pos0 + step;
+    c.nb = 0;
+    fence(c);
+    sync(c);  // embed
+    if (!L.ok) return stop();
+    for (int li = 0; li < M.num_layers; ++li) {
+      LayerPtr Lp = layer_at(M, li);
+      const int kind = Lp->kind;
+      {  // input projection
+        fence(c);
+        const Gemv g = gemv_of(Lp, q, 0, c.xcd, c.r);
+        sync(c);
+        norm_w(L, c, hidden, M.eps);
+        gemv_consume(g, c, st, M, q, steps, L);
+        sync(c);
+      }
+      if (kind == 0) {
+        fence(c);
+        sync(c);  // delta inputs staged
+        if (!L.ok) return stop();
+        dn_compute(c, Lp, L);
+        {  // gated norm + out_proj
+          fence(c);
+          const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
+            sync(c);
+          if (!L.ok) return stop();
+          // GatedRMSNorm per 128-head, one element per thread (a head = 2 waves)
+          const int i = c.tid;
+          const float v = bf2f(g_x[i]);
+          const float ss = wave_sum(v * v);
+          if (c.lane == 0) L.red[c.wave] = ss;
+          sync(c);
+          const int h = i >> 7;
+          const float tot = L.red[2 * h] + L.red[2 * h + 1];
+          const float rr = 1.0f / sqrtf(tot / 128.0f + M.eps);
+          const float t = round_bf(bf2f(L.nw[i & 127]) * round_bf(v * rr));
+          const uint16_t xb = f2bf(t * silu(L.u.on.z[i]));
+          g_x[i] = xb;
+          const float gs = wave_sum(bf2f(xb));
+          if (c.lane == 0) L.red[16 + c.wave] = gs;
+          sync(c);
+          if (c.tid < 4) L.xs[c.tid] = kBias * (L.red[16 + 2 * c.tid] + L.red[16 + 2 * c.tid + 1]);
+          sync(c);
+          gemv_consume(g, c, st, M, q, steps, L);
+          sync(c);
+          sync(c);  // all-reduce done, h in LDS
+          if (!L.ok) return stop();
+        }
+      } else {
+        // attention split
+        fence(c);
+        int j0, j1;
+        at_keys(c, j0, j1);
+        auto& A = L.u.at;
+        sync(c);  // q/k/v staged
+        if (!L.ok) return stop();
+        const float posf = static_cast<float>(c.pos);
+        if (c.wave < 3) {
+          float x[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[i] = c.wave < 2 ? A.qraw[c.wave][c.lane * 4 + i] : A.kraw[c.lane * 4 + i];
+          norm_rope4_lds(x, c.wave < 2 ? A.qn_w : A.kn_w, M.eps, A.inv, posf, c.lane);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (c.wave < 2) A.q[c.wave][c.lane * 4 + i] = f2bf(x[i]);
+            else A.knew[c.lane * 4 + i] = f2bf(x[i]);
+          }
+        } else if (c.wave == 3) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) A.vnew[c.lane * 4 + i] = f2bf(A.vraw[c.lane * 4 + i]);
+        }
+        sync(c);
+        // the even XCD of the pair writes the new key/value (write-through: the odd XCD
+        // reads this row in later steps)
+        if ((c.xcd & 1) == 0 && c.pos >= j0 && c.pos < j1 && c.tid < kHd / 2) {
+          const size_t row = ((size_t)(c.xcd >> 1) * M.max_len + c.pos) * kHd;
+          const uint32_t kw = static_cast<uint32_t>(A.knew[2 * c.tid]) | (static_cast<uint32_t>(A.knew[2 * c.tid + 1]) << 16);
+          const uint32_t vw = static_cast<uint32_t>(A.vnew[2 * c.tid]) | (static_cast<uint32_t>(A.vnew[2 * c.tid + 1]) << 16);
+          st_sys(reinterpret_cast<uint32_t*>(Lp->k_cache + row) + c.tid, kw);
+          st_sys(reinterpret_cast<uint32_t*>(Lp->v_cache + row) + c.tid, vw);
+        }
+        float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        for (int t0 = j0; t0 < j1; t0 += kTileKeys) {
+          // K rows are loaded here, in straight-line code with their use (a prefetch across
+          // the staging barrier leaves the compiler unsure they completed, and it then makes
+          // the weight-stream loops wait for them)
+          AtPre P;
+          at_issue_k(c, Lp, t0, j1, P);
+          at_tile(c, Lp, t0, j1, P, acc, L);
+        }
+        // the split's KV loads are consumed (wait unconditionally: the compiler cannot pair
+        // the first tile's prefetch with the loop, and the held stream has nothing in flight)
+        wait_vm<0>();
+        // the weight stream resumes with o_proj
+        if (st.state == kHeld) {
+          st.state = kReleased;
+          seg_open(st, M, q, c, steps);
+          fill(st, M, q, c, steps);
+        }
+        // combine the waves' PV partials (into wave 0's row)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) A.red[c.wave][hh][c.lane * 4 + i] = acc[hh][i];
+        sync(c);
+        {
+          const int e = c.tid;  // 512 = 2 heads x 256 dims
+          const int hh = e / kHd, d = e % kHd;
+          float sum = 0.0f;
+#pragma unroll
+          for (int wv = 0; wv < kCompute; ++wv) sum += A.red[wv][hh][d];
+          A.red[0][hh][d] = sum;
+        }
+        sync(c);
+        {  // o_proj (the merge runs on the control wave meanwhile)
+          fence(c);
+          const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
+            sync(c);
+          if (!L.ok) return stop();
+          gemv_consume(g, c, st, M, q, steps, L);
+          sync(c);
+          sync(c);  // all-reduce done
+          if (!L.ok) return stop();
+        }
+      }
+      {  // gate|up + SwiGLU
+        fence(c);
+        const Gemv g = gemv_of(Lp, q, 2, c.xcd, c.r);
+        sync(c);
+        norm_w(L, c, hidden, M.eps);
+        gemv_consume(g, c, st, M, q, steps, L);
+        sync(c);
+      }
+      {  // down
+        fence(c);
+        const Gemv g = gemv_of(Lp, q, 3, c.xcd, c.r);
+        sync(c);
+        if (!L.ok) return stop();
+        gemv_consume(g, c, st, M, q, steps, L);
+        sync(c);
+        sync(c);  // all-reduce done
+        if (!L.ok) return stop();
+      }
+    }
+    {  // final norm + tied head
+      fence(c);
+      auto& H = L.hd;
+      sync(c);
+      norm_w(L, c, hidden, M.eps);
+      // tiles t_lo + wave + 8 j, all groups, from the weight stream
+      const int ntw = head_tiles_of_wave(q, c.wave);
+      const uint16_t* xb = g_x + (c.lane >> 4) * 32;
+      float bv = -INFINITY;
+      int bi = 0x7FFFFFFF;
+      float acc = 0.0f;
+      int gl = 0, j = 0;
+      // G is a multiple of 4 (hidden % 512 == 0), so a pair never straddles two tiles
+#pragma unroll 1
+      for (int i = 0; i < ntw * G; i += 2) {
+        uint4 w0, w1;
+        uint32_t s0, s1;
+        take_blocks2(st, c, w0, s0, w1, s1);
+        const float v0 = block_dot(w0, s0, xb + gl * kGroup, L.xs[gl], c.lane);
+        const float v1 = block_dot(w1, s1, xb + (gl + 1) * kGroup, L.xs[gl + 1], c.lane);
+        fill(st, M, q, c, steps);
+        acc += v0;
+        acc += v1;
+        gl += 2;
+        if (gl == G) {  // tile complete: logits of 16 columns in lanes 0..15
+          const int t = q.t_lo + c.wave + j * kCompute;
+          const uint16_t lb = f2bf(acc);
+          if (c.lane < 16) {
+            H.logit[(t - q.t_lo) * 16 + c.lane] = lb;
+            const float lv = bf2f(lb);
+            const int lix = t * 16 + c.lane;
+            if (lv > bv || (lv == bv && lix < bi)) {
+              bv = lv;
+              bi = lix;
+            }
+          }
+          acc = 0.0f;
+          gl = 0;
+          ++j;
+        }
+      }
+      for (int off = 8; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if (c.lane == 0) {
+        H.bv[c.wave] = bv;
+        H.bi[c.wave] = bi;
+      }
+      if (c.tid == 0) L.nbw = c.nb + 2;
+      sync(c);
+      sync(c);  // global argmax done
+      if (!L.ok) return stop();
+    }
+  }
+  stop();
+}
+
+// The control wave's whole launch.
+DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int steps, int teacher_forced, Lds& L) {
+  const int hidden = M.hidden;
+  const int G = q.Gh;
+  const int pos0 = *M.position;
+  const int step0 = M.step ? *M.step : 0;
+  int64_t token = M.tokens[0];
+  auto fail = [&](int nbars) {  // pass the barriers the compute waves still wait at, then stop
+    if (c.lane == 0) L.ok = 0;
+    for (int i = 0; i < nbars; ++i) bar();
+  };
+
+  for (int step = 0; step < steps; ++step) {
+    c.pos = pos0 + step;
+    c.tr = (M.trace && step == M.trace_step) ? M.trace : nullptr;
+    c.tn = 0;
+    c.nb = 0;
+    // ---- embedding of the step's token into L.h ---------------------------------------
+    fence(c, kTEmbed);
+    if (teacher_forced) token = M.prompt[c.pos];
+    if (token < 0 || token >= M.vocab) {
+      if (c.lane == 0 && c.xcd == 0 && c.r == 0) raise_abort(c, kErrToken);
+      return fail(1);
+    }
+    {
+      const int tt = static_cast<int>(token / 16), cc = static_cast<int>(token % 16);
+      const uint32_t* wt = reinterpret_cast<const uint32_t*>(M.head_w);
+      constexpr int K = (kMaxHidden / kGroup * 16 + 63) / 64;
+      uint32_t wd[K];
+      uint16_t sc[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int idx = c.lane + 64 * k;  // idx = g*16 + s*4 + d
+        if (idx < G * 16) {
+          const size_t block = (size_t)tt * G + idx / 16;
+          wd[k] = wt[block * 256 + (((idx / 4) & 3) * 16 + cc) * 4 + (idx & 3)];
+          sc[k] = M.head_s[block * 16 + cc];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int idx = c.lane + 64 * k;
+        if (idx < G * 16) {
+          const int g = idx / 16, s = (idx / 4) & 3, d = idx & 3;
+          const float scv = bf2f(sc[k]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int sh = (e & 1) ? 16 + 4 * (e >> 1) : 4 * (e >> 1);
+            const int qv = static_cast<int>((wd[k] >> sh) & 15u) - 8;
+            L.h[g * 128 + s * 32 + d * 8 + e] = f2bf(static_cast<float>(qv) * scv);
+          }
+        }
+      }
+    }
+    if (c.lane == 0) L.ok = 1;
+    sync(c);
+
+    for (int li = 0; li < M.num_layers; ++li) {
+      LayerPtr Lp = layer_at(M, li);
+      const int kind = Lp->kind;
+      // ================= input projection (column-parallel) =========================
+      {
+        fence(c, kTProj);
+        const Gemv g = gemv_of(Lp, q, 0, c.xcd, c.r);
+        stage16<kHidChunks, kCpPlain>(L.nw, Lp->in_norm, hidden, c.lane);  // h is already in LDS
+        sync(c);
+        for (int i = 0; i < kNormBars; ++i) sync(c);
+        sync(c);  // blocks consumed
+        c.epoch += 1;
+        colpar_epilogue(g, c, L);
+        signal_local(c, c.epoch);
+      }
+      if (kind == 0) {
+        // ================= conv + gated delta step ===================================
+        fence(c, kTDelta);
+        const bool ok = dn_stage(c, Lp, L);
+        if (!ok) return fail(1);
+        sync(c);
+        stamp(c, kTStaged);
+        for (int i = 0; i < kDnBars; ++i) sync(c);
+        c.epoch += 1;
+        {
+          const int hvl = c.r >> 3, vs = c.r & 7;
+          if (c.lane < 16) c.w.core[(size_t)c.xcd * 512 + hvl * kDk + vs * 16 + c.lane] = L.u.dn.core[c.lane];
+        }
+        signal_local(c, c.epoch);
+        // ================= gated norm + out_proj (row-parallel) ======================
+        {
+          fence(c, kTOut);
+          const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
+          if (!wait_local(c, c.epoch)) return fail(1);
+          // core (512) and z (512) of the XCD's four value heads
+          stage16<1, kCpAgent>(g_x, c.w.core + (size_t)c.xcd * 512, 512, c.lane);
+          const Seg seg[1] = {{kLinZ, 512, L.u.on.z}};
+          gather_colpar<1, 2>(c, seg);
+          stage16<1, kCpPlain>(L.nw, Lp->gnorm_w, kDk, c.lane);
+          sync(c);
+          stamp(c, kTStaged);
+          sync(c);
+          sync(c);
+          sync(c);  // g_x, group sums
+          sync(c);  // blocks consumed
+          rowpar_epilogue(g, c, L, hidden);
+          if (!allreduce_residual(c, L, hidden)) return fail(1);
+          sync(c);
+        }
+      } else {
+        // ================= attention split ===========================================
+        fence(c, kTAttn);
+        auto& A = L.u.at;
+        if (!wait_local(c, c.epoch)) return fail(1);
+        {
+          const Seg seg[3] = {{0, kHd, A.qraw[0]}, {512, kHd, A.qraw[1]}, {kAttnK, 2 * kHd, A.kraw}};
+          gather_colpar<3, 4>(c, seg);  // kraw and vraw are adjacent in LDS
+          stage16<1, kCpPlain>(A.qn_w, Lp->q_norm, kHd, c.lane);
+          stage16<1, kCpPlain>(A.kn_w, Lp->k_norm, kHd, c.lane);
+          if (c.lane < kRot / 2) A.inv[c.lane] = M.inv_freq[c.lane];
+          if (c.lane < 2) {
+            A.ml[c.lane][0] = -INFINITY;
+            A.ml[c.lane][1] = 0.0f;
+          }
+        }
+        sync(c);
+        stamp(c, kTStaged);
+        sync(c);  // q/k normed and roped
+        int j0, j1;
+        at_keys(c, j0, j1);
+        for (int t0 = j0; t0 < j1; t0 += kTileKeys)
+          for (int i = 0; i < kTileBars; ++i) sync(c);
+        sync(c);
+        sync(c);  // PV partials summed into A.red[0]
+        c.epoch += 1;
+        {
+          float* ap = c.w.apart + ((size_t)c.xcd * kPerXcd + c.r) * 2 * kApHead;
+          for (int e = c.lane; e < 2 * kHd; e += 64) ap[(e / kHd) * kApHead + e % kHd] = A.red[0][e / kHd][e % kHd];
+          if (c.lane < 2) {
+            ap[c.lane * kApHead + kHd] = A.ml[c.lane][0];
+            ap[c.lane * kApHead + kHd + 1] = A.ml[c.lane][1];
+          }
+        }
+        signal_local(c, c.epoch);
+        // ================= merge the 32 splits: head r/16, dims 16 (r%16) ..+15 =======
+        {
+          fence(c, kTMerge);
+          auto& Mg = L.u.mg;
+          const int hl = c.r >> 4, d0 = (c.r & 15) * 16;
+          if (!wait_local(c, c.epoch)) return fail(1);
+          c.epoch += 1;
+          // split s: (m, l) of head hl and its accumulator dims d0 .. d0+15 (4 chunks)
+          const float* ap = c.w.apart + (size_t)c.xcd * kPerXcd * 2 * kApHead + hl * kApHead;
+          const auto r = rsrc(ap);
+          uint64_t ml = 0;
+          uint4 av[2];
+          if (c.lane < kPerXcd) ml = ld8<kCpAgent>(r, (c.lane * 2 * kApHead + kHd) * 4);
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const int ch = c.lane + 64 * k;  // 128 chunks: split ch / 4, dims 4 (ch % 4)
+            av[k] = ld16<kCpAgent>(r, ((ch / 4) * 2 * kApHead + d0 + 4 * (ch % 4)) * 4);
+          }
+          const Seg seg[1] = {{hl * 512 + kHd + d0, 16, Mg.gate}};
+          gather_colpar<1, 1>(c, seg);
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const int ch = c.lane + 64 * k;
+            *reinterpret_cast<uint4*>(&Mg.acc[ch / 4][4 * (ch % 4)]) = av[k];
+          }
+          stamp(c, kTStaged);
+          const float m = __uint_as_float(static_cast<uint32_t>(ml));
+          const float l = __uint_as_float(static_cast<uint32_t>(ml >> 32));
+          const float mm = c.lane < kPerXcd && l > 0.0f ? m : -INFINITY;
+          const float mstar = wave_max(mm);
+          const float wgt = mm == -INFINITY ? 0.0f : expf(mm - mstar);
+          const float den = wave_sum(c.lane < kPerXcd ? wgt * l : 0.0f);
+          if (c.lane < kPerXcd) Mg.wgt[c.lane] = wgt;
+          if (c.lane < 16) {
+            float num = 0.0f;
+            for (int sp = 0; sp < kPerXcd; ++sp) num += Mg.wgt[sp] * Mg.acc[sp][c.lane];
+            const float o = round_bf(num / den);
+            const float gx = Mg.gate[c.lane];
+            const float gate = round_bf(M.gate_kind == 0 ? sigmoid(gx) : silu(gx));
+            c.w.core[(size_t)c.xcd * 512 + hl * kHd + d0 + c.lane] = f2bf(o * gate);
+          }
+          signal_local(c, c.epoch);
+        }
+        // ================= o_proj (row-parallel) =====================================
+        {
+          fence(c, kTOProj);
+          const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
+          if (!wait_local(c, c.epoch)) return fail(1);
+          stage16<1, kCpAgent>(g_x, c.w.core + (size_t)c.xcd * 512, 512, c.lane);
+          group_sums(L, c, 4);
+          sync(c);
+          stamp(c, kTStaged);
+          sync(c);  // blocks consumed
+          rowpar_epilogue(g, c, L, hidden);
+          if (!allreduce_residual(c, L, hidden)) return fail(1);
+          sync(c);
+        }
+      }
+      // ================= gate|up + SwiGLU (column-parallel) ============================
+      {
+        fence(c, kTGateUp);
+        const Gemv g = gemv_of(Lp, q, 2, c.xcd, c.r);
+        stage16<kHidChunks, kCpPlain>(L.nw, Lp->post_norm, hidden, c.lane);
+        sync(c);
+        for (int i = 0; i < kNormBars; ++i) sync(c);
+        sync(c);  // blocks consumed
+        c.epoch += 1;
+        colpar_epilogue(g, c, L);
+        signal_local(c, c.epoch);
+      }
+      // ================= down (row-parallel) ===========================================
+      {
+        fence(c, kTDown);
+        const Gemv g = gemv_of(Lp, q, 3, c.xcd, c.r);
+        if (!wait_local(c, c.epoch)) return fail(1);
+        stage_act<(kColparMax / 4 + 63) / 64>(c, q.inter_x);
+        group_sums(L, c, q.ngx);
+        sync(c);
+        stamp(c, kTStaged);
+        sync(c);  // blocks consumed
+        rowpar_epilogue(g, c, L, hidden);
+        if (!allreduce_residual(c, L, hidden)) return fail(1);
+        sync(c);
+      }
+    }
+
+    // ================= final norm + tied head + argmax =================================
+    {
+      fence(c, kTHead);
+      auto& H = L.hd;
+      stage16<kHidChunks, kCpPlain>(L.nw, M.final_norm, hidden, c.lane);
+      sync(c);
+      for (int i = 0; i < kNormBars; ++i) sync(c);
+      sync(c);  // head blocks consumed, per-wave candidates in LDS
+      c.epoch += 1;
+      // logits out (this workgroup's columns, 32 B per tile)
+      if (M.logits) {
+        const int chunks = (q.t_hi - q.t_lo) * 2;
+        for (int e = c.lane; e < chunks; e += 64)
+          *reinterpret_cast<uint4*>(M.logits + (size_t)q.t_lo * 16 + e * 8) = *reinterpret_cast<const uint4*>(&H.logit[e * 8]);
+      }
+      // this workgroup's candidate: one atomic word of value, 18-bit index and the epoch's
+      // low 14 bits (a slot is rewritten once per token, so its previous epoch differs by
+      // the phases per token)
+      if (c.lane == 0) {
+        float v = H.bv[0];
+        int i = H.bi[0];
+        for (int wv = 1; wv < kCompute; ++wv) {
+          if (H.bv[wv] > v || (H.bv[wv] == v && H.bi[wv] < i)) {
+            v = H.bv[wv];
+            i = H.bi[wv];
+          }
+        }
+        st_sys(reinterpret_cast<uint64_t*>(c.w.cand) + blockIdx.x, pack_cand(v, i, c.epoch));
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      // every workgroup reduces the 256 candidates
+      const auto r = rsrc(c.w.cand);
+      uint64_t v[kNwg / 64];
+      bool ok = true;
+      const uint64_t t0 = now();
+      for (;;) {
+#pragma unroll
+        for (int k = 0; k < kNwg / 64; ++k) v[k] = ld8<kCpSystem>(r, (c.lane + 64 * k) * 8);
+        bool ready = true;
+#pragma unroll
+        for (int k = 0; k < kNwg / 64; ++k) ready = ready && (static_cast<uint32_t>(v[k]) & 0x3FFFu) == (c.epoch & 0x3FFFu);
+        if (__all(ready)) break;
+        if (ld_sys(c.w.ctl + 1)) { ok = false; break; }
+        if (now() - t0 > kTimeout) { raise_abort(c, kErrTimeout); ok = false; break; }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      float bv = -INFINITY;
+      int bi = 0x7FFFFFFF;
+#pragma unroll
+      for (int k = 0; k < kNwg / 64; ++k) {
+        const float cv = __uint_as_float(static_cast<uint32_t>(v[k] >> 32));
+        const int ci = static_cast<int>((static_cast<uint32_t>(v[k]) >> 14) & 0x3FFFFu);
+        if (cv > bv || (cv == bv && ci < bi)) {
+          bv = cv;
+          bi = ci;
+        }
+      }
+      for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      // the barrier schedules of the two roles must agree (compute waves recorded theirs)
+      if (ok && L.nbw != c.nb + 1) {
+        raise_abort(c, kErrSchedule);
+        ok = false;
+      }
+      if (c.lane == 0) L.ok = ok;
+      sync(c);
+      if (!ok) return;
+      token = bi;
+      if (c.lane == 0 && c.xcd == 0 && c.r == 0 && !teacher_forced && M.token_log) M.token_log[step0 + step] = token;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  if (c.lane == 0 && c.xcd == 0 && c.r == 0) {
+    M.tokens[0] = token;
+    *M.position = pos0 + steps;
+    if (M.step && !teacher_forced) *M.step = step0 + steps;
+    c.w.ctl[0] = static_cast<int>(c.epoch);
+  }
+}
 
 __global__ __launch_bounds__(kThreads) void decode_kernel(DfPersistModel M, Ws w, int steps, int teacher_forced) {
   __shared__ Lds L;
   Ctx c;
-  c.M = M;
   c.w = w;
   c.ar = 0;
-  const int hidden = M.hidden;
-  const int G = hidden / kGroup;
+  c.nb = 0;
+  c.tcap = M.trace_capacity;
+  c.max_len = M.max_len;
+  c.tr = nullptr;
+  c.tn = 0;
 
   // Role = (XCD this workgroup runs on, its ticket among that XCD's workgroups). The
   // dispatcher spreads a launch round-robin over the XCDs but not from XCD 0 every time,
@@ -951,12 +1869,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DfPersistModel M, Ws w
   if (!L.ok) return;
   c.xcd = L.token / kPerXcd;
   c.r = L.token % kPerXcd;
-  c.tr = nullptr;
-  c.tn = 0;
   fence(c);
-  __syncthreads();
-  const uint32_t epoch0 = static_cast<uint32_t>(w.ctl[0]);
-  c.epoch = epoch0;
+  c.epoch = static_cast<uint32_t>(w.ctl[0]);
   const int pos0 = *M.position;
   const int step0 = M.step ? *M.step : 0;
   if (pos0 < 0 || pos0 + steps > M.max_len || (teacher_forced && pos0 + steps > M.prompt_len) ||
@@ -964,505 +1878,24 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DfPersistModel M, Ws w
     if (c.tid == 0 && c.xcd == 0 && c.r == 0) raise_abort(c, kErrPosition);
     return;
   }
-  int64_t token = M.tokens[0];
 
-  // per-XCD geometry of the phases
-  const int inter_x = M.inter / kXcd;                  // intermediate channels per XCD
-  const int gu_tiles = 2 * inter_x / kTileCols;         // gate|up tiles per XCD
-  const int row_tiles = hidden / kTileCols;             // output tiles of row-parallel GEMVs
-  const int rp_lo = (c.r * row_tiles) / kPerXcd, rp_hi = ((c.r + 1) * row_tiles) / kPerXcd;
+  Geo q;
+  q.hidden = M.hidden;
+  q.Gh = M.hidden / kGroup;
+  q.inter = M.inter;
+  q.inter_x = M.inter / kXcd;
+  q.gu_tiles = 2 * q.inter_x / kTileCols;
+  const int row_tiles = M.hidden / kTileCols;
+  q.rp_lo = (c.r * row_tiles) / kPerXcd;
+  q.rp_hi = ((c.r + 1) * row_tiles) / kPerXcd;
+  q.ngx = q.inter_x / kGroup;
   const int vocab_tiles = M.vocab / kTileCols / kXcd;
+  q.t_lo = c.xcd * vocab_tiles + (c.r * vocab_tiles) / kPerXcd;
+  q.t_hi = c.xcd * vocab_tiles + ((c.r + 1) * vocab_tiles) / kPerXcd;
+  __syncthreads();  // everyone has read the registration before L.token is reused
 
-  for (int step = 0; step < steps; ++step) {
-    c.pos = pos0 + step;
-    c.tr = (M.trace && step == M.trace_step) ? M.trace : nullptr;
-    c.tn = 0;
-    // ---- embedding of the step's token (every workgroup, into L.h) --------------------
-    fence(c, kTEmbed);
-    if (teacher_forced) token = M.prompt[c.pos];
-    if (token < 0 || token >= M.vocab) {
-      if (c.tid == 0 && c.xcd == 0 && c.r == 0) raise_abort(c, kErrToken);
-      return;
-    }
-    {
-      const int tt = static_cast<int>(token / 16), cc = static_cast<int>(token % 16);
-      const uint32_t* wt = reinterpret_cast<const uint32_t*>(M.head_w);
-      for (int idx = c.tid; idx < G * 16; idx += kThreads) {  // idx = g*16 + s*4 + d
-        const int g = idx / 16, s = (idx / 4) & 3, d = idx & 3;
-        const size_t block = (size_t)tt * G + g;
-        const uint32_t word = wt[block * 256 + (s * 16 + cc) * 4 + d];
-        const float sc = bf2f(M.head_s[block * 16 + cc]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int sh = (e & 1) ? 16 + 4 * (e >> 1) : 4 * (e >> 1);
-          const int q = static_cast<int>((word >> sh) & 15u) - 8;
-          L.h[g * 128 + s * 32 + d * 8 + e] = f2bf(static_cast<float>(q) * sc);
-        }
-      }
-    }
-    __syncthreads();
-
-    for (int li = 0; li < M.num_layers; ++li) {
-      const DfPersistLayer Lr = M.layers[li];
-      // ================= input projection (column-parallel) =========================
-      {
-        fence(c, kTProj);
-        const int cols = Lr.kind == 0 ? kLinCols : kAttnCols;
-        const int nt = cols / kTileCols;
-        Gemv g{Lr.proj_w, Lr.proj_s, G, c.xcd * nt, 0, G, 0, 0};
-        const int B = nt * G;
-        g.b_lo = (c.r * B) / kPerXcd;
-        g.b_hi = ((c.r + 1) * B) / kPerXcd;
-        WaveBlocks wb;
-        if (!c.control) gemv_issue(g, c, wb, L);
-        else stage16<kHidChunks, kCpPlain>(L.nw, Lr.in_norm, hidden, c.lane);  // h is already in LDS
-        zero_part(L, c);
-        __syncthreads();
-        norm_prologue(L, c, hidden, M.eps);
-        if (!c.control) gemv_compute(g, c, wb, L);
-        __syncthreads();
-        colpar_epilogue(g, c, L);
-        c.epoch += 1;
-        signal_local(c, c.epoch);
-      }
-      if (Lr.kind == 0) {
-        // ================= conv + gated delta step ===================================
-        fence(c, kTDelta);
-        DnPre P;
-        if (!c.control) dn_issue(c, Lr, P);
-        if (c.control) {
-          bool ok = wait_local(c, c.epoch);
-          if (ok) {
-            const int hvl = c.r >> 3, vs = c.r & 7, khl = hvl >> 1;
-            const Seg seg[4] = {{kLinQ + khl * 128, 128, L.u.dn.qkv_in},
-                                {kLinK + khl * 128, 128, L.u.dn.qkv_in + 128},
-                                {kLinV + hvl * 128 + vs * 16, 16, L.u.dn.qkv_in + 256},
-                                {kLinA, 8, L.u.dn.ab8}};
-            gather_colpar<4, 2>(c, seg);
-          }
-          if (c.lane == 0) L.ok = ok;
-        }
-        __syncthreads();
-        if (!L.ok) return;
-        stamp(c, kTStaged);
-        dn_compute(c, Lr, P, L);
-        c.epoch += 1;
-        signal_local(c, c.epoch);
-        // ================= gated norm + out_proj (row-parallel) ======================
-        {
-          fence(c, kTOut);
-          Gemv g{Lr.out_w, Lr.out_s, 4096 / kGroup, 0, c.xcd * 4, 4, 0, 0};
-          g.b_lo = rp_lo * 4;
-          g.b_hi = rp_hi * 4;
-          WaveBlocks wb;
-          if (!c.control) gemv_issue(g, c, wb, L);
-          if (c.control) {
-            bool ok = wait_local(c, c.epoch);
-            if (ok) {
-              // core (512) and z (512) of the XCD's four value heads
-              stage16<1, kCpAgent>(L.x[0], c.w.core + (size_t)c.xcd * 512, 512, c.lane);
-              const Seg seg[1] = {{kLinZ, 512, L.gated_z}};
-              gather_colpar<1, 2>(c, seg);
-              stage16<1, kCpPlain>(L.nw, Lr.gnorm_w, kDk, c.lane);
-            }
-            if (c.lane == 0) L.ok = ok;
-          }
-          zero_part(L, c);
-          __syncthreads();
-          if (!L.ok) return;
-          stamp(c, kTStaged);
-          // GatedRMSNorm per 128-head: 8 elements per thread of the first 64 threads of
-          // each of waves 0..3 is simpler as one element per thread over 512 threads.
-          {
-            const int i = c.tid;  // 0..575; 512 elements
-            float v = 0.f;
-            if (i < 512) v = bf2f(L.x[0][i]);
-            float ss = v * v;
-            // a head is 128 consecutive elements = 2 waves; reduce within each wave, then pair
-            ss = wave_sum(ss);
-            if (c.lane == 0) L.red[c.wave] = ss;
-            __syncthreads();
-            if (i < 512) {
-              const int h = i >> 7;
-              const float tot = L.red[2 * h] + L.red[2 * h + 1];
-              const float rr = 1.0f / sqrtf(tot / 128.0f + M.eps);
-              const float t = round_bf(bf2f(L.nw[i & 127]) * round_bf(v * rr));
-              L.x[0][i] = f2bf(t * silu(L.gated_z[i]));
-              L.x[1][i] = 0;
-            }
-            __syncthreads();
-          }
-          if (!c.control) gemv_compute(g, c, wb, L);
-          __syncthreads();
-          c.epoch += 1;
-          rowpar_epilogue(g, c, L, hidden);
-          if (!allreduce_residual(c, L, hidden)) return;
-        }
-      } else {
-        // ================= attention split ===========================================
-        fence(c, kTAttn);
-        int j0, j1;
-        at_keys(c, j0, j1);
-        AtPre P;
-        if (!c.control && j0 < j1) at_issue_tile(c, Lr, j0, j1, P);
-        auto& A = L.u.at;
-        if (c.control) {
-          bool ok = wait_local(c, c.epoch);
-          if (ok) {
-            const Seg seg[3] = {{0, kHd, A.qraw[0]}, {512, kHd, A.qraw[1]}, {kAttnK, 2 * kHd, A.kraw}};
-            gather_colpar<3, 4>(c, seg);  // kraw and vraw are adjacent in LDS
-            stage16<1, kCpPlain>(A.qn_w, Lr.q_norm, kHd, c.lane);
-            stage16<1, kCpPlain>(A.kn_w, Lr.k_norm, kHd, c.lane);
-            if (c.lane < kRot / 2) A.inv[c.lane] = M.inv_freq[c.lane];
-            if (c.lane < 2) {
-              A.ml[c.lane][0] = -INFINITY;
-              A.ml[c.lane][1] = 0.0f;
-            }
-          }
-          if (c.lane == 0) L.ok = ok;
-        }
-        __syncthreads();
-        if (!L.ok) return;
-        stamp(c, kTStaged);
-        const float posf = static_cast<float>(c.pos);
-        if (c.wave < 3) {
-          float x[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) x[i] = c.wave < 2 ? A.qraw[c.wave][c.lane * 4 + i] : A.kraw[c.lane * 4 + i];
-          norm_rope4_lds(x, c.wave < 2 ? A.qn_w : A.kn_w, M.eps, A.inv, posf, c.lane);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            if (c.wave < 2) A.q[c.wave][c.lane * 4 + i] = f2bf(x[i]);
-            else A.knew[c.lane * 4 + i] = f2bf(x[i]);
-          }
-        } else if (c.wave == 3) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) A.vnew[c.lane * 4 + i] = f2bf(A.vraw[c.lane * 4 + i]);
-        }
-        __syncthreads();
-        // the even XCD of the pair writes the new key/value (write-through: the odd XCD
-        // reads this row in later steps)
-        if ((c.xcd & 1) == 0 && c.pos >= j0 && c.pos < j1 && c.tid < kHd / 2) {
-          const size_t row = ((size_t)(c.xcd >> 1) * M.max_len + c.pos) * kHd;
-          const uint32_t kw = static_cast<uint32_t>(A.knew[2 * c.tid]) | (static_cast<uint32_t>(A.knew[2 * c.tid + 1]) << 16);
-          const uint32_t vw = static_cast<uint32_t>(A.vnew[2 * c.tid]) | (static_cast<uint32_t>(A.vnew[2 * c.tid + 1]) << 16);
-          st_sys(reinterpret_cast<uint32_t*>(Lr.k_cache + row) + c.tid, kw);
-          st_sys(reinterpret_cast<uint32_t*>(Lr.v_cache + row) + c.tid, vw);
-        }
-        float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        float m_run = -INFINITY, l_run = 0.f;
-        for (int t0 = j0; t0 < j1; t0 += kTileKeys) {
-          if (t0 != j0 && !c.control) at_issue_tile(c, Lr, t0, j1, P);
-          at_tile(c, t0, j1, P, acc, m_run, l_run, L);
-        }
-        // combine the waves' PV partials; publish (acc, m, l) of both heads
-        if (!c.control) {
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) A.red[c.wave][h][c.lane * 4 + i] = acc[h][i];
-        }
-        __syncthreads();
-        {
-          float* ap = c.w.apart + ((size_t)c.xcd * kPerXcd + c.r) * 2 * kApHead;
-          for (int e = c.tid; e < 2 * kHd; e += kThreads) {
-            const int h = e / kHd, d = e % kHd;
-            float s = 0.0f;
-#pragma unroll
-            for (int wv = 0; wv < kCompute; ++wv) s += A.red[wv][h][d];
-            ap[h * kApHead + d] = s;
-          }
-          if (c.tid < 2) {
-            ap[c.tid * kApHead + kHd] = A.ml[c.tid][0];
-            ap[c.tid * kApHead + kHd + 1] = A.ml[c.tid][1];
-          }
-        }
-        c.epoch += 1;
-        signal_local(c, c.epoch);
-        // ================= merge the 32 splits: head r/16, dims 16 (r%16) ..+15 =======
-        {
-          fence(c, kTMerge);
-          auto& Mg = L.u.mg;
-          const int hl = c.r >> 4, d0 = (c.r & 15) * 16;
-          if (c.control) {
-            bool ok = wait_local(c, c.epoch);
-            if (ok) {
-              // split s: (m, l) of head hl and its accumulator dims d0 .. d0+15 (4 chunks)
-              const float* ap = c.w.apart + (size_t)c.xcd * kPerXcd * 2 * kApHead + hl * kApHead;
-              const auto r = rsrc(ap);
-              uint64_t ml = 0;
-              uint4 av[2];
-              if (c.lane < kPerXcd) ml = ld8<kCpAgent>(r, (c.lane * 2 * kApHead + kHd) * 4);
-#pragma unroll
-              for (int k = 0; k < 2; ++k) {
-                const int ch = c.lane + 64 * k;  // 128 chunks: split ch / 4, dims 4 (ch % 4)
-                av[k] = ld16<kCpAgent>(r, ((ch / 4) * 2 * kApHead + d0 + 4 * (ch % 4)) * 4);
-              }
-              if (c.lane < kPerXcd) {
-                Mg.m[c.lane] = __uint_as_float(static_cast<uint32_t>(ml));
-                Mg.l[c.lane] = __uint_as_float(static_cast<uint32_t>(ml >> 32));
-              }
-#pragma unroll
-              for (int k = 0; k < 2; ++k) {
-                const int ch = c.lane + 64 * k;
-                *reinterpret_cast<uint4*>(&Mg.acc[ch / 4][4 * (ch % 4)]) = av[k];
-              }
-              const Seg seg[1] = {{hl * 512 + kHd + d0, 16, Mg.gate}};
-              gather_colpar<1, 1>(c, seg);
-            }
-            if (c.lane == 0) L.ok = ok;
-          }
-          __syncthreads();
-          if (!L.ok) return;
-          stamp(c, kTStaged);
-          if (c.wave == 0) {
-            const float mm = c.lane < kPerXcd && Mg.l[c.lane] > 0.0f ? Mg.m[c.lane] : -INFINITY;
-            const float mstar = wave_max(mm);
-            const float wgt = mm == -INFINITY ? 0.0f : expf(mm - mstar);
-            const float den = wave_sum(c.lane < kPerXcd ? wgt * Mg.l[c.lane] : 0.0f);
-            if (c.lane < kPerXcd) Mg.wgt[c.lane] = wgt;
-            if (c.lane == 0) Mg.den = den;
-          }
-          __syncthreads();
-          if (c.tid < 16) {
-            float num = 0.0f;
-            for (int s = 0; s < kPerXcd; ++s) num += Mg.wgt[s] * Mg.acc[s][c.tid];
-            const float o = round_bf(num / Mg.den);
-            const float gx = Mg.gate[c.tid];
-            const float gate = round_bf(M.gate_kind == 0 ? sigmoid(gx) : silu(gx));
-            c.w.core[(size_t)c.xcd * 512 + hl * kHd + d0 + c.tid] = f2bf(o * gate);
-          }
-          c.epoch += 1;
-          signal_local(c, c.epoch);
-        }
-        // ================= o_proj (row-parallel) =====================================
-        {
-          fence(c, kTOProj);
-          Gemv g{Lr.out_w, Lr.out_s, 4096 / kGroup, 0, c.xcd * 4, 4, 0, 0};
-          g.b_lo = rp_lo * 4;
-          g.b_hi = rp_hi * 4;
-          WaveBlocks wb;
-          if (!c.control) gemv_issue(g, c, wb, L);
-          if (c.control) {
-            bool ok = wait_local(c, c.epoch);
-            if (ok) stage16<1, kCpAgent>(L.x[0], c.w.core + (size_t)c.xcd * 512, 512, c.lane);
-            if (c.lane == 0) L.ok = ok;
-          }
-          zero_part(L, c);
-          for (int i = c.tid; i < 512; i += kThreads) L.x[1][i] = 0;
-          __syncthreads();
-          if (!L.ok) return;
-          stamp(c, kTStaged);
-          if (!c.control) gemv_compute(g, c, wb, L);
-          __syncthreads();
-          c.epoch += 1;
-          rowpar_epilogue(g, c, L, hidden);
-          if (!allreduce_residual(c, L, hidden)) return;
-        }
-      }
-      // ================= gate|up + SwiGLU (column-parallel) ============================
-      {
-        fence(c, kTGateUp);
-        Gemv g{Lr.gu_w, Lr.gu_s, G, c.xcd * gu_tiles, 0, G, 0, 0};
-        const int B = gu_tiles * G;
-        g.b_lo = (c.r * B) / kPerXcd;
-        g.b_hi = ((c.r + 1) * B) / kPerXcd;
-        WaveBlocks wb;
-        if (!c.control) gemv_issue(g, c, wb, L);
-        else stage16<kHidChunks, kCpPlain>(L.nw, Lr.post_norm, hidden, c.lane);
-        zero_part(L, c);
-        __syncthreads();
-        norm_prologue(L, c, hidden, M.eps);
-        if (!c.control) gemv_compute(g, c, wb, L);
-        __syncthreads();
-        colpar_epilogue(g, c, L);
-        c.epoch += 1;
-        signal_local(c, c.epoch);
-      }
-      // ================= down (row-parallel) ===========================================
-      {
-        fence(c, kTDown);
-        const int ngx = inter_x / kGroup;
-        Gemv g{Lr.down_w, Lr.down_s, M.inter / kGroup, 0, c.xcd * ngx, ngx, 0, 0};
-        g.b_lo = rp_lo * ngx;
-        g.b_hi = rp_hi * ngx;
-        WaveBlocks wb;
-        if (!c.control) gemv_issue(g, c, wb, L);
-        if (c.control) {
-          bool ok = wait_local(c, c.epoch);
-          if (ok) stage_act<(kColparMax / 4 + 63) / 64>(c, inter_x, L);
-          if (c.lane == 0) L.ok = ok;
-        }
-        zero_part(L, c);
-        for (int i = c.tid; i < inter_x; i += kThreads) L.x[1][i] = 0;
-        __syncthreads();
-        if (!L.ok) return;
-        stamp(c, kTStaged);
-        if (!c.control) gemv_compute(g, c, wb, L);
-        __syncthreads();
-        c.epoch += 1;
-        rowpar_epilogue(g, c, L, hidden);
-        if (!allreduce_residual(c, L, hidden)) return;
-      }
-    }
-
-    // ================= final norm + tied head + argmax =================================
-    {
-      fence(c, kTHead);
-      const int t_lo = c.xcd * vocab_tiles + (c.r * vocab_tiles) / kPerXcd;
-      const int t_hi = c.xcd * vocab_tiles + ((c.r + 1) * vocab_tiles) / kPerXcd;
-      auto& H = L.hd;
-      // Compute waves own whole tiles t_lo + wave + 8 j; their (tile, group) blocks form one
-      // stream through an 8-block LDS ring (LDS DMA), the first 8 requested before the norm.
-      const int ntw = c.control ? 0 : (t_hi - t_lo - c.wave + kCompute - 1) / kCompute;
-      const int nblk = ntw > 0 ? ntw * G : 0;
-      auto blk_idx = [&](int q) -> size_t {
-        const int t = t_lo + c.wave + (q / G) * kCompute;
-        return (size_t)t * G + q % G;
-      };
-      if (!c.control) {
-#pragma unroll 1
-        for (int u = 0; u < kDepthH && u < nblk; ++u) dma_block(M.head_w, M.head_s, blk_idx(u), c.wave, u, c.lane, L);
-      } else {
-        stage16<kHidChunks, kCpPlain>(L.nw, M.final_norm, hidden, c.lane);
-      }
-      __syncthreads();
-      norm_prologue(L, c, hidden, M.eps);
-      float bv = -INFINITY;
-      int bi = 0x7FFFFFFF;
-      if (!c.control) {
-        const int col = c.lane & 15, slot = c.lane >> 4;
-        const uint16_t* xrow = &L.x[col == 0 ? 0 : 1][slot * 32];
-        df_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int q0 = 0; q0 < nblk; q0 += kDepthH) {
-#pragma unroll
-          for (int u = 0; u < kDepthH; ++u) {
-            const int q = q0 + u;
-            if (q < nblk) {
-              // block q has landed once at most the 7 later blocks (weights + scales each)
-              // are still in flight; near the end of the stream, wait for everything
-              if (q + kDepthH - 1 < nblk) wait_vm<2 * (kDepthH - 1)>();
-              else wait_vm<0>();
-              const uint4 wv = L.u.wq.wblk[c.wave][u][c.lane];
-              const uint16_t sv = block_scale(L, c.wave, u, c.lane);
-              const int gl = q % G;
-              const GroupScale gs = group_scale(sv);
-              const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
-              df_f32x4 a2 = acc;
-#pragma unroll
-              for (int d = 0; d < 4; ++d) {
-                const uint4 bw = dequant8(words[d], gs);
-                const uint4 aw = *reinterpret_cast<const uint4*>(xrow + gl * kGroup + d * 8);
-                a2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, aw),
-                                                             __builtin_bit_cast(df_bf16x8, bw), a2, 0, 0, 0);
-              }
-              acc = a2;
-              const int qn = q + kDepthH;
-              if (qn < nblk) dma_block(M.head_w, M.head_s, blk_idx(qn), c.wave, u, c.lane, L);  // refill the slot
-              if (gl == G - 1) {  // tile complete: logits of 16 columns in lanes 0..15
-                const int t = t_lo + c.wave + (q / G) * kCompute;
-                const uint16_t lb = f2bf(acc[0]);
-                if (c.lane < 16) {
-                  H.logit[(t - t_lo) * 16 + c.lane] = lb;
-                  const float lv = bf2f(lb);
-                  const int li = t * 16 + c.lane;
-                  if (lv > bv || (lv == bv && li < bi)) {
-                    bv = lv;
-                    bi = li;
-                  }
-                }
-                acc = df_f32x4{0.f, 0.f, 0.f, 0.f};
-              }
-            }
-          }
-        }
-        for (int off = 8; off > 0; off >>= 1) {
-          const float ov = __shfl_xor(bv, off, 64);
-          const int oi = __shfl_xor(bi, off, 64);
-          if (ov > bv || (ov == bv && oi < bi)) {
-            bv = ov;
-            bi = oi;
-          }
-        }
-        if (c.lane == 0) {
-          H.bv[c.wave] = bv;
-          H.bi[c.wave] = bi;
-        }
-      }
-      __syncthreads();
-      // logits out (this workgroup's columns) and its candidate
-      if (M.logits) {
-        for (int e = c.tid; e < (t_hi - t_lo) * 16; e += kThreads) M.logits[(size_t)t_lo * 16 + e] = H.logit[e];
-      }
-      c.epoch += 1;
-      if (c.tid == 0) {
-        float v = H.bv[0];
-        int i = H.bi[0];
-        for (int wv = 1; wv < kCompute; ++wv) {
-          if (H.bv[wv] > v || (H.bv[wv] == v && H.bi[wv] < i)) {
-            v = H.bv[wv];
-            i = H.bi[wv];
-          }
-        }
-        // one atomic word: value, 18-bit index, the epoch's low 14 bits (a slot is rewritten
-        // once per token, so its previous epoch differs by the phases per token)
-        st_sys(reinterpret_cast<uint64_t*>(w.cand) + blockIdx.x, pack_cand(v, i, c.epoch));
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      // every workgroup reduces the 256 candidates (control wave)
-      if (c.control) {
-        const auto r = rsrc(w.cand);
-        uint64_t v[kNwg / 64];
-        bool ok = true;
-        const uint64_t t0 = now();
-        for (;;) {
-#pragma unroll
-          for (int k = 0; k < kNwg / 64; ++k) v[k] = ld8<kCpSystem>(r, (c.lane + 64 * k) * 8);
-          bool ready = true;
-#pragma unroll
-          for (int k = 0; k < kNwg / 64; ++k) ready = ready && (static_cast<uint32_t>(v[k]) & 0x3FFFu) == (c.epoch & 0x3FFFu);
-          if (__all(ready)) break;
-          if (ld_sys(w.ctl + 1)) { ok = false; break; }
-          if (now() - t0 > kTimeout) { raise_abort(c, kErrTimeout); ok = false; break; }
-          __builtin_amdgcn_s_sleep(1);
-        }
-        float bv = -INFINITY;
-        int bi = 0x7FFFFFFF;
-#pragma unroll
-        for (int k = 0; k < kNwg / 64; ++k) {
-          const float cv = __uint_as_float(static_cast<uint32_t>(v[k] >> 32));
-          const int ci = static_cast<int>((static_cast<uint32_t>(v[k]) >> 14) & 0x3FFFFu);
-          if (cv > bv || (cv == bv && ci < bi)) {
-            bv = cv;
-            bi = ci;
-          }
-        }
-        for (int off = 32; off > 0; off >>= 1) {
-          const float ov = __shfl_xor(bv, off, 64);
-          const int oi = __shfl_xor(bi, off, 64);
-          if (ov > bv || (ov == bv && oi < bi)) {
-            bv = ov;
-            bi = oi;
-          }
-        }
-        if (c.lane == 0) {
-          L.ok = ok;
-          L.token = bi;
-        }
-      }
-      __syncthreads();
-      if (!L.ok) return;
-      token = L.token;
-      if (c.xcd == 0 && c.r == 0 && c.tid == 0 && !teacher_forced && M.token_log) M.token_log[step0 + step] = token;
-    }
-  }
-  if (c.xcd == 0 && c.r == 0 && c.tid == 0) {
-    M.tokens[0] = token;
-    *M.position = pos0 + steps;
-    if (M.step && !teacher_forced) *M.step = step0 + steps;
-    w.ctl[0] = static_cast<int>(c.epoch);
-  }
+  if (c.control) control_main(M, q, c, steps, teacher_forced, L);
+  else compute_main(M, q, c, steps, L);
 }
 
 __global__ void register_reset_kernel(int* ctl) {
@@ -1485,19 +1918,16 @@ extern "C" int df_decode_persistent(const DfPersistModel* model, int steps, int 
   if (!model || !workspace || steps < 0) return DF_BAD_ARGUMENT;
   DfPersistModel m = *model;
   if (m.hidden <= 0 || m.hidden > kMaxHidden || m.hidden % 512 || m.inter <= 0 || m.inter % 1024 ||
-      m.vocab <= 0 || m.vocab % 128 || m.vocab > (1 << 18) || m.num_layers < 1 || m.max_len < 1 || !m.layers || !m.head_w || !m.head_s ||
-      !m.final_norm || !m.inv_freq || !m.position || !m.tokens)
+      m.vocab <= 0 || m.vocab % 128 || m.vocab > (1 << 18) || m.num_layers < 1 || m.max_len < 1 || !m.layers ||
+      !m.head_w || !m.head_s || !m.final_norm || !m.inv_freq || !m.position || !m.tokens)
     return DF_BAD_ARGUMENT;
   if (2 * (m.inter / kXcd) > kColparMax) return DF_BAD_ARGUMENT;
-  if ((m.vocab / kTileCols / kXcd + kPerXcd - 1) / kPerXcd > kMaxWgTiles * kCompute) return DF_BAD_ARGUMENT;
+  if (m.inter / kXcd / kGroup > kMaxGroups || m.hidden / kGroup > kMaxGroups) return DF_BAD_ARGUMENT;
+  if ((m.vocab / kTileCols / kXcd + kPerXcd - 1) / kPerXcd > kMaxHeadTiles) return DF_BAD_ARGUMENT;
   if (teacher_forced && !m.prompt) return DF_BAD_ARGUMENT;
-  // per-wave register budgets: blocks per wave of every GEMV phase <= kMaxNb, and tiles
-  // per workgroup range <= kMaxWgTiles
+  // a workgroup's block range of every GEMV phase spans at most kMaxWgTiles output tiles
   const int G = m.hidden / kGroup;
-  auto fits = [&](int blocks, int ng) {
-    const int per_wg = (blocks + kPerXcd - 1) / kPerXcd;
-    return (per_wg + kCompute - 1) / kCompute <= kMaxNb && per_wg / ng + 2 <= kMaxWgTiles;
-  };
+  auto fits = [&](int blocks, int ng) { return (blocks + kPerXcd - 1) / kPerXcd / ng + 2 <= kMaxWgTiles; };
   const int gu_tiles = 2 * (m.inter / kXcd) / kTileCols;
   const int row_tiles = m.hidden / kTileCols;
   if (!fits((kLinCols / kTileCols) * G, G) || !fits((kAttnCols / kTileCols) * G, G) || !fits(gu_tiles * G, G) ||
