@@ -54,7 +54,10 @@ constexpr int kCompute = 8;
 constexpr int kCtl = kCompute;                      // wave index of the control wave
 constexpr int kThreads = (kCompute + 1) * 64;       // 576
 constexpr int kMaxHidden = 2560;
-constexpr int kRing = 11;                           // weight blocks in flight per compute wave
+#ifndef DF_RING
+#define DF_RING 11
+#endif
+constexpr int kRing = DF_RING;                      // weight blocks in flight per compute wave
 constexpr int kMaxWgTiles = 8;                      // output tiles of a workgroup's GEMV range
 constexpr int kMaxGroups = 24;                      // 128-groups of a GEMV phase's input row
 constexpr int kMaxHeadTiles = 64;                   // head tiles per workgroup
@@ -159,6 +162,64 @@ DF_DEVICE void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// Wave reductions without LDS round trips (DPP inside 16-lane rows, readlane across rows).
+// __shfl_xor compiles to ds_bpermute, an LDS round trip per step, which sits on the
+// critical path of every norm and hand-off of this kernel.
+template <int CTRL>
+DF_DEVICE float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+DF_DEVICE int dpp_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+constexpr int kDppRor1 = 0x121, kDppRor2 = 0x122, kDppRor4 = 0x124, kDppRor8 = 0x128;
+// Sum over each 16-lane row, in every lane of the row.
+DF_DEVICE float row_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  return v;
+}
+DF_DEVICE float row_max(float v) {
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppMirror>(v));
+  return v;
+}
+DF_DEVICE float lane_f(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+// Whole-wave sum / max (same value in every lane).
+DF_DEVICE float dsum(float v) {
+  v = row_sum(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
+DF_DEVICE float dmax(float v) {
+  v = row_max(v);
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+// (max value, lowest index among maxima) over each 16-lane row, in every lane of the row.
+DF_DEVICE void argmax_step(float& bv, int& bi, float ov, int oi) {
+  if (ov > bv || (ov == bv && oi < bi)) {
+    bv = ov;
+    bi = oi;
+  }
+}
+DF_DEVICE void row_argmax(float& bv, int& bi) {
+  argmax_step(bv, bi, dpp<kDppRor8>(bv), dpp_i<kDppRor8>(bi));
+  argmax_step(bv, bi, dpp<kDppRor4>(bv), dpp_i<kDppRor4>(bi));
+  argmax_step(bv, bi, dpp<kDppRor2>(bv), dpp_i<kDppRor2>(bi));
+  argmax_step(bv, bi, dpp<kDppRor1>(bv), dpp_i<kDppRor1>(bi));
+}
+// Sum over the lanes of a row that share lane % 4 (rotations by 4 and 8 inside the row).
+DF_DEVICE float row_sum_mod4(float v) {
+  v += dpp<kDppRor4>(v);
+  v += dpp<kDppRor8>(v);
+  return v;
+}
+
 // ---------------------------------------------------------------------------------------
 // LDS. The weight ring and the GEMV input row are objects of their own: the compiler then
 // knows that reads of the input row and of the workgroup struct cannot alias a ring DMA.
@@ -192,7 +253,7 @@ struct Lds {
       uint2 hist[kDnCh];                         // conv history ring (bf16 x4, slot position % 4)
       float qkv_in[kDnCh];                       // pre-conv inputs: q 128, k 128, v 16
       float q[kDk], k[kDk], v[16];
-      float sred[kCompute][16];
+      float sred[kCompute][4][16];               // per wave and 16-lane row
       float ab8[8];                              // a of the XCD's 4 value heads, then b
       float gpar[2];                             // A_log, dt_bias of the unit's value head
       float scal[4];
@@ -349,7 +410,7 @@ DF_DEVICE void norm_w(Lds& L, Ctx& c, int hidden, float eps) {
     const float v = bf2f(L.h[k]);
     ss += v * v;
   }
-  ss = wave_sum(ss);
+  ss = dsum(ss);
   if (c.lane == 0) L.red[c.wave] = ss;
   sync(c);
   float tot = 0.0f;
@@ -367,7 +428,7 @@ DF_DEVICE void norm_w(Lds& L, Ctx& c, int hidden, float eps) {
       g_x[k + e] = b;
       y[e] = bf2f(b);
     }
-    const float sg = wave_sum(y[0] + y[1]);
+    const float sg = dsum(y[0] + y[1]);
     if (c.lane == 0) L.xs[g] = kBias * sg;
   }
   sync(c);
@@ -377,7 +438,7 @@ DF_DEVICE void norm_w(Lds& L, Ctx& c, int hidden, float eps) {
 DF_DEVICE void group_sums(Lds& L, const Ctx& c, int groups) {
   for (int g = 0; g < groups; ++g) {
     const uint32_t pr = *reinterpret_cast<const uint32_t*>(&g_x[g * kGroup + 2 * c.lane]);
-    const float s = wave_sum(bf2f(static_cast<uint16_t>(pr)) + bf2f(static_cast<uint16_t>(pr >> 16)));
+    const float s = dsum(bf2f(static_cast<uint16_t>(pr)) + bf2f(static_cast<uint16_t>(pr >> 16)));
     if (c.lane == 0) L.xs[g] = kBias * s;
   }
 }
@@ -558,31 +619,13 @@ DF_DEVICE void fill(Stream& st, const DfPersistModel& M, const Geo& q, const Ctx
   while (st.state == kStreaming && st.issued - st.consumed < kRing) issue_one(st, M, q, c, steps);
 }
 
-// Wait until at most k blocks (2 loads each) issued after the oldest pending one are in flight.
-DF_DEVICE void wait_blocks(int k) {
-  switch (k) {
-    case 0: wait_vm<0>(); break;
-    case 1: wait_vm<2>(); break;
-    case 2: wait_vm<4>(); break;
-    case 3: wait_vm<6>(); break;
-    case 4: wait_vm<8>(); break;
-    case 5: wait_vm<10>(); break;
-    case 6: wait_vm<12>(); break;
-    case 7: wait_vm<14>(); break;
-    case 8: wait_vm<16>(); break;
-    case 9: wait_vm<18>(); break;
-    case 10: wait_vm<20>(); break;
-    default: wait_vm<0>(); break;
-  }
-}
-static_assert(kRing <= 11, "wait_blocks covers k < kRing");
-
-// Wait for the oldest `need` pending blocks (need = 1 or 2); a full ring is the common case.
-DF_DEVICE void wait_oldest(const Stream& st, int need) {
-  const int pending = st.issued - st.consumed;
-  if (need == 1 && pending == kRing) wait_vm<2 * (kRing - 1)>();
-  else if (need == 2 && pending == kRing) wait_vm<2 * (kRing - 2)>();
-  else wait_blocks(pending - need);
+// Wait for the oldest `need` pending blocks (need = 1 or 2). The ring is full except while
+// it drains before an attention layer's hold or at the end of a launch, where waiting for
+// every block in flight costs nothing extra.
+template <int NEED>
+DF_DEVICE void wait_oldest(const Stream& st) {
+  if (st.issued - st.consumed == kRing) wait_vm<2 * (kRing - NEED)>();
+  else wait_vm<0>();
 }
 
 DF_DEVICE int next_slot(int s) { return s + 1 == kRing ? 0 : s + 1; }
@@ -597,65 +640,96 @@ DF_DEVICE void ring_read1(int slot, const Ctx& c, uint4& wv, uint32_t& sd) {
                : "memory");
 }
 
-// Two consecutive blocks (slots `slot` and next_slot(slot)) with one LDS wait.
-DF_DEVICE void ring_read2(int slot, const Ctx& c, uint4& w0, uint32_t& s0, uint4& w1, uint32_t& s1) {
+// Everything a pair of blocks needs from LDS, with one wait: both ring slots (weights,
+// scale dword), the two groups' input chunks of this lane's k slot and their group sums.
+struct PairIn {
+  uint4 w0, w1;
+  uint32_t s0, s1;
+  uint4 x0[4], x1[4];
+  float xs0, xs1;
+};
+DF_DEVICE void pair_read(int slot, const Ctx& c, const uint16_t* xg0, const uint16_t* xg1, const float* xsp0,
+                         const float* xsp1, PairIn& in) {
   const int slot1 = next_slot(slot);
   const uint32_t wa0 = lds_addr(&g_ring_w[c.wave][slot][c.lane]);
   const uint32_t sa0 = lds_addr(&g_ring_s[c.wave][slot][c.lane]);
   const uint32_t wa1 = lds_addr(&g_ring_w[c.wave][slot1][c.lane]);
   const uint32_t sa1 = lds_addr(&g_ring_s[c.wave][slot1][c.lane]);
+  const uint32_t xa0 = lds_addr(xg0), xa1 = lds_addr(xg1);
+  const uint32_t ya0 = lds_addr(xsp0), ya1 = lds_addr(xsp1);
   asm volatile(
-      "ds_read_b128 %0, %4\n\tds_read_b32 %1, %5\n\tds_read_b128 %2, %6\n\tds_read_b32 %3, %7\n\t"
+      "ds_read_b128 %0, %14\n\t"
+      "ds_read_b32 %2, %15\n\t"
+      "ds_read_b128 %1, %16\n\t"
+      "ds_read_b32 %3, %17\n\t"
+      "ds_read_b128 %4, %18\n\t"
+      "ds_read_b128 %5, %18 offset:16\n\t"
+      "ds_read_b128 %6, %18 offset:32\n\t"
+      "ds_read_b128 %7, %18 offset:48\n\t"
+      "ds_read_b128 %8, %19\n\t"
+      "ds_read_b128 %9, %19 offset:16\n\t"
+      "ds_read_b128 %10, %19 offset:32\n\t"
+      "ds_read_b128 %11, %19 offset:48\n\t"
+      "ds_read_b32 %12, %20\n\t"
+      "ds_read_b32 %13, %21\n\t"
       "s_waitcnt lgkmcnt(0)"
-      : "=&v"(w0), "=&v"(s0), "=&v"(w1), "=&v"(s1)
-      : "v"(wa0), "v"(sa0), "v"(wa1), "v"(sa1)
+      : "=&v"(in.w0), "=&v"(in.w1), "=&v"(in.s0), "=&v"(in.s1), "=&v"(in.x0[0]), "=&v"(in.x0[1]), "=&v"(in.x0[2]),
+        "=&v"(in.x0[3]), "=&v"(in.x1[0]), "=&v"(in.x1[1]), "=&v"(in.x1[2]), "=&v"(in.x1[3]), "=&v"(in.xs0),
+        "=&v"(in.xs1)
+      : "v"(wa0), "v"(sa0), "v"(wa1), "v"(sa1), "v"(xa0), "v"(xa1), "v"(ya0), "v"(ya1)
       : "memory");
 }
 
 // Wait for the oldest pending block and read it.
 DF_DEVICE void take_block(Stream& st, const Ctx& c, uint4& wv, uint32_t& sd) {
-  wait_oldest(st, 1);
+  wait_oldest<1>(st);
   ring_read1(st.rslot, c, wv, sd);
   st.consumed += 1;
   st.rslot = next_slot(st.rslot);
 }
 
-DF_DEVICE void take_blocks2(Stream& st, const Ctx& c, uint4& w0, uint32_t& s0, uint4& w1, uint32_t& s1) {
-  wait_oldest(st, 2);
-  ring_read2(st.rslot, c, w0, s0, w1, s1);
+DF_DEVICE void take_pair(Stream& st, const Ctx& c, const uint16_t* xg0, const uint16_t* xg1, const float* xsp0,
+                          const float* xsp1, PairIn& in) {
+  wait_oldest<2>(st);
+  pair_read(st.rslot, c, xg0, xg1, xsp0, xsp1, in);
   st.consumed += 2;
   st.rslot = next_slot(next_slot(st.rslot));
 }
 
-// (a & mask) | bias in one VALU op (gfx9 VOP3 takes no literals: mask from an SGPR, bias
-// from a VGPR, one constant-bus read).
-DF_DEVICE uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bias) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(bias));
-  return r;
-}
-
-// Two weights k = 2j, 2j+1 of a dword (nibbles at bits 4j and 16 + 4j) as bf16(128 + n).
-DF_DEVICE uint32_t bias_pair(uint32_t w, int j, uint32_t bias) {
-  return and_or(j == 0 ? w : w >> (4 * j), 0x000F000Fu, bias);
+// Two weights k = 2j, 2j+1 of a dword (nibbles at bits 4j and 16 + 4j) as bf16(128 + n):
+// ((w >> 4j) & mask) | bias. The mask and bias arrive as opaque register values (mask in an
+// SGPR, bias in a VGPR), so the compiler emits one v_and_or_b32 (gfx9 VOP3 encodes no
+// literal) and its hazard checks still cover the result, which feeds an MFMA.
+DF_DEVICE uint32_t bias_pair(uint32_t w, int j, uint32_t mask, uint32_t bias) {
+  return ((j == 0 ? w : w >> (4 * j)) & mask) | bias;
 }
 
 // Row 0 of one block's product: lanes 0..15 return s_col * sum_k x_k (n_k - 8) over the
-// block's 128 k (x = the group's input at this lane's k slot; xs = 136 * sum of the group).
-DF_DEVICE float block_dot(const uint4& wv, uint32_t sd, const uint16_t* x, float xs, int lane) {
-  const float s = __uint_as_float((lane & 1) ? (sd & 0xFFFF0000u) : (sd << 16));
+// block's 128 k (x = the group's input chunks at this lane's k slot, xs = 136 * the group's
+// sum, sh = 16 * (lane & 1) selects this lane's scale in the dword).
+DF_DEVICE float block_dot_r(const uint4& wv, uint32_t sd, const uint4 (&x)[4], float xs, uint32_t sh) {
+  const float s = __uint_as_float((sd >> sh) << 16);
   const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
-  const uint32_t bias = kBiasPair;
+  uint32_t mask = 0x000F000Fu, bias = kBiasPair;
+  asm("" : "+s"(mask));
+  asm("" : "+v"(bias));
   df_f32x4 d4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    const uint4 bw = make_uint4(bias_pair(words[d], 0, bias), bias_pair(words[d], 1, bias),
-                                bias_pair(words[d], 2, bias), bias_pair(words[d], 3, bias));
-    const uint4 aw = *reinterpret_cast<const uint4*>(x + d * 8);
-    d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, aw), __builtin_bit_cast(df_bf16x8, bw),
+    const uint4 bw = make_uint4(bias_pair(words[d], 0, mask, bias), bias_pair(words[d], 1, mask, bias),
+                                bias_pair(words[d], 2, mask, bias), bias_pair(words[d], 3, mask, bias));
+    d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, x[d]), __builtin_bit_cast(df_bf16x8, bw),
                                                  d4, 0, 0, 0);
   }
   return s * (d4[0] - xs);
+}
+
+// Single-block form reading its input from LDS.
+DF_DEVICE float block_dot(const uint4& wv, uint32_t sd, const uint16_t* x, float xs, int lane) {
+  uint4 xv[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) xv[d] = *reinterpret_cast<const uint4*>(x + d * 8);
+  return block_dot_r(wv, sd, xv, xs, 16u * (lane & 1));
 }
 
 // Compute waves: consume this wave's blocks of GEMV phase g (input row g_x, group sums
@@ -681,15 +755,15 @@ DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPer
       ++tr;
     }
   };
+  const uint32_t sh = 16u * (c.lane & 1);
   int i = 0;
 #pragma unroll 1
   for (; i + 1 < n; i += 2) {
-    uint4 w0, w1;
-    uint32_t s0, s1;
-    take_blocks2(st, c, w0, s0, w1, s1);
     const int gl1 = gl + 1 == g.ng ? 0 : gl + 1;
-    const float v0 = block_dot(w0, s0, xb + gl * kGroup, L.xs[gl], c.lane);
-    const float v1 = block_dot(w1, s1, xb + gl1 * kGroup, L.xs[gl1], c.lane);
+    PairIn in;
+    take_pair(st, c, xb + gl * kGroup, xb + gl1 * kGroup, &L.xs[gl], &L.xs[gl1], in);
+    const float v0 = block_dot_r(in.w0, in.s0, in.x0, in.xs0, sh);
+    const float v1 = block_dot_r(in.w1, in.s1, in.x1, in.xs1, sh);
     fill(st, M, q, c, steps);
     add(v0);
     add(v1);
@@ -746,6 +820,27 @@ DF_DEVICE void stage16(uint16_t* dst, const uint16_t* src, int n, int lane) {
   }
 }
 constexpr int kHidChunks = (kMaxHidden / 8 + 63) / 64;  // 16-byte chunks per lane of a hidden row
+
+// Control wave: the next GEMV phase's norm weight, loaded a phase ahead (after the current
+// phase's signal, so the load overlaps the next hand-off instead of delaying either).
+struct NormPre {
+  uint4 v[kHidChunks];
+};
+DF_DEVICE void norm_fetch(NormPre& p, const uint16_t* src, int n, int lane) {
+  const auto r = rsrc(src);
+#pragma unroll
+  for (int k = 0; k < kHidChunks; ++k) {
+    const int ch = lane + 64 * k;
+    if (ch * 8 < n) p.v[k] = ld16<kCpPlain>(r, ch * 16);
+  }
+}
+DF_DEVICE void norm_put(const NormPre& p, uint16_t* dst, int n, int lane) {
+#pragma unroll
+  for (int k = 0; k < kHidChunks; ++k) {
+    const int ch = lane + 64 * k;
+    if (ch * 8 < n) *reinterpret_cast<uint4*>(dst + ch * 8) = p.v[k];
+  }
+}
 
 // A run of XCD-local columns [j0, j0 + n) of the column-parallel outputs (j0, n multiples of
 // 4), delivered as bf16-rounded slot sums into dst.
@@ -1025,7 +1120,7 @@ DF_DEVICE void dn_compute(Ctx& c, LayerPtr Lp, Lds& L) {
   if (c.wave < 2) {
     float* vec = c.wave == 0 ? D.q : D.k;
     const float x0 = vec[c.lane * 2], x1 = vec[c.lane * 2 + 1];
-    const float ss = wave_sum(x0 * x0 + x1 * x1);
+    const float ss = dsum(x0 * x0 + x1 * x1);
     const float rr = 1.0f / sqrtf(ss + 1e-6f);
     float y0 = x0 * rr, y1 = x1 * rr;
     if (c.wave == 0) {
@@ -1050,18 +1145,12 @@ DF_DEVICE void dn_compute(Ctx& c, LayerPtr Lp, Lds& L) {
     S.z = S.z * eg;
     S.w = S.w * eg;
     float part[4] = {S.x * kr, S.y * kr, S.z * kr, S.w * kr};
+    // sums over the rows k of this wave's 16-lane row that share the column (lane % 4)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float v = part[j];
-      v += __shfl_xor(v, 4, 64);
-      v += __shfl_xor(v, 8, 64);
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      part[j] = v;
-    }
-    if (c.lane < 4) {
+    for (int j = 0; j < 4; ++j) part[j] = row_sum_mod4(part[j]);
+    if ((c.lane & 15) < 4) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) D.sred[c.wave][c4 * 4 + j] = part[j];
+      for (int j = 0; j < 4; ++j) D.sred[c.wave][c.lane >> 4][c4 * 4 + j] = part[j];
     }
   }
   sync(c);
@@ -1071,7 +1160,9 @@ DF_DEVICE void dn_compute(Ctx& c, LayerPtr Lp, Lds& L) {
     const int col = c4 * 4 + j;
     float recalled = 0.0f;
 #pragma unroll
-    for (int wv = 0; wv < kCompute; ++wv) recalled += D.sred[wv][col];
+    for (int wv = 0; wv < kCompute; ++wv)
+#pragma unroll
+      for (int rw = 0; rw < 4; ++rw) recalled += D.sred[wv][rw][col];
     delta[j] = (D.v[col] - recalled) * beta;
   }
   sync(c);  // sred is reused below
@@ -1083,24 +1174,19 @@ DF_DEVICE void dn_compute(Ctx& c, LayerPtr Lp, Lds& L) {
     float o[4] = {S.x * qr, S.y * qr, S.z * qr, S.w * qr};
     *reinterpret_cast<float4*>(Lp->state + ((size_t)hv * kDk + k) * kDk + vs * 16 + c4 * 4) = S;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float v = o[j];
-      v += __shfl_xor(v, 4, 64);
-      v += __shfl_xor(v, 8, 64);
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      o[j] = v;
-    }
-    if (c.lane < 4) {
+    for (int j = 0; j < 4; ++j) o[j] = row_sum_mod4(o[j]);
+    if ((c.lane & 15) < 4) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) D.sred[c.wave][c4 * 4 + j] = o[j];
+      for (int j = 0; j < 4; ++j) D.sred[c.wave][c.lane >> 4][c4 * 4 + j] = o[j];
     }
   }
   sync(c);
   if (c.tid < 16) {
     float o = 0.0f;
 #pragma unroll
-    for (int wv = 0; wv < kCompute; ++wv) o += D.sred[wv][c.tid];
+    for (int wv = 0; wv < kCompute; ++wv)
+#pragma unroll
+      for (int rw = 0; rw < 4; ++rw) o += D.sred[wv][rw][c.tid];
     D.core[c.tid] = f2bf(o);
   }
   sync(c);
@@ -1113,7 +1199,7 @@ DF_DEVICE void dn_compute(Ctx& c, LayerPtr Lp, Lds& L) {
 // RMSNorm(1+w) over 256 dims held 4 per lane, then partial RoPE (attention.hip's order).
 DF_DEVICE void norm_rope4_lds(float x[4], const uint16_t* nw, float eps, const float* inv, float posf, int lane) {
   float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
-  ss = wave_sum(ss);
+  ss = dsum(ss);
   const float r = 1.0f / sqrtf(ss / static_cast<float>(kHd) + eps);
   float n[4];
 #pragma unroll
@@ -1121,7 +1207,8 @@ DF_DEVICE void norm_rope4_lds(float x[4], const uint16_t* nw, float eps, const f
   constexpr int half = kRot / 2;
   float partner[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) partner[i] = __shfl_xor(n[i], half / 4, 64);
+  for (int i = 0; i < 4; ++i) partner[i] = dpp<kDppRor8>(n[i]);  // lane ^ 8 = (lane + 8) mod 16 in a row
+  static_assert(half / 4 == 8, "the partner of a rotary dim is 8 lanes away");
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int dim = lane * 4 + i;
@@ -1218,7 +1305,7 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, floa
   if (c.wave < 2) {
     const int h = c.wave;
     const float s0 = A.sc[h][c.lane], s1 = A.sc[h][c.lane + 64];
-    const float tmax = wave_max(fmaxf(s0, s1));
+    const float tmax = dmax(fmaxf(s0, s1));
     const float mo = A.ml[h][0];
     const float m_new = fmaxf(mo, tmax);
     float p0 = 0.f, p1 = 0.f, alpha = 1.0f;
@@ -1227,7 +1314,7 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, floa
       p1 = s1 == -INFINITY ? 0.0f : expf(s1 - m_new);
       alpha = mo == -INFINITY ? 0.0f : expf(mo - m_new);
     }
-    const float lsum = wave_sum(p0 + p1);
+    const float lsum = dsum(p0 + p1);
     A.sc[h][c.lane] = p0;
     A.sc[h][c.lane + 64] = p1;
     if (c.lane == 0) {
@@ -1348,7 +1435,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           // GatedRMSNorm per 128-head, one element per thread (a head = 2 waves)
           const int i = c.tid;
           const float v = bf2f(g_x[i]);
-          const float ss = wave_sum(v * v);
+          const float ss = dsum(v * v);
           if (c.lane == 0) L.red[c.wave] = ss;
           sync(c);
           const int h = i >> 7;
@@ -1357,7 +1444,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           const float t = round_bf(bf2f(L.nw[i & 127]) * round_bf(v * rr));
           const uint16_t xb = f2bf(t * silu(L.u.on.z[i]));
           g_x[i] = xb;
-          const float gs = wave_sum(bf2f(xb));
+          const float gs = dsum(bf2f(xb));
           if (c.lane == 0) L.red[16 + c.wave] = gs;
           sync(c);
           if (c.tid < 4) L.xs[c.tid] = kBias * (L.red[16 + 2 * c.tid] + L.red[16 + 2 * c.tid + 1]);
@@ -1471,6 +1558,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       // tiles t_lo + wave + 8 j, all groups, from the weight stream
       const int ntw = head_tiles_of_wave(q, c.wave);
       const uint16_t* xb = g_x + (c.lane >> 4) * 32;
+      const uint32_t sh = 16u * (c.lane & 1);
       float bv = -INFINITY;
       int bi = 0x7FFFFFFF;
       float acc = 0.0f;
@@ -1478,11 +1566,10 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       // G is a multiple of 4 (hidden % 512 == 0), so a pair never straddles two tiles
 #pragma unroll 1
       for (int i = 0; i < ntw * G; i += 2) {
-        uint4 w0, w1;
-        uint32_t s0, s1;
-        take_blocks2(st, c, w0, s0, w1, s1);
-        const float v0 = block_dot(w0, s0, xb + gl * kGroup, L.xs[gl], c.lane);
-        const float v1 = block_dot(w1, s1, xb + (gl + 1) * kGroup, L.xs[gl + 1], c.lane);
+        PairIn in;
+        take_pair(st, c, xb + gl * kGroup, xb + (gl + 1) * kGroup, &L.xs[gl], &L.xs[gl + 1], in);
+        const float v0 = block_dot_r(in.w0, in.s0, in.x0, in.xs0, sh);
+        const float v1 = block_dot_r(in.w1, in.s1, in.x1, in.xs1, sh);
         fill(st, M, q, c, steps);
         acc += v0;
         acc += v1;
@@ -1504,14 +1591,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           ++j;
         }
       }
-      for (int off = 8; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(bv, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
-        if (ov > bv || (ov == bv && oi < bi)) {
-          bv = ov;
-          bi = oi;
-        }
-      }
+      row_argmax(bv, bi);
       if (c.lane == 0) {
         H.bv[c.wave] = bv;
         H.bi[c.wave] = bi;
@@ -1532,6 +1612,8 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
   const int pos0 = *M.position;
   const int step0 = M.step ? *M.step : 0;
   int64_t token = M.tokens[0];
+  NormPre np;
+  norm_fetch(np, layer_at(M, 0)->in_norm, hidden, c.lane);
   auto fail = [&](int nbars) {  // pass the barriers the compute waves still wait at, then stop
     if (c.lane == 0) L.ok = 0;
     for (int i = 0; i < nbars; ++i) bar();
@@ -1589,13 +1671,14 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       {
         fence(c, kTProj);
         const Gemv g = gemv_of(Lp, q, 0, c.xcd, c.r);
-        stage16<kHidChunks, kCpPlain>(L.nw, Lp->in_norm, hidden, c.lane);  // h is already in LDS
+        norm_put(np, L.nw, hidden, c.lane);  // in_norm (h is already in LDS)
         sync(c);
         for (int i = 0; i < kNormBars; ++i) sync(c);
         sync(c);  // blocks consumed
         c.epoch += 1;
         colpar_epilogue(g, c, L);
         signal_local(c, c.epoch);
+        norm_fetch(np, Lp->post_norm, hidden, c.lane);
       }
       if (kind == 0) {
         // ================= conv + gated delta step ===================================
@@ -1695,9 +1778,9 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           const float m = __uint_as_float(static_cast<uint32_t>(ml));
           const float l = __uint_as_float(static_cast<uint32_t>(ml >> 32));
           const float mm = c.lane < kPerXcd && l > 0.0f ? m : -INFINITY;
-          const float mstar = wave_max(mm);
+          const float mstar = dmax(mm);
           const float wgt = mm == -INFINITY ? 0.0f : expf(mm - mstar);
-          const float den = wave_sum(c.lane < kPerXcd ? wgt * l : 0.0f);
+          const float den = dsum(c.lane < kPerXcd ? wgt * l : 0.0f);
           if (c.lane < kPerXcd) Mg.wgt[c.lane] = wgt;
           if (c.lane < 16) {
             float num = 0.0f;
@@ -1728,13 +1811,14 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       {
         fence(c, kTGateUp);
         const Gemv g = gemv_of(Lp, q, 2, c.xcd, c.r);
-        stage16<kHidChunks, kCpPlain>(L.nw, Lp->post_norm, hidden, c.lane);
+        norm_put(np, L.nw, hidden, c.lane);  // post_norm
         sync(c);
         for (int i = 0; i < kNormBars; ++i) sync(c);
         sync(c);  // blocks consumed
         c.epoch += 1;
         colpar_epilogue(g, c, L);
         signal_local(c, c.epoch);
+        norm_fetch(np, li + 1 < M.num_layers ? layer_at(M, li + 1)->in_norm : M.final_norm, hidden, c.lane);
       }
       // ================= down (row-parallel) ===========================================
       {
@@ -1756,7 +1840,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
     {
       fence(c, kTHead);
       auto& H = L.hd;
-      stage16<kHidChunks, kCpPlain>(L.nw, M.final_norm, hidden, c.lane);
+      norm_put(np, L.nw, hidden, c.lane);  // final_norm
       sync(c);
       for (int i = 0; i < kNormBars; ++i) sync(c);
       sync(c);  // head blocks consumed, per-wave candidates in LDS
@@ -1827,6 +1911,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       if (!ok) return;
       token = bi;
       if (c.lane == 0 && c.xcd == 0 && c.r == 0 && !teacher_forced && M.token_log) M.token_log[step0 + step] = token;
+      norm_fetch(np, layer_at(M, 0)->in_norm, hidden, c.lane);  // the next token's first norm
     }
   }
   __builtin_amdgcn_s_waitcnt(0);
