@@ -282,6 +282,9 @@ struct Lds {
     struct {                                     // all-reduce slice
       float y[kXcd][128];
     } rd;
+    struct {                                     // down: the XCD's gate|up column sums
+      __align__(16) float gu[kColparMax];
+    } ac;
   } u;
 };
 
@@ -432,15 +435,6 @@ DF_DEVICE void norm_w(Lds& L, Ctx& c, int hidden, float eps) {
     if (c.lane == 0) L.xs[g] = kBias * sg;
   }
   sync(c);
-}
-
-// Control wave: L.xs of `groups` 128-groups of g_x (after it wrote g_x itself).
-DF_DEVICE void group_sums(Lds& L, const Ctx& c, int groups) {
-  for (int g = 0; g < groups; ++g) {
-    const uint32_t pr = *reinterpret_cast<const uint32_t*>(&g_x[g * kGroup + 2 * c.lane]);
-    const float s = dsum(bf2f(static_cast<uint16_t>(pr)) + bf2f(static_cast<uint16_t>(pr >> 16)));
-    if (c.lane == 0) L.xs[g] = kBias * s;
-  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -642,6 +636,11 @@ DF_DEVICE void ring_read1(int slot, const Ctx& c, uint4& wv, uint32_t& sd) {
 
 // Everything a pair of blocks needs from LDS, with one wait: both ring slots (weights,
 // scale dword), the two groups' input chunks of this lane's k slot and their group sums.
+// Only row 0 of each product is used: its A operand comes from lanes 0, 16, 32 and 48, and
+// its scales, group sums and results live in lanes 0..15. The input chunks are read by
+// those four lanes only and the scale dwords and group sums by lanes 0..15 (exec masked
+// inside the asm and restored before it ends), which cuts the LDS traffic of a pair from
+// 11 KB to under 3 KB; the other lanes' copies hold stale values that only feed rows 1..15.
 struct PairIn {
   uint4 w0, w1;
   uint32_t s0, s1;
@@ -657,25 +656,35 @@ DF_DEVICE void pair_read(int slot, const Ctx& c, const uint16_t* xg0, const uint
   const uint32_t sa1 = lds_addr(&g_ring_s[c.wave][slot1][c.lane]);
   const uint32_t xa0 = lds_addr(xg0), xa1 = lds_addr(xg1);
   const uint32_t ya0 = lds_addr(xsp0), ya1 = lds_addr(xsp1);
+  uint64_t saved;
   asm volatile(
-      "ds_read_b128 %0, %14\n\t"
-      "ds_read_b32 %2, %15\n\t"
-      "ds_read_b128 %1, %16\n\t"
-      "ds_read_b32 %3, %17\n\t"
-      "ds_read_b128 %4, %18\n\t"
-      "ds_read_b128 %5, %18 offset:16\n\t"
-      "ds_read_b128 %6, %18 offset:32\n\t"
-      "ds_read_b128 %7, %18 offset:48\n\t"
-      "ds_read_b128 %8, %19\n\t"
-      "ds_read_b128 %9, %19 offset:16\n\t"
-      "ds_read_b128 %10, %19 offset:32\n\t"
-      "ds_read_b128 %11, %19 offset:48\n\t"
-      "ds_read_b32 %12, %20\n\t"
-      "ds_read_b32 %13, %21\n\t"
+      "ds_read_b128 %0, %15\n\t"
+      "ds_read_b128 %1, %17\n\t"
+      "s_mov_b64 %14, exec\n\t"
+      "s_mov_b32 exec_lo, 0x10001\n\t"
+      "s_mov_b32 exec_hi, 0x10001\n\t"
+      "s_nop 0\n\t"
+      "ds_read_b128 %4, %19\n\t"
+      "ds_read_b128 %5, %19 offset:16\n\t"
+      "ds_read_b128 %6, %19 offset:32\n\t"
+      "ds_read_b128 %7, %19 offset:48\n\t"
+      "ds_read_b128 %8, %20\n\t"
+      "ds_read_b128 %9, %20 offset:16\n\t"
+      "ds_read_b128 %10, %20 offset:32\n\t"
+      "ds_read_b128 %11, %20 offset:48\n\t"
+      "s_mov_b32 exec_lo, 0xffff\n\t"
+      "s_mov_b32 exec_hi, 0\n\t"
+      "s_nop 0\n\t"
+      "ds_read_b32 %2, %16\n\t"
+      "ds_read_b32 %3, %18\n\t"
+      "ds_read_b32 %12, %21\n\t"
+      "ds_read_b32 %13, %22\n\t"
+      "s_mov_b64 exec, %14\n\t"
+      "s_nop 0\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&v"(in.w0), "=&v"(in.w1), "=&v"(in.s0), "=&v"(in.s1), "=&v"(in.x0[0]), "=&v"(in.x0[1]), "=&v"(in.x0[2]),
         "=&v"(in.x0[3]), "=&v"(in.x1[0]), "=&v"(in.x1[1]), "=&v"(in.x1[2]), "=&v"(in.x1[3]), "=&v"(in.xs0),
-        "=&v"(in.xs1)
+        "=&v"(in.xs1), "=&s"(saved)
       : "v"(wa0), "v"(sa0), "v"(wa1), "v"(sa1), "v"(xa0), "v"(xa1), "v"(ya0), "v"(ya1)
       : "memory");
 }
@@ -886,14 +895,12 @@ DF_DEVICE void gather_colpar(const Ctx& c, const Seg (&seg)[NS]) {
   }
 }
 
-// The down projection's input into g_x: act = bf16(bf16(silu(g)) * u) over the XCD's
-// inter_x gate|up column pairs (16-column gate tile, then its up tile), straight from the
-// column-parallel slots. Chunk ch (4 columns) of pair ch / 8 is a gate chunk for
-// ch % 8 < 4; its up partner is chunk ch + 4, held 4 lanes up.
+// Control wave: the XCD's 2 inter_x gate|up columns as (unrounded) sums of the two
+// column-parallel slots, into gu.
 template <int K>
-DF_DEVICE void stage_act(const Ctx& c, int inter_x) {
+DF_DEVICE void stage_gu(const Ctx& c, int inter_x, float* gu) {
   const auto r = rsrc(c.w.colpar + (size_t)c.xcd * 2 * kColparMax);
-  const int chunks = inter_x / 2;
+  const int chunks = inter_x / 2;  // 4 columns each
   uint4 a[K], b[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
@@ -906,22 +913,52 @@ DF_DEVICE void stage_act(const Ctx& c, int inter_x) {
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const int ch = c.lane + 64 * k;
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (ch < chunks) {
-      v[0] = round_bf(__uint_as_float(a[k].x) + __uint_as_float(b[k].x));
-      v[1] = round_bf(__uint_as_float(a[k].y) + __uint_as_float(b[k].y));
-      v[2] = round_bf(__uint_as_float(a[k].z) + __uint_as_float(b[k].z));
-      v[3] = round_bf(__uint_as_float(a[k].w) + __uint_as_float(b[k].w));
-    }
-    float u[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) u[e] = __shfl(v[e], (c.lane + 4) & 63, 64);
-    if (ch < chunks && (c.lane & 7) < 4) {
-      const int j = (ch / 8) * 16 + (ch % 8) * 4;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) g_x[j + e] = f2bf(round_bf(silu(v[e])) * u[e]);
+      float4 v;
+      v.x = __uint_as_float(a[k].x) + __uint_as_float(b[k].x);
+      v.y = __uint_as_float(a[k].y) + __uint_as_float(b[k].y);
+      v.z = __uint_as_float(a[k].z) + __uint_as_float(b[k].z);
+      v.w = __uint_as_float(a[k].w) + __uint_as_float(b[k].w);
+      *reinterpret_cast<float4*>(gu + 4 * ch) = v;
     }
   }
+}
+
+// Compute waves (1 barrier; the control wave passes 1): the down projection's input
+// act = bf16(bf16(silu(g)) * u) into g_x and its group sums L.xs. The gate|up columns come
+// in 32-column pairs (16 gate columns, then their 16 up columns), so act j reads gate
+// column 32 (j / 16) + j % 16 and the up column 16 further. A wave produces whole
+// 128-groups (2 elements per lane).
+constexpr int kActBars = 1;
+DF_DEVICE void swiglu_act(Lds& L, Ctx& c, int inter_x) {
+  const float* gu = L.u.ac.gu;
+  for (int g = c.wave; g < inter_x / kGroup; g += kCompute) {
+    const int j = g * kGroup + 2 * c.lane;      // even: j and j + 1 share a 16-run
+    const int col = (j >> 4) * 32 + (j & 15);
+    const float2 gv = *reinterpret_cast<const float2*>(gu + col);
+    const float2 uv = *reinterpret_cast<const float2*>(gu + col + 16);
+    const uint16_t b0 = f2bf(round_bf(silu(round_bf(gv.x))) * round_bf(uv.x));
+    const uint16_t b1 = f2bf(round_bf(silu(round_bf(gv.y))) * round_bf(uv.y));
+    *reinterpret_cast<uint32_t*>(&g_x[j]) = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
+    const float sg = dsum(bf2f(b0) + bf2f(b1));
+    if (c.lane == 0) L.xs[g] = kBias * sg;
+  }
+  sync(c);
+}
+
+// Control wave: the XCD's 512 merged attention / delta outputs (bf16, published by the
+// workgroups of the XCD) into g_x with the group sums L.xs of its four 128-groups (a group is
+// one 16-lane row of 8 values per lane).
+DF_DEVICE void stage_core(Lds& L, const Ctx& c) {
+  const auto r = rsrc(c.w.core + (size_t)c.xcd * 512);
+  const uint4 v = ld16<kCpAgent>(r, c.lane * 16);
+  *reinterpret_cast<uint4*>(&g_x[c.lane * 8]) = v;
+  float s = 0.0f;
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) s += __uint_as_float(w[e] << 16) + __uint_as_float(w[e] & 0xFFFF0000u);
+  s = row_sum(s);
+  if ((c.lane & 15) == 0) L.xs[c.lane >> 4] = kBias * s;
 }
 
 // Control wave, column-parallel epilogue: this workgroup's partial of each tile it touched
@@ -1378,7 +1415,10 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, floa
 //   o_proj     C: hand-off, core -> g_x, group sums                    | 1
 //              W: consume                                              | 1
 //              C: row-parallel partials, all-reduce                    | 1
-//   gate|up    as in_proj; down as o_proj with C staging act
+//   gate|up    as in_proj
+//   down       C: hand-off, gate|up column sums                        | 1
+//              W: SwiGLU -> g_x, group sums                            | kActBars
+//              then as o_proj
 //   head       C: stage norm weight                                    | 1
 //              W: RMSNorm                                              | kNormBars
 //              W: consume head blocks, argmax per wave                 | 1
@@ -1544,6 +1584,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         const Gemv g = gemv_of(Lp, q, 3, c.xcd, c.r);
         sync(c);
         if (!L.ok) return stop();
+        swiglu_act(L, c, q.inter_x);
         gemv_consume(g, c, st, M, q, steps, L);
         sync(c);
         sync(c);  // all-reduce done
@@ -1797,8 +1838,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           fence(c, kTOProj);
           const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
           if (!wait_local(c, c.epoch)) return fail(1);
-          stage16<1, kCpAgent>(g_x, c.w.core + (size_t)c.xcd * 512, 512, c.lane);
-          group_sums(L, c, 4);
+          stage_core(L, c);
           sync(c);
           stamp(c, kTStaged);
           sync(c);  // blocks consumed
@@ -1825,10 +1865,10 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         fence(c, kTDown);
         const Gemv g = gemv_of(Lp, q, 3, c.xcd, c.r);
         if (!wait_local(c, c.epoch)) return fail(1);
-        stage_act<(kColparMax / 4 + 63) / 64>(c, q.inter_x);
-        group_sums(L, c, q.ngx);
+        stage_gu<(kColparMax / 4 + 63) / 64>(c, q.inter_x, L.u.ac.gu);
         sync(c);
         stamp(c, kTStaged);
+        for (int i = 0; i < kActBars; ++i) sync(c);
         sync(c);  // blocks consumed
         rowpar_epilogue(g, c, L, hidden);
         if (!allreduce_residual(c, L, hidden)) return fail(1);
