@@ -375,10 +375,11 @@ DF_DEVICE void raise_abort(const Ctx& c, int err) {
 DF_DEVICE bool wait_local(const Ctx& c, uint32_t epoch) {
   const int* f = c.w.flags + c.xcd * kPerXcd;
   const uint64_t t0 = now();
-  for (;;) {
+  for (int it = 1;; ++it) {
     const int v = c.lane < kPerXcd ? ld_agent(f + c.lane) : static_cast<int>(epoch);
     if (__all(v >= static_cast<int>(epoch))) return true;
-    if (ld_sys(c.w.ctl + 1)) return false;
+    // the abort word is read through to memory: only every 32nd poll pays for that
+    if ((it & 31) == 0 && ld_sys(c.w.ctl + 1)) return false;
     if (now() - t0 > kTimeout) {
       raise_abort(c, kErrTimeout);
       return false;
@@ -393,9 +394,11 @@ DF_DEVICE void signal_local(Ctx& c, uint32_t epoch) {
   __builtin_amdgcn_s_waitcnt(0);
   stamp(c, kTSignal);
   if (c.lane == 0) {
-    // a plain store lands in this XCD's L2, where the agent-scope polls of the other
-    // workgroups of the XCD read it
-    *(volatile __attribute__((address_space(1))) int*)(c.w.flags + c.xcd * kPerXcd + c.r) = static_cast<int>(epoch);
+    // a plain store (relaxed, workgroup scope: no cache bits and no wait after it) lands in
+    // this XCD's L2, where the agent-scope polls of the other workgroups of the XCD read it; a
+    // volatile or wider-scope store would write through to memory and wait for that
+    __hip_atomic_store((__attribute__((address_space(1))) int*)(c.w.flags + c.xcd * kPerXcd + c.r),
+                       static_cast<int>(epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 }
 
@@ -1009,7 +1012,7 @@ DF_DEVICE bool allreduce_residual(Ctx& c, Lds& L, int hidden) {
   uint64_t v[K];
   bool ok = true;
   const uint64_t t0 = now();
-  for (;;) {
+  for (int it = 1;; ++it) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       const int i = c.lane + 64 * k;
@@ -1022,7 +1025,7 @@ DF_DEVICE bool allreduce_residual(Ctx& c, Lds& L, int hidden) {
       if (i < items) ready = ready && static_cast<uint32_t>(v[k] >> 32) == want;
     }
     if (__all(ready)) break;
-    if (ld_sys(c.w.ctl + 1)) { ok = false; break; }
+    if ((it & 31) == 0 && ld_sys(c.w.ctl + 1)) { ok = false; break; }
     if (now() - t0 > kTimeout) { raise_abort(c, kErrTimeout); ok = false; break; }
     __builtin_amdgcn_s_sleep(1);
   }
@@ -1911,14 +1914,14 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       uint64_t v[kNwg / 64];
       bool ok = true;
       const uint64_t t0 = now();
-      for (;;) {
+      for (int it = 1;; ++it) {
 #pragma unroll
         for (int k = 0; k < kNwg / 64; ++k) v[k] = ld8<kCpSystem>(r, (c.lane + 64 * k) * 8);
         bool ready = true;
 #pragma unroll
         for (int k = 0; k < kNwg / 64; ++k) ready = ready && (static_cast<uint32_t>(v[k]) & 0x3FFFu) == (c.epoch & 0x3FFFu);
         if (__all(ready)) break;
-        if (ld_sys(c.w.ctl + 1)) { ok = false; break; }
+        if ((it & 31) == 0 && ld_sys(c.w.ctl + 1)) { ok = false; break; }
         if (now() - t0 > kTimeout) { raise_abort(c, kErrTimeout); ok = false; break; }
         __builtin_amdgcn_s_sleep(1);
       }
