@@ -226,7 +226,7 @@ DF_DEVICE float row_sum_mod4(float v) {
 // ---------------------------------------------------------------------------------------
 
 __shared__ __align__(16) uint4 g_ring_w[kCompute][kRing][64];     // 1 KB blocks
-__shared__ __align__(16) uint32_t g_ring_s[kCompute][kRing][64];  // scale dword of lane i: columns (i & 14), +1
+__shared__ __align__(16) uint32_t g_ring_s[kCompute][kRing][16];  // scale dword of lane i < 16: columns (i & 14), +1
 __shared__ __align__(16) uint16_t g_x[kMaxHidden + 8];            // GEMV input row (bf16)
 
 struct Lds {
@@ -288,14 +288,29 @@ struct Lds {
   } u;
 };
 
-constexpr size_t kLdsBytes = sizeof(Lds) + sizeof(g_ring_w) + sizeof(g_ring_s) + sizeof(g_x);
+// The layer table, copied into LDS when the launch starts. Read through the scalar cache
+// instead, each phase's first access missed (the weight stream evicts the table from L2
+// between layers) and stalled the wave for about a microsecond, in the middle of the weight
+// stream's issue loop. Fields are read with LF(), which makes them wave-uniform (SGPRs).
+constexpr int kMaxLayers = 32;
+static_assert(sizeof(DfPersistLayer) % 8 == 0, "layer table copied in 8-byte words");
+__shared__ __align__(16) DfPersistLayer g_layers[kMaxLayers];
+
+constexpr size_t kLdsBytes = sizeof(Lds) + sizeof(g_ring_w) + sizeof(g_ring_s) + sizeof(g_x) + sizeof(g_layers);
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
 
-// The layer table is never written during a launch: reading it through the constant
-// address space lets the compiler use scalar loads (a vector load would sit behind the
-// compute wave's weight ring in the in-order vmcnt queue).
-typedef const __attribute__((address_space(4))) DfPersistLayer* LayerPtr;
-DF_DEVICE LayerPtr layer_at(const DfPersistModel& M, int li) { return (LayerPtr)M.layers + li; }
+typedef const DfPersistLayer* LayerPtr;  // points into g_layers
+DF_DEVICE LayerPtr layer_at(const DfPersistModel&, int li) { return &g_layers[li]; }
+template <class T>
+DF_DEVICE T* uniform_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<T*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+DF_DEVICE int uniform_int(int v) { return __builtin_amdgcn_readfirstlane(v); }
+#define LF(Lp, field) uniform_ptr((Lp)->field)
+#define LKIND(Lp) uniform_int((Lp)->kind)
 
 DF_DEVICE uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
@@ -458,16 +473,16 @@ struct Gemv {
 DF_DEVICE Gemv gemv_of(LayerPtr Lp, const Geo& q, int k, int xcd, int r) {
   Gemv g;
   if (k == 0) {
-    const int nt = (Lp->kind == 0 ? kLinCols : kAttnCols) / kTileCols;
+    const int nt = (LKIND(Lp) == 0 ? kLinCols : kAttnCols) / kTileCols;
     const int B = nt * q.Gh;
-    g = Gemv{Lp->proj_w, Lp->proj_s, q.Gh, xcd * nt, 0, q.Gh, (r * B) / kPerXcd, ((r + 1) * B) / kPerXcd};
+    g = Gemv{LF(Lp, proj_w), LF(Lp, proj_s), q.Gh, xcd * nt, 0, q.Gh, (r * B) / kPerXcd, ((r + 1) * B) / kPerXcd};
   } else if (k == 1) {
-    g = Gemv{Lp->out_w, Lp->out_s, 4096 / kGroup, 0, xcd * 4, 4, q.rp_lo * 4, q.rp_hi * 4};
+    g = Gemv{LF(Lp, out_w), LF(Lp, out_s), 4096 / kGroup, 0, xcd * 4, 4, q.rp_lo * 4, q.rp_hi * 4};
   } else if (k == 2) {
     const int B = q.gu_tiles * q.Gh;
-    g = Gemv{Lp->gu_w, Lp->gu_s, q.Gh, xcd * q.gu_tiles, 0, q.Gh, (r * B) / kPerXcd, ((r + 1) * B) / kPerXcd};
+    g = Gemv{LF(Lp, gu_w), LF(Lp, gu_s), q.Gh, xcd * q.gu_tiles, 0, q.Gh, (r * B) / kPerXcd, ((r + 1) * B) / kPerXcd};
   } else {
-    g = Gemv{Lp->down_w, Lp->down_s, q.inter / kGroup, 0, xcd * q.ngx, q.ngx, q.rp_lo * q.ngx, q.rp_hi * q.ngx};
+    g = Gemv{LF(Lp, down_w), LF(Lp, down_s), q.inter / kGroup, 0, xcd * q.ngx, q.ngx, q.rp_lo * q.ngx, q.rp_hi * q.ngx};
   }
   return g;
 }
@@ -519,7 +534,7 @@ DF_DEVICE void seg_open(Stream& st, const DfPersistModel& M, const Geo& q, const
       }
     } else {
       LayerPtr Lp = layer_at(M, st.li);
-      if (st.k == 1 && Lp->kind == 1) {
+      if (st.k == 1 && LKIND(Lp) == 1) {
         if (st.state == kStreaming) {
           st.state = kHeld;
           return;
@@ -571,15 +586,26 @@ DF_DEVICE void dma16(const void* gaddr, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds_base)
                : "memory", "m0");
 }
-DF_DEVICE void dma4(const void* gaddr, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(gaddr), "s"(lds_base)
-               : "memory", "m0");
+// The scale DMA runs on lanes 0..15 only (the lanes that apply scales), 64 bytes per block.
+DF_DEVICE void dma4_16(const void* gaddr, uint32_t lds_base) {
+  uint64_t saved;
+  asm volatile(
+      "s_mov_b64 %0, exec\n\t"
+      "s_mov_b32 exec_lo, 0xffff\n\t"
+      "s_mov_b32 exec_hi, 0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %1, off\n\t"
+      "s_mov_b64 exec, %0"
+      : "=&s"(saved)
+      : "v"(gaddr), "s"(lds_base)
+      : "memory", "m0");
 }
 
 // Issue the cursor's block into the next ring slot (weights + scales) and advance.
 DF_DEVICE void issue_one(Stream& st, const DfPersistModel& M, const Geo& q, const Ctx& c, int steps) {
   dma16(st.wp + c.lane * 16, lds_addr(&g_ring_w[c.wave][st.wslot][0]));
-  dma4(st.sp + (c.lane & 14), lds_addr(&g_ring_s[c.wave][st.wslot][0]));
+  dma4_16(st.sp + (c.lane & 14), lds_addr(&g_ring_s[c.wave][st.wslot][0]));
   st.issued += 1;
   st.wslot = st.wslot + 1 == kRing ? 0 : st.wslot + 1;
   int adv = 1;
@@ -630,7 +656,7 @@ DF_DEVICE int next_slot(int s) { return s + 1 == kRing ? 0 : s + 1; }
 // One block's weights and scale dword from ring slot `slot` of this wave.
 DF_DEVICE void ring_read1(int slot, const Ctx& c, uint4& wv, uint32_t& sd) {
   const uint32_t wa = lds_addr(&g_ring_w[c.wave][slot][c.lane]);
-  const uint32_t sa = lds_addr(&g_ring_s[c.wave][slot][c.lane]);
+  const uint32_t sa = lds_addr(&g_ring_s[c.wave][slot][c.lane & 15]);
   asm volatile("ds_read_b128 %0, %2\n\tds_read_b32 %1, %3\n\ts_waitcnt lgkmcnt(0)"
                : "=&v"(wv), "=&v"(sd)
                : "v"(wa), "v"(sa)
@@ -654,9 +680,9 @@ DF_DEVICE void pair_read(int slot, const Ctx& c, const uint16_t* xg0, const uint
                          const float* xsp1, PairIn& in) {
   const int slot1 = next_slot(slot);
   const uint32_t wa0 = lds_addr(&g_ring_w[c.wave][slot][c.lane]);
-  const uint32_t sa0 = lds_addr(&g_ring_s[c.wave][slot][c.lane]);
+  const uint32_t sa0 = lds_addr(&g_ring_s[c.wave][slot][c.lane & 15]);
   const uint32_t wa1 = lds_addr(&g_ring_w[c.wave][slot1][c.lane]);
-  const uint32_t sa1 = lds_addr(&g_ring_s[c.wave][slot1][c.lane]);
+  const uint32_t sa1 = lds_addr(&g_ring_s[c.wave][slot1][c.lane & 15]);
   const uint32_t xa0 = lds_addr(xg0), xa1 = lds_addr(xg1);
   const uint32_t ya0 = lds_addr(xsp0), ya1 = lds_addr(xsp1);
   uint64_t saved;
@@ -1071,7 +1097,7 @@ DF_DEVICE bool dn_stage(Ctx& c, LayerPtr Lp, Lds& L) {
   constexpr int kSt = kCompute;              // float4 of the state slice per lane
   constexpr int kCh = (kDnCh + 63) / 64;     // conv channels per lane
   uint4 sv[kSt];
-  const float* state = Lp->state;
+  const float* state = LF(Lp, state);
 #pragma unroll
   for (int i = 0; i < kSt; ++i) {
     const int e = c.lane + 64 * i;  // row e / 4, columns 4 (e % 4)
@@ -1084,12 +1110,12 @@ DF_DEVICE bool dn_stage(Ctx& c, LayerPtr Lp, Lds& L) {
     const int ch = c.lane + 64 * i;
     if (ch < kDnCh) {
       const int gc = dn_channel(c, ch);
-      tp[i] = *reinterpret_cast<const uint2*>(Lp->conv_w + (size_t)gc * 4);
+      tp[i] = *reinterpret_cast<const uint2*>(LF(Lp, conv_w) + (size_t)gc * 4);
       // another workgroup of the XCD writes the q/k history slots: read at agent scope
-      hs[i] = ld_agent(reinterpret_cast<const uint64_t*>(Lp->conv_ring + (size_t)gc * 4));
+      hs[i] = ld_agent(reinterpret_cast<const uint64_t*>(LF(Lp, conv_ring) + (size_t)gc * 4));
     }
   }
-  const float alog = bf2f(Lp->A_log[hv]), dtb = bf2f(Lp->dt_bias[hv]);
+  const float alog = bf2f(LF(Lp, A_log)[hv]), dtb = bf2f(LF(Lp, dt_bias)[hv]);
   const bool ok = wait_local(c, c.epoch);
   if (ok) {
     const int khl = hvl >> 1;
@@ -1146,7 +1172,7 @@ DF_DEVICE void dn_compute(Ctx& c, LayerPtr Lp, Lds& L) {
     // history: this unit owns its v slice; the (even value head, slice 0) unit owns the
     // key head's q/k channels
     const bool owner = c.tid >= 256 || ((hvl & 1) == 0 && vs == 0);
-    if (owner) Lp->conv_ring[(size_t)dn_channel(c, c.tid) * 4 + (c.pos & 3)] = f2bf(x);
+    if (owner) LF(Lp, conv_ring)[(size_t)dn_channel(c, c.tid) * 4 + (c.pos & 3)] = f2bf(x);
   }
   if (c.tid == 0) {
     const float a = D.ab8[hvl], b = D.ab8[4 + hvl];
@@ -1212,7 +1238,7 @@ DF_DEVICE void dn_compute(Ctx& c, LayerPtr Lp, Lds& L) {
     S.z = S.z + kr * delta[2];
     S.w = S.w + kr * delta[3];
     float o[4] = {S.x * qr, S.y * qr, S.z * qr, S.w * qr};
-    *reinterpret_cast<float4*>(Lp->state + ((size_t)hv * kDk + k) * kDk + vs * 16 + c4 * 4) = S;
+    *reinterpret_cast<float4*>(LF(Lp, state) + ((size_t)hv * kDk + k) * kDk + vs * 16 + c4 * 4) = S;
 #pragma unroll
     for (int j = 0; j < 4; ++j) o[j] = row_sum_mod4(o[j]);
     if ((c.lane & 15) < 4) {
@@ -1293,7 +1319,7 @@ DF_DEVICE void at_issue_k(const Ctx& c, LayerPtr Lp, int t0, int j1, AtPre& P) {
   const size_t base = (size_t)(c.xcd >> 1) * c.max_len;
   const int key = t0 + c.wave * 16 + col;
   if (key < j1 && key != c.pos) {
-    GlobalBf16 kp = (GlobalBf16)Lp->k_cache + (base + key) * kHd + slot * 8;
+    GlobalBf16 kp = (GlobalBf16)LF(Lp, k_cache) + (base + key) * kHd + slot * 8;
 #pragma unroll
     for (int d = 0; d < 8; ++d) P.kb[d] = gload16(kp + d * 32);
   }
@@ -1333,7 +1359,7 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, floa
   uint2 vb[16];
   {
     const size_t base = (size_t)(c.xcd >> 1) * c.max_len;
-    GlobalBf16 vc = (GlobalBf16)Lp->v_cache;
+    GlobalBf16 vc = (GlobalBf16)LF(Lp, v_cache);
 #pragma unroll
     for (int jj = 0; jj < 16; ++jj) {
       const int kk = t0 + c.wave * 16 + jj;
@@ -1456,7 +1482,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
     if (!L.ok) return stop();
     for (int li = 0; li < M.num_layers; ++li) {
       LayerPtr Lp = layer_at(M, li);
-      const int kind = Lp->kind;
+      const int kind = LKIND(Lp);
       {  // input projection
         fence(c);
         const Gemv g = gemv_of(Lp, q, 0, c.xcd, c.r);
@@ -1527,8 +1553,8 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           const size_t row = ((size_t)(c.xcd >> 1) * M.max_len + c.pos) * kHd;
           const uint32_t kw = static_cast<uint32_t>(A.knew[2 * c.tid]) | (static_cast<uint32_t>(A.knew[2 * c.tid + 1]) << 16);
           const uint32_t vw = static_cast<uint32_t>(A.vnew[2 * c.tid]) | (static_cast<uint32_t>(A.vnew[2 * c.tid + 1]) << 16);
-          st_sys(reinterpret_cast<uint32_t*>(Lp->k_cache + row) + c.tid, kw);
-          st_sys(reinterpret_cast<uint32_t*>(Lp->v_cache + row) + c.tid, vw);
+          st_sys(reinterpret_cast<uint32_t*>(LF(Lp, k_cache) + row) + c.tid, kw);
+          st_sys(reinterpret_cast<uint32_t*>(LF(Lp, v_cache) + row) + c.tid, vw);
         }
         float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
         for (int t0 = j0; t0 < j1; t0 += kTileKeys) {
@@ -1657,7 +1683,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
   const int step0 = M.step ? *M.step : 0;
   int64_t token = M.tokens[0];
   NormPre np;
-  norm_fetch(np, layer_at(M, 0)->in_norm, hidden, c.lane);
+  norm_fetch(np, LF(layer_at(M, 0), in_norm), hidden, c.lane);
   auto fail = [&](int nbars) {  // pass the barriers the compute waves still wait at, then stop
     if (c.lane == 0) L.ok = 0;
     for (int i = 0; i < nbars; ++i) bar();
@@ -1710,7 +1736,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
 
     for (int li = 0; li < M.num_layers; ++li) {
       LayerPtr Lp = layer_at(M, li);
-      const int kind = Lp->kind;
+      const int kind = LKIND(Lp);
       // ================= input projection (column-parallel) =========================
       {
         fence(c, kTProj);
@@ -1722,7 +1748,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         c.epoch += 1;
         colpar_epilogue(g, c, L);
         signal_local(c, c.epoch);
-        norm_fetch(np, Lp->post_norm, hidden, c.lane);
+        norm_fetch(np, LF(Lp, post_norm), hidden, c.lane);
       }
       if (kind == 0) {
         // ================= conv + gated delta step ===================================
@@ -1747,7 +1773,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           stage16<1, kCpAgent>(g_x, c.w.core + (size_t)c.xcd * 512, 512, c.lane);
           const Seg seg[1] = {{kLinZ, 512, L.u.on.z}};
           gather_colpar<1, 2>(c, seg);
-          stage16<1, kCpPlain>(L.nw, Lp->gnorm_w, kDk, c.lane);
+          stage16<1, kCpPlain>(L.nw, LF(Lp, gnorm_w), kDk, c.lane);
           sync(c);
           stamp(c, kTStaged);
           sync(c);
@@ -1766,8 +1792,8 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         {
           const Seg seg[3] = {{0, kHd, A.qraw[0]}, {512, kHd, A.qraw[1]}, {kAttnK, 2 * kHd, A.kraw}};
           gather_colpar<3, 4>(c, seg);  // kraw and vraw are adjacent in LDS
-          stage16<1, kCpPlain>(A.qn_w, Lp->q_norm, kHd, c.lane);
-          stage16<1, kCpPlain>(A.kn_w, Lp->k_norm, kHd, c.lane);
+          stage16<1, kCpPlain>(A.qn_w, LF(Lp, q_norm), kHd, c.lane);
+          stage16<1, kCpPlain>(A.kn_w, LF(Lp, k_norm), kHd, c.lane);
           if (c.lane < kRot / 2) A.inv[c.lane] = M.inv_freq[c.lane];
           if (c.lane < 2) {
             A.ml[c.lane][0] = -INFINITY;
@@ -1861,7 +1887,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         c.epoch += 1;
         colpar_epilogue(g, c, L);
         signal_local(c, c.epoch);
-        norm_fetch(np, li + 1 < M.num_layers ? layer_at(M, li + 1)->in_norm : M.final_norm, hidden, c.lane);
+        norm_fetch(np, li + 1 < M.num_layers ? LF(layer_at(M, li + 1), in_norm) : M.final_norm, hidden, c.lane);
       }
       // ================= down (row-parallel) ===========================================
       {
@@ -1954,7 +1980,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       if (!ok) return;
       token = bi;
       if (c.lane == 0 && c.xcd == 0 && c.r == 0 && !teacher_forced && M.token_log) M.token_log[step0 + step] = token;
-      norm_fetch(np, layer_at(M, 0)->in_norm, hidden, c.lane);  // the next token's first norm
+      norm_fetch(np, LF(layer_at(M, 0), in_norm), hidden, c.lane);  // the next token's first norm
     }
   }
   __builtin_amdgcn_s_waitcnt(0);
@@ -1992,6 +2018,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DfPersistModel M, Ws w
       L.ok = 0;
     }
     L.token = xcc * kPerXcd + ticket;
+  }
+  {
+    const uint64_t* src = reinterpret_cast<const uint64_t*>(M.layers);
+    uint64_t* dst = reinterpret_cast<uint64_t*>(g_layers);
+    const int words = M.num_layers * static_cast<int>(sizeof(DfPersistLayer) / 8);
+    for (int i = threadIdx.x; i < words; i += kThreads) dst[i] = src[i];
   }
   __syncthreads();
   if (!L.ok) return;
@@ -2046,7 +2078,7 @@ extern "C" int df_decode_persistent(const DfPersistModel* model, int steps, int 
   if (!model || !workspace || steps < 0) return DF_BAD_ARGUMENT;
   DfPersistModel m = *model;
   if (m.hidden <= 0 || m.hidden > kMaxHidden || m.hidden % 512 || m.inter <= 0 || m.inter % 1024 ||
-      m.vocab <= 0 || m.vocab % 128 || m.vocab > (1 << 18) || m.num_layers < 1 || m.max_len < 1 || !m.layers ||
+      m.vocab <= 0 || m.vocab % 128 || m.vocab > (1 << 18) || m.num_layers < 1 || m.num_layers > kMaxLayers || m.max_len < 1 || !m.layers ||
       !m.head_w || !m.head_s || !m.final_norm || !m.inv_freq || !m.position || !m.tokens)
     return DF_BAD_ARGUMENT;
   if (2 * (m.inter / kXcd) > kColparMax) return DF_BAD_ARGUMENT;
