@@ -468,22 +468,48 @@ struct Gemv {
   int b_lo, b_hi;  // this workgroup's block range (relative to the slice, tile-major)
 };
 
-// Phase k of a layer (0 input projection, 1 out_proj / o_proj, 2 gate|up, 3 down) for
-// workgroup (xcd, r).
-DF_DEVICE Gemv gemv_of(LayerPtr Lp, const Geo& q, int k, int xcd, int r) {
+// Phase k of a layer of kind `kind` (phases: 0 input projection, 1 out_proj / o_proj,
+// 2 gate|up, 3 down) for workgroup (xcd, r), without its weight pointers.
+DF_DEVICE Gemv gemv_geom(int kind, const Geo& q, int k, int xcd, int r) {
   Gemv g;
   if (k == 0) {
-    const int nt = (LKIND(Lp) == 0 ? kLinCols : kAttnCols) / kTileCols;
+    const int nt = (kind == 0 ? kLinCols : kAttnCols) / kTileCols;
     const int B = nt * q.Gh;
-    g = Gemv{LF(Lp, proj_w), LF(Lp, proj_s), q.Gh, xcd * nt, 0, q.Gh, (r * B) / kPerXcd, ((r + 1) * B) / kPerXcd};
+    g = Gemv{nullptr, nullptr, q.Gh, xcd * nt, 0, q.Gh, (r * B) / kPerXcd, ((r + 1) * B) / kPerXcd};
   } else if (k == 1) {
-    g = Gemv{LF(Lp, out_w), LF(Lp, out_s), 4096 / kGroup, 0, xcd * 4, 4, q.rp_lo * 4, q.rp_hi * 4};
+    g = Gemv{nullptr, nullptr, 4096 / kGroup, 0, xcd * 4, 4, q.rp_lo * 4, q.rp_hi * 4};
   } else if (k == 2) {
     const int B = q.gu_tiles * q.Gh;
-    g = Gemv{LF(Lp, gu_w), LF(Lp, gu_s), q.Gh, xcd * q.gu_tiles, 0, q.Gh, (r * B) / kPerXcd, ((r + 1) * B) / kPerXcd};
+    g = Gemv{nullptr, nullptr, q.Gh, xcd * q.gu_tiles, 0, q.Gh, (r * B) / kPerXcd, ((r + 1) * B) / kPerXcd};
   } else {
-    g = Gemv{LF(Lp, down_w), LF(Lp, down_s), q.inter / kGroup, 0, xcd * q.ngx, q.ngx, q.rp_lo * q.ngx, q.rp_hi * q.ngx};
+    g = Gemv{nullptr, nullptr, q.inter / kGroup, 0, xcd * q.ngx, q.ngx, q.rp_lo * q.ngx, q.rp_hi * q.ngx};
   }
+  return g;
+}
+
+// The weight and scale pointers of phase k are adjacent in the layer table (checked below),
+// so one LDS read fetches both.
+static_assert(offsetof(DfPersistLayer, proj_s) == offsetof(DfPersistLayer, proj_w) + 8 &&
+                  offsetof(DfPersistLayer, out_w) == offsetof(DfPersistLayer, proj_w) + 16 &&
+                  offsetof(DfPersistLayer, out_s) == offsetof(DfPersistLayer, proj_w) + 24 &&
+                  offsetof(DfPersistLayer, gu_w) == offsetof(DfPersistLayer, proj_w) + 32 &&
+                  offsetof(DfPersistLayer, gu_s) == offsetof(DfPersistLayer, proj_w) + 40 &&
+                  offsetof(DfPersistLayer, down_w) == offsetof(DfPersistLayer, proj_w) + 48 &&
+                  offsetof(DfPersistLayer, down_s) == offsetof(DfPersistLayer, proj_w) + 56 &&
+                  offsetof(DfPersistLayer, proj_w) % 8 == 0,
+              "phase weight/scale pointers are consecutive pairs in DfPersistLayer");
+DF_DEVICE void phase_ptrs(int li, int k, const uint8_t*& w, const uint16_t*& s) {
+  const uint64_t* p = reinterpret_cast<const uint64_t*>(reinterpret_cast<const char*>(&g_layers[li]) +
+                                                        offsetof(DfPersistLayer, proj_w)) + 2 * k;
+  const uint64_t a = p[0], b = p[1];
+  w = uniform_ptr(reinterpret_cast<const uint8_t*>(a));
+  s = uniform_ptr(reinterpret_cast<const uint16_t*>(b));
+}
+
+DF_DEVICE Gemv gemv_of(LayerPtr Lp, const Geo& q, int k, int xcd, int r) {
+  Gemv g = gemv_geom(LKIND(Lp), q, k, xcd, r);
+  const int li = static_cast<int>(Lp - g_layers);
+  phase_ptrs(li, k, g.w, g.s);
   return g;
 }
 
@@ -512,48 +538,70 @@ struct Stream {
   int state;             // 0 streaming, 1 held before an attention layer's o_proj,
                          // 2 released, 3 past the launch's last block
   int li, k, istep;      // segment of the cursor: layer, phase (0..3; 4 = head), token
+  uint32_t kinds;        // bit li: layer li is an attention layer
 };
 
+// Per compute wave, where its share of each phase starts, for either layer kind (index
+// kind * 4 + phase) and for the head (index 8): {first block relative to the phase's
+// weights, run position | groups per run << 16, blocks skipped after a run, blocks}. The
+// same for every layer of a kind, so opening a segment only adds the layer's pointers.
+constexpr int kDescs = 9;
+__shared__ __align__(16) int4 g_desc[kCompute][kDescs];
+
 enum StreamState : int { kStreaming = 0, kHeld = 1, kReleased = 2, kDone = 3 };
+
+// Compute waves, once per launch: this wave's row of g_desc (lane i < kDescs fills entry i).
+DF_DEVICE void desc_init(const Geo& q, const Ctx& c) {
+  if (c.lane < kDescs) {
+    int4 d = make_int4(0, 0, 0, 0);
+    if (c.lane == 8) {
+      const int ntw = head_tiles_of_wave(q, c.wave);
+      d = make_int4((q.t_lo + c.wave) * q.Gh, q.Gh << 16, (kCompute - 1) * q.Gh, ntw * q.Gh);
+    } else {
+      const Gemv g = gemv_geom(c.lane >> 2, q, c.lane & 3, c.xcd, c.r);
+      int lo, n;
+      wave_range(g, c.wave, lo, n);
+      if (n > 0)
+        d = make_int4((g.tile0 + lo / g.ng) * g.G + g.g0 + lo % g.ng, (lo % g.ng) | (g.ng << 16), g.G - g.ng, n);
+    }
+    g_desc[c.wave][c.lane] = d;
+  }
+}
 
 // Position the cursor on the first block of the current segment, skipping empty segments;
 // stop at an attention layer's o_proj (until released) and after the last token.
 DF_DEVICE void seg_open(Stream& st, const DfPersistModel& M, const Geo& q, const Ctx& c, int steps) {
   for (;;) {
+    int di;
+    const uint8_t* wb;
+    const uint16_t* sb;
     if (st.k == 4) {
-      const int ntw = head_tiles_of_wave(q, c.wave);
-      if (ntw > 0) {
-        const size_t blk = (size_t)(q.t_lo + c.wave) * q.Gh;
-        st.wp = M.head_w + blk * kBlockBytes;
-        st.sp = M.head_s + blk * kTileCols;
-        st.g = 0;
-        st.ng = q.Gh;
-        st.wjump = (kCompute - 1) * q.Gh;
-        st.left = ntw * q.Gh;
-        return;
-      }
+      di = 8;
+      wb = M.head_w;
+      sb = M.head_s;
     } else {
-      LayerPtr Lp = layer_at(M, st.li);
-      if (st.k == 1 && LKIND(Lp) == 1) {
+      const int kind = (st.kinds >> st.li) & 1;
+      if (st.k == 1 && kind == 1) {
         if (st.state == kStreaming) {
           st.state = kHeld;
           return;
         }
         st.state = kStreaming;
       }
-      const Gemv g = gemv_of(Lp, q, st.k, c.xcd, c.r);
-      int lo, n;
-      wave_range(g, c.wave, lo, n);
-      if (n > 0) {
-        const size_t blk = (size_t)(g.tile0 + lo / g.ng) * g.G + g.g0 + lo % g.ng;
-        st.wp = g.w + blk * kBlockBytes;
-        st.sp = g.s + blk * kTileCols;
-        st.g = lo % g.ng;
-        st.ng = g.ng;
-        st.wjump = g.G - g.ng;
-        st.left = n;
-        return;
-      }
+      di = kind * 4 + st.k;
+      phase_ptrs(st.li, st.k, wb, sb);
+    }
+    const int4 dv = g_desc[c.wave][di];
+    const int left = uniform_int(dv.w);
+    if (left > 0) {
+      const int blk = uniform_int(dv.x), gpos = uniform_int(dv.y);
+      st.wp = wb + (size_t)blk * kBlockBytes;
+      st.sp = sb + (size_t)blk * kTileCols;
+      st.g = gpos & 0xFFFF;
+      st.ng = gpos >> 16;
+      st.wjump = uniform_int(dv.z);
+      st.left = left;
+      return;
     }
     // next segment
     if (st.k < 3) {
@@ -1470,6 +1518,9 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
   st.issued = st.consumed = st.wslot = st.rslot = 0;
   st.li = st.k = st.istep = 0;
   st.state = kStreaming;
+  st.kinds = 0;
+  for (int li = 0; li < M.num_layers; ++li) st.kinds |= static_cast<uint32_t>(LKIND(&g_layers[li]) & 1) << li;
+  desc_init(q, c);  // a wave's LDS accesses complete in order: its own row reads back as written
   seg_open(st, M, q, c, steps);
   fill(st, M, q, c, steps);
   auto stop = [&]() { __builtin_amdgcn_s_waitcnt(0); };
