@@ -421,35 +421,35 @@ DF_DEVICE void signal_local(Ctx& c, uint32_t epoch) {
 // GEMV input rows
 // ---------------------------------------------------------------------------------------
 
-// Compute waves (2 barriers; the control wave passes 2): g_x = bf16(RMSNorm(h) * (1 + w))
-// over `hidden` (w staged in L.nw) and the group sums L.xs. A wave produces whole 128-groups
+// Compute waves (1 barrier; the control wave passes 1): g_x = bf16(RMSNorm(h) * (1 + w))
+// over `hidden` (w staged in L.nw) and the group sums L.xs. Every wave sums the squares of
+// all of h itself (identical code and order in every wave, so all agree on the factor), which
+// saves the cross-wave exchange and its barrier; a wave then produces whole 128-groups
 // (2 elements per lane).
-constexpr int kNormBars = 2;
+constexpr int kNormBars = 1;
 DF_DEVICE void norm_w(Lds& L, Ctx& c, int hidden, float eps) {
   float ss = 0.0f;
-  for (int k = c.tid; k < hidden; k += kCompute * 64) {
-    const float v = bf2f(L.h[k]);
-    ss += v * v;
+  for (int k = c.lane * 8; k < hidden; k += 64 * 8) {
+    const uint4 v = *reinterpret_cast<const uint4*>(&L.h[k]);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xFFFF0000u);
+      ss += lo * lo;
+      ss += hi * hi;
+    }
   }
   ss = dsum(ss);
-  if (c.lane == 0) L.red[c.wave] = ss;
-  sync(c);
-  float tot = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kCompute; ++i) tot += L.red[i];
-  const float r = 1.0f / sqrtf(tot / static_cast<float>(hidden) + eps);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(hidden) + eps);
   const int G = hidden / kGroup;
   for (int g = c.wave; g < G; g += kCompute) {
     const int k = g * kGroup + 2 * c.lane;
-    float y[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const float scaled = bf2f(L.h[k + e]) * r;
-      const uint16_t b = f2bf(scaled * (1.0f + bf2f(L.nw[k + e])));
-      g_x[k + e] = b;
-      y[e] = bf2f(b);
-    }
-    const float sg = dsum(y[0] + y[1]);
+    const uint32_t hv = *reinterpret_cast<const uint32_t*>(&L.h[k]);
+    const uint32_t wv = *reinterpret_cast<const uint32_t*>(&L.nw[k]);
+    const uint16_t b0 = f2bf(__uint_as_float(hv << 16) * r * (1.0f + __uint_as_float(wv << 16)));
+    const uint16_t b1 = f2bf(__uint_as_float(hv & 0xFFFF0000u) * r * (1.0f + __uint_as_float(wv & 0xFFFF0000u)));
+    *reinterpret_cast<uint32_t*>(&g_x[k]) = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
+    const float sg = dsum(bf2f(b0) + bf2f(b1));
     if (c.lane == 0) L.xs[g] = kBias * sg;
   }
   sync(c);
