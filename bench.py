@@ -44,6 +44,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--roofline-reps", type=int, default=10)
     ap.add_argument("--roofline-only", action="store_true")
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="after the timed decode, run three plain 256 MiB device copies (for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE passes)")
     ap.add_argument("--engine", choices=("persistent", "graph"), default="persistent",
                     help="persistent: one cooperative launch per decode run (df_decode_persistent); "
                          "graph: the per-op kernels replayed as one HIP graph per step")
@@ -60,9 +63,10 @@ GATE_UP_KERNEL = "w4_gemv_kernel<RMSNORM, SWIGLU> (post-attention norm + gate/up
 # the counter reads for a plain 256 MiB device copy (x 2.000 for FETCH_SIZE, x 1.000 for
 # WRITE_SIZE). Re-measure when the kernel changes.
 GATE_UP_TRAFFIC_BYTES = 12049 * 1024 * 2 + 18 * 1024
-# HBM bytes per decode token of the persistent kernel from the same calibrated PMC passes
-# (None until measured).
-PERSISTENT_TRAFFIC_BYTES_PER_TOKEN = None
+# HBM bytes per decode token of the persistent kernel from the same calibrated PMC passes over
+# the timed 256-token launch (364,187,679 KiB fetched x 1.9998, 82,357,669 KiB written, / 256).
+# Re-measure when the kernel changes.
+PERSISTENT_TRAFFIC_BYTES_PER_TOKEN = 3242644093
 
 
 def gate_up_bytes(cfg) -> int:
@@ -227,6 +231,8 @@ def main() -> int:
         return 0
 
     seconds, tokens = run_decode(engine, args, persistent)
+    if args.calibration_copy:
+        copy_calibration()
     tok_s = args.steps / seconds
     bytes_per_token = mean_decode_bytes(cfg, args.prompt_len, args.steps)
     achieved = bytes_per_token * tok_s

@@ -44,6 +44,8 @@
 #include "deltaforge_hip.h"
 #include "int4_block.h"
 
+#include <cstdlib>
+
 namespace df {
 namespace pd {
 
@@ -2113,6 +2115,18 @@ __global__ void register_reset_kernel(int* ctl) {
   if (threadIdx.x < kXcd) ctl[kRegBase + threadIdx.x] = 0;
 }
 
+// DF_PERSISTENT_PLAIN_LAUNCH=1 launches the decode kernel as an ordinary dispatch instead of a
+// cooperative one (read once per process). rocprofv3 cannot finish its trace of a process
+// that made cooperative launches (it faults at process exit before writing results), so
+// profiles of the decode kernel are taken with this set.
+inline bool plain_launch() {
+  static const bool v = [] {
+    const char* e = std::getenv("DF_PERSISTENT_PLAIN_LAUNCH");
+    return e && e[0] == '1';
+  }();
+  return v;
+}
+
 }  // namespace pd
 }  // namespace df
 
@@ -2150,6 +2164,20 @@ extern "C" int df_decode_persistent(const DfPersistModel* model, int steps, int 
   ws_layout(m.hidden, &w, reinterpret_cast<char*>(workspace));
   hipLaunchKernelGGL(register_reset_kernel, dim3(1), dim3(64), 0, stream, w.ctl);
   if (hipGetLastError() != hipSuccess) return DF_LAUNCH_FAILED;
+  if (plain_launch()) {
+    // an ordinary dispatch of the same grid: co-residency is checked here instead of by the
+    // cooperative launch (one workgroup per CU, every CU of the device), and a workgroup that
+    // never starts makes the others' hand-off waits time out into the abort word
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(decode_kernel), kThreads,
+                                                     0) != hipSuccess ||
+        cus * per_cu < kNwg)
+      return DF_LAUNCH_FAILED;
+    hipLaunchKernelGGL(decode_kernel, dim3(kNwg), dim3(kThreads), 0, stream, m, w, steps, teacher_forced);
+    return hipGetLastError() == hipSuccess ? DF_OK : DF_LAUNCH_FAILED;
+  }
   void* args[] = {&m, &w, &steps, &teacher_forced};
   const hipError_t e =
       hipLaunchCooperativeKernel(reinterpret_cast<const void*>(decode_kernel), dim3(kNwg), dim3(kThreads), args, 0, stream);

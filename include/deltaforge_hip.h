@@ -260,7 +260,9 @@ size_t df_decode_persistent_workspace_bytes(int hidden);
  * prompt[position] (prefill; token_log untouched); else the previous step's argmax
  * (greedy; appended to token_log). Either way the last argmax is left in tokens[0] and
  * position advances by `steps`. Needs all 256 workgroups co-resident (cooperative
- * launch); returns DF_LAUNCH_FAILED if the device cannot host them. */
+ * launch); returns DF_LAUNCH_FAILED if the device cannot host them. With the environment
+ * variable DF_PERSISTENT_PLAIN_LAUNCH=1 the same grid goes out as an ordinary dispatch
+ * (for profilers that cannot follow cooperative launches), after the same capacity check. */
 int df_decode_persistent(const DfPersistModel* model, int steps, int teacher_forced, void* workspace,
                          size_t workspace_bytes, hipStream_t stream);
 
