@@ -627,13 +627,15 @@ DF_DEVICE void seg_open(Stream& st, const DfPersistModel& M, const Geo& q, const
   }
 }
 
-// LDS DMA of 16 (or 4) bytes per lane: lane i's bytes land at lds_base + 16 i (4 i). Written
+// LDS DMA of 16 (or 4) bytes per lane: lane i's bytes land at lds_base + 16 i (4 i). The loads
+// are non-temporal (nt): each weight byte is used once per token, and streaming it through L2
+// as evict-first keeps the hand-off data, activations and cache rows resident. Written
 // as inline asm so the compiler does not track these loads: it would otherwise treat every
 // later LDS access of the wave as possibly aliasing a pending DMA and wait for all of them
 // (vmcnt(0)), draining the ring. The kernel orders ring reads itself (wait_blocks); the
 // compiler's own vmcnt waits only get stricter, never wrong, for loads it does not count.
 DF_DEVICE void dma16(const void* gaddr, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds_base)
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(gaddr), "s"(lds_base)
                : "memory", "m0");
 }
 // The scale DMA runs on lanes 0..15 only (the lanes that apply scales), 64 bytes per block.
@@ -645,7 +647,7 @@ DF_DEVICE void dma4_16(const void* gaddr, uint32_t lds_base) {
       "s_mov_b32 exec_hi, 0\n\t"
       "s_mov_b32 m0, %2\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dword %1, off\n\t"
+      "global_load_lds_dword %1, off nt\n\t"
       "s_mov_b64 exec, %0"
       : "=&s"(saved)
       : "v"(gaddr), "s"(lds_base)
@@ -1368,6 +1370,10 @@ DF_DEVICE void at_issue_k(const Ctx& c, LayerPtr Lp, int t0, int j1, AtPre& P) {
   const int col = c.lane & 15, slot = c.lane >> 4;
   const size_t base = (size_t)(c.xcd >> 1) * c.max_len;
   const int key = t0 + c.wave * 16 + col;
+  // defined on every path: a conditionally-set register array is a value the compiler carries
+  // around the whole layer loop (spilled across every other phase)
+#pragma unroll
+  for (int d = 0; d < 8; ++d) P.kb[d] = make_uint4(0u, 0u, 0u, 0u);
   if (key < j1 && key != c.pos) {
     GlobalBf16 kp = (GlobalBf16)LF(Lp, k_cache) + (base + key) * kHd + slot * 8;
 #pragma unroll
