@@ -217,4 +217,11 @@ _CHAMPIONS = (
 for _name, _impl, _op, _notes in _CHAMPIONS:
     REGISTRY.register(_name, impl=_impl, replaces=_op, status=KernelStatus.CHAMPION, notes=_notes)
 
+# Batch 1 only, and Qwen3.5-4B's head geometry only, so not the default champion of its
+# operation; REGISTRY.promote("hip_persistent_decode") before apply_champions selects it.
+REGISTRY.register(
+    "hip_persistent_decode", impl=_hip.persistent_decoder, replaces="decode_cache", status=KernelStatus.CANDIDATE,
+    notes="Every layer of every decode step in one persistent launch; the 8 XCDs act as 8 tensor-parallel "
+          "ranks (column-parallel projections, row-parallel out/down with a cross-XCD all-reduce).")
+
 register_checks("hip_tiled_gemv_int4", _hip.tiled_gemv_int4_checks)

@@ -250,3 +250,11 @@ def static_decode_engine(model, *, batch: int = 1, max_seq_len: int, device="cud
     from ..engine import DecodeEngine
 
     return DecodeEngine(model, batch=batch, max_seq_len=max_seq_len, device=device, max_new_tokens=max_new_tokens)
+
+
+def persistent_decoder(model, *, max_seq_len: int, device="cuda", max_new_tokens: int = 256):
+    """The ``decode_cache`` candidate for batch 1: a ``PersistentDecoder`` whose launches run
+    every layer of many decode steps inside one kernel (see ``deltaforge_amd.persistent``)."""
+    from ..persistent import PersistentDecoder
+
+    return PersistentDecoder(model, max_seq_len=max_seq_len, device=device, max_new_tokens=max_new_tokens)

@@ -24,6 +24,7 @@ __all__ = [
     "INSTALLERS",
     "EngineDecodeLoop",
     "InstallerMissing",
+    "PersistentDecodeLoop",
     "apply_champions",
     "greedy_decode",
     "register_installer",
@@ -176,6 +177,51 @@ def _install_decode_loop(model, entry: KernelEntry) -> None:
     _installed(model).add(entry.name)
 
 
+class PersistentDecodeLoop:
+    """``model.decode_loop`` for batch 1: prefill and greedy decode each run in one persistent
+    launch of ``df_decode_persistent`` (every layer of every step inside one kernel), in a
+    ``PersistentDecoder`` sized for the request. Batch > 1 raises ``ValueError``: the
+    persistent kernel decodes one sequence."""
+
+    def __init__(self, device: str | torch.device = "cuda") -> None:
+        self.device = torch.device(device)
+        self.decoder = None
+
+    def __call__(self, model, input_ids: torch.Tensor, max_new_tokens: int, cache=None) -> torch.Tensor:
+        from .persistent import PersistentDecoder
+
+        if input_ids.dim() != 2 or input_ids.dtype != torch.int64:
+            raise ValueError(f"input_ids must be int64 [B, P], got {input_ids.dtype} {tuple(input_ids.shape)}")
+        batch, plen = input_ids.shape
+        if batch != 1:
+            raise ValueError(f"the persistent decode loop runs batch 1, got batch {batch}")
+        need = plen + max_new_tokens + 1
+        d = self.decoder
+        if d is None or d.max_seq_len < need or d.max_new_tokens < max_new_tokens:
+            d = PersistentDecoder(model, max_seq_len=need, device=self.device, max_new_tokens=max_new_tokens)
+            self.decoder = d
+        d.prefill(input_ids.to(self.device))
+        first = d.tokens.clone()  # argmax after the last prompt token
+        if max_new_tokens > 1:
+            d.decode(max_new_tokens - 1)
+        d.check()
+        generated = torch.cat((first.view(1, 1), d.token_log[:, : max_new_tokens - 1]), dim=1)
+        return generated.to(input_ids.device)
+
+
+def _install_persistent_loop(model, entry: KernelEntry) -> None:
+    """The persistent kernel replaces the whole step, so it needs none of ``STEP_KERNELS``; it
+    takes the decode loop over from any other ``decode_cache`` implementation."""
+    from .persistent import check_geometry
+
+    try:
+        check_geometry(model.config)
+    except ValueError as e:
+        raise ValueError(f"{entry.name} does not support this model: {e}") from None
+    model.decode_loop = PersistentDecodeLoop()
+    _installed(model).add(entry.name)
+
+
 register_installer("hip_tiled_gemv_int4", _install_gemv)
 register_installer("hip_silu_mul", _install_marker)
 register_installer("hip_rms_norm", _install_marker)
@@ -185,3 +231,4 @@ register_installer("hip_causal_conv_step", _install_delta)
 register_installer("hip_gated_delta_decode", _install_delta)
 register_installer("hip_gated_attention_decode", _install_attention)
 register_installer("hip_decode_engine", _install_decode_loop)
+register_installer("hip_persistent_decode", _install_persistent_loop)

@@ -22,7 +22,7 @@ from . import ops
 from .config import FULL_ATTENTION, SIGMOID_GATE, ModelConfig
 from .synth import SynthModel, inv_freq
 
-__all__ = ["PersistentDecoder", "attention_proj_columns", "linear_proj_columns"]
+__all__ = ["PersistentDecoder", "attention_proj_columns", "check_geometry", "linear_proj_columns"]
 
 BF16 = torch.bfloat16
 XCD = 8
@@ -74,7 +74,7 @@ def _select_cols(packed: torch.Tensor, scale: torch.Tensor, cols: torch.Tensor):
     return p.contiguous(), s.contiguous()
 
 
-def _check_geometry(c: ModelConfig) -> None:
+def check_geometry(c: ModelConfig) -> None:
     ok = (c.linear_num_key_heads == 16 and c.linear_num_value_heads == 32 and c.linear_key_head_dim == 128
           and c.linear_value_head_dim == 128 and c.num_attention_heads == 16 and c.num_key_value_heads == 4
           and c.head_dim == 256 and c.rotary_dim == 64 and c.linear_conv_kernel_dim == 4)
@@ -91,7 +91,7 @@ class PersistentDecoder:
     def __init__(self, model: SynthModel, *, max_seq_len: int, device: str | torch.device = "cuda",
                  max_new_tokens: int = 256) -> None:
         c = model.config
-        _check_geometry(c)
+        check_geometry(c)
         if c.output_gate_type not in (SIGMOID_GATE, "swish"):
             raise ValueError(f"unknown gate {c.output_gate_type}")
         self.config = c

@@ -116,6 +116,45 @@ def test_apply_champions_installs_the_decode_loop():
         greedy_decode(model, torch.zeros((1, 4), dtype=torch.int64), 0)
 
 
+def _promoted_persistent_registry() -> KernelRegistry:
+    """A copy of the shipped registry with the persistent decoder promoted (the global one is
+    left as shipped)."""
+    reg = KernelRegistry()
+    for e in REGISTRY:
+        reg.register(e.name, impl=e.impl, replaces=e.replaces, status=e.status, notes=e.notes)
+    reg.promote("hip_persistent_decode")
+    return reg
+
+
+def test_persistent_decoder_is_a_decode_cache_candidate():
+    e = REGISTRY.get("hip_persistent_decode")
+    assert e.replaces == "decode_cache" and e.status is KernelStatus.CANDIDATE
+    assert "hip_persistent_decode" in INSTALLERS
+
+
+def test_promoted_persistent_decoder_installs_its_loop_and_refuses_batches():
+    from deltaforge_amd.model import PersistentDecodeLoop
+    from deltaforge_amd.synth import synth_model
+
+    model = synth_model(mid_config(num_layers=4), seed=0)
+    reg = _promoted_persistent_registry()
+    applied = apply_champions(model, reg)
+    assert "hip_persistent_decode" in applied and "hip_decode_engine" not in applied
+    assert isinstance(model.decode_loop, PersistentDecodeLoop)
+    with pytest.raises(ValueError, match="batch 1"):
+        greedy_decode(model, torch.zeros((2, 4), dtype=torch.int64), 2)
+
+
+def test_persistent_installer_refuses_other_head_geometry():
+    from deltaforge_amd.config import tiny_config
+    from deltaforge_amd.synth import synth_model
+
+    model = synth_model(tiny_config(), seed=0)
+    with pytest.raises(ValueError, match="hip_persistent_decode does not support"):
+        INSTALLERS["hip_persistent_decode"](model, REGISTRY.get("hip_persistent_decode"))
+    assert getattr(model, "decode_loop", None) is None
+
+
 def test_greedy_decode_without_loop_fails_loudly():
     class Bare:
         pass

@@ -121,3 +121,24 @@ def test_persistent_prefill_across_launches_and_determinism(mid):
     dec.decode(4)
     dec.check()
     assert torch.equal(dec.logits, one[0]) and torch.equal(dec.token_log[0, :4], one[1])
+
+
+def test_greedy_decode_through_the_promoted_persistent_candidate(mid):
+    """The reference plugin surface: promote ``hip_persistent_decode``, ``apply_champions``,
+    ``greedy_decode`` (reference model.py:108-148), twice (the decoder is reused)."""
+    from deltaforge_amd.kernels import REGISTRY, KernelRegistry
+    from deltaforge_amd.model import PersistentDecodeLoop, apply_champions, greedy_decode
+
+    cfg, model, prompt, ref_tokens, _ = mid
+    reg = KernelRegistry()
+    for e in REGISTRY:
+        reg.register(e.name, impl=e.impl, replaces=e.replaces, status=e.status, notes=e.notes)
+    reg.promote("hip_persistent_decode")
+    apply_champions(model, reg)
+    assert isinstance(model.decode_loop, PersistentDecodeLoop)
+    got = greedy_decode(model, prompt, 6)
+    print(f"greedy_decode (persistent) {got.tolist()}, oracle {ref_tokens[0, :6].tolist()}", flush=True)
+    assert got.shape == (1, 6) and got.device == prompt.device
+    assert got[0, :4].tolist() == ref_tokens[0, :4].tolist()
+    again = greedy_decode(model, prompt, 6)
+    assert torch.equal(again, got)
