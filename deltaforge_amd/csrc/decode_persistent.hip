@@ -57,7 +57,7 @@ constexpr int kCtl = kCompute;                      // wave index of the control
 constexpr int kThreads = (kCompute + 1) * 64;       // 576
 constexpr int kMaxHidden = 2560;
 #ifndef DF_RING
-#define DF_RING 11
+#define DF_RING 8
 #endif
 constexpr int kRing = DF_RING;                      // weight blocks in flight per compute wave
 constexpr int kMaxWgTiles = 8;                      // output tiles of a workgroup's GEMV range
@@ -526,105 +526,101 @@ DF_DEVICE int head_tiles_of_wave(const Geo& q, int wave) {
   return n > 0 ? (n + kCompute - 1) / kCompute : 0;
 }
 
-// A compute wave's weight stream. The issue cursor is the next block's weight and scale
-// addresses; a segment (one (layer, phase) or the head, of token `istep` of the launch) is
-// a run of blocks whose addresses advance by one block, with a jump of `wjump` blocks after
-// every `ng`-group tile run (row-parallel slices and the head's strided tiles).
+// A compute wave's weight stream: the wave's 1 KB blocks of every GEMV phase of every layer
+// and then of the head, in consumption order, as a list of runs (blocks contiguous in HBM)
+// built once per launch in LDS. The same list serves every token of the launch.
+//
+// Run descriptor: w = weights of the first block | (blocks << 48), s = its scales | hold << 63
+// (hold: the first run of an attention layer's o_proj; the stream stops there until the
+// layer's KV-cache loads are consumed, because they share the wave's in-order vmcnt).
+struct RunDesc {
+  uint64_t w, s;
+};
+constexpr int kMaxRuns = 200;  // per wave and token: 6 per layer (<= 2 per row-parallel phase) + the head's tiles
+constexpr uint64_t kPtrMask = (1ull << 48) - 1;
+__shared__ __align__(16) RunDesc g_runs[kCompute][kMaxRuns];
+
 struct Stream {
   const uint8_t* wp;     // weights of the next block to issue (lane 0's 16 bytes)
   const uint16_t* sp;    // its 16 scales
-  int g, ng, wjump;      // position in the tile run, groups per run, blocks skipped after a run
-  int left;              // blocks left in the segment
+  int left;              // blocks left in the current run
+  int ri, nruns;         // next run to open, runs per token
   int issued, consumed;  // blocks, since the launch began
   int wslot, rslot;      // ring slots of the next issue / the next consume
   int state;             // 0 streaming, 1 held before an attention layer's o_proj,
                          // 2 released, 3 past the launch's last block
-  int li, k, istep;      // segment of the cursor: layer, phase (0..3; 4 = head), token
-  uint32_t kinds;        // bit li: layer li is an attention layer
+  int istep;             // token of the cursor
 };
-
-// Per compute wave, where its share of each phase starts, for either layer kind (index
-// kind * 4 + phase) and for the head (index 8): {first block relative to the phase's
-// weights, run position | groups per run << 16, blocks skipped after a run, blocks}. The
-// same for every layer of a kind, so opening a segment only adds the layer's pointers.
-constexpr int kDescs = 9;
-__shared__ __align__(16) int4 g_desc[kCompute][kDescs];
 
 enum StreamState : int { kStreaming = 0, kHeld = 1, kReleased = 2, kDone = 3 };
 
-// Compute waves, once per launch: this wave's row of g_desc (lane i < kDescs fills entry i).
-DF_DEVICE void desc_init(const Geo& q, const Ctx& c) {
-  if (c.lane < kDescs) {
-    int4 d = make_int4(0, 0, 0, 0);
-    if (c.lane == 8) {
-      const int ntw = head_tiles_of_wave(q, c.wave);
-      d = make_int4((q.t_lo + c.wave) * q.Gh, q.Gh << 16, (kCompute - 1) * q.Gh, ntw * q.Gh);
-    } else {
-      const Gemv g = gemv_geom(c.lane >> 2, q, c.lane & 3, c.xcd, c.r);
-      int lo, n;
-      wave_range(g, c.wave, lo, n);
-      if (n > 0)
-        d = make_int4((g.tile0 + lo / g.ng) * g.G + g.g0 + lo % g.ng, (lo % g.ng) | (g.ng << 16), g.G - g.ng, n);
+// Compute waves, once per launch: this wave's run list (lane 0 writes it; the wave's LDS
+// accesses complete in order, so its own later reads see it). Returns the runs per token.
+DF_DEVICE int build_runs(const DfPersistModel& M, const Geo& q, const Ctx& c) {
+  int n = 0;
+  auto put = [&](const uint8_t* w, const uint16_t* sc, int blocks, bool hold) {
+    if (c.lane == 0 && n < kMaxRuns)
+      g_runs[c.wave][n] = RunDesc{reinterpret_cast<uint64_t>(w) | (static_cast<uint64_t>(blocks) << 48),
+                                  reinterpret_cast<uint64_t>(sc) | (hold ? 1ull << 63 : 0ull)};
+    n += 1;
+  };
+  bool hold = false;  // pending until the next run (a wave with no o_proj blocks holds at gate|up)
+  for (int li = 0; li < M.num_layers; ++li) {
+    const int kind = LKIND(&g_layers[li]) & 1;
+    for (int k = 0; k < 4; ++k) {
+      const Gemv g = gemv_of(&g_layers[li], q, k, c.xcd, c.r);
+      int lo, cnt;
+      wave_range(g, c.wave, lo, cnt);
+      hold = hold || (kind == 1 && k == 1);
+      // blocks lo .. lo + cnt of the slice (tile-major, ng groups per tile): a tile's run is
+      // contiguous, and so are consecutive tiles when the slice spans every group
+      while (cnt > 0) {
+        const int t = lo / g.ng, gi = lo % g.ng;
+        const int len = g.ng == g.G ? cnt : min(cnt, g.ng - gi);
+        const size_t blk = (size_t)(g.tile0 + t) * g.G + g.g0 + gi;
+        put(g.w + blk * kBlockBytes, g.s + blk * kTileCols, len, hold);
+        hold = false;
+        lo += len;
+        cnt -= len;
+      }
     }
-    g_desc[c.wave][c.lane] = d;
   }
+  const int ntw = head_tiles_of_wave(q, c.wave);
+  for (int j = 0; j < ntw; ++j) {
+    const size_t blk = (size_t)(q.t_lo + c.wave + j * kCompute) * q.Gh;
+    put(M.head_w + blk * kBlockBytes, M.head_s + blk * kTileCols, q.Gh, hold);
+    hold = false;
+  }
+  // Every geometry the launcher accepts fits: per layer at most 1 run each for the
+  // column-parallel phases and 2 for each row-parallel one (a wave's share of out_proj /
+  // o_proj is at most 3 blocks of 4-group runs, of down at most 5/8 of a run of ngx blocks),
+  // and at most 8 head tiles per wave (64 per workgroup), so 6 x 32 + 8 = kMaxRuns.
+  return min(n, kMaxRuns);
 }
 
-// Position the cursor on the first block of the current segment, skipping empty segments;
-// stop at an attention layer's o_proj (until released) and after the last token.
-DF_DEVICE void seg_open(Stream& st, const DfPersistModel& M, const Geo& q, const Ctx& c, int steps) {
-  for (;;) {
-    int di;
-    const uint8_t* wb;
-    const uint16_t* sb;
-    if (st.k == 4) {
-      di = 8;
-      wb = M.head_w;
-      sb = M.head_s;
-    } else {
-      const int kind = (st.kinds >> st.li) & 1;
-      if (st.k == 1 && kind == 1) {
-        if (st.state == kStreaming) {
-          st.state = kHeld;
-          return;
-        }
-        st.state = kStreaming;
-      }
-      di = kind * 4 + st.k;
-      phase_ptrs(st.li, st.k, wb, sb);
-    }
-    const int4 dv = g_desc[c.wave][di];
-    const int left = uniform_int(dv.w);
-    if (left > 0) {
-      const int blk = uniform_int(dv.x), gpos = uniform_int(dv.y);
-      st.wp = wb + (size_t)blk * kBlockBytes;
-      st.sp = sb + (size_t)blk * kTileCols;
-      st.g = gpos & 0xFFFF;
-      st.ng = gpos >> 16;
-      st.wjump = uniform_int(dv.z);
-      st.left = left;
+// Open the next run (the cursor's run is exhausted): stop at a hold run unless released,
+// wrap to the next token's first run, stop after the launch's last token.
+DF_DEVICE void open_run(Stream& st, int steps) {
+  if (st.ri == st.nruns) {
+    st.istep += 1;
+    if (st.istep >= steps) {
+      st.state = kDone;
       return;
     }
-    // next segment
-    if (st.k < 3) {
-      st.k += 1;
-    } else if (st.k == 3) {
-      if (st.li + 1 < M.num_layers) {
-        st.li += 1;
-        st.k = 0;
-      } else {
-        st.k = 4;
-      }
-    } else {
-      st.istep += 1;
-      if (st.istep >= steps) {
-        st.state = kDone;
-        return;
-      }
-      st.li = 0;
-      st.k = 0;
-    }
+    st.ri = 0;
   }
+  const uint4 d = *reinterpret_cast<const uint4*>(&g_runs[__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)][st.ri]);
+  const uint64_t w = (static_cast<uint64_t>(uniform_int(static_cast<int>(d.y))) << 32) | static_cast<uint32_t>(uniform_int(static_cast<int>(d.x)));
+  const uint64_t sc = (static_cast<uint64_t>(uniform_int(static_cast<int>(d.w))) << 32) | static_cast<uint32_t>(uniform_int(static_cast<int>(d.z)));
+  if ((sc >> 63) && st.state == kStreaming) {
+    st.state = kHeld;
+    return;
+  }
+  st.state = kStreaming;
+  st.wp = reinterpret_cast<const uint8_t*>(w & kPtrMask);
+  st.sp = reinterpret_cast<const uint16_t*>(sc & kPtrMask);
+  st.left = static_cast<int>(w >> 48);
+  st.ri += 1;
 }
 
 // LDS DMA of 16 (or 4) bytes per lane: lane i's bytes land at lds_base + 16 i (4 i). The loads
@@ -654,44 +650,27 @@ DF_DEVICE void dma4_16(const void* gaddr, uint32_t lds_base) {
       : "memory", "m0");
 }
 
-// Issue the cursor's block into the next ring slot (weights + scales) and advance.
-DF_DEVICE void issue_one(Stream& st, const DfPersistModel& M, const Geo& q, const Ctx& c, int steps) {
+// Issue the cursor's block into the next ring slot (weights + scales) and advance. Every
+// block is two vector memory operations, weights then scales: the consumer's vmcnt waits
+// count on it.
+DF_DEVICE void issue_one(Stream& st, const Ctx& c) {
   dma16(st.wp + c.lane * 16, lds_addr(&g_ring_w[c.wave][st.wslot][0]));
   dma4_16(st.sp + (c.lane & 14), lds_addr(&g_ring_s[c.wave][st.wslot][0]));
   st.issued += 1;
   st.wslot = st.wslot + 1 == kRing ? 0 : st.wslot + 1;
-  int adv = 1;
-  if (++st.g == st.ng) {
-    st.g = 0;
-    adv += st.wjump;
-  }
-  st.wp += (size_t)adv * kBlockBytes;
-  st.sp += (size_t)adv * kTileCols;
-  if (--st.left == 0) {
-    if (st.k < 3) {
-      st.k += 1;
-    } else if (st.k == 3) {
-      if (st.li + 1 < M.num_layers) {
-        st.li += 1;
-        st.k = 0;
-      } else {
-        st.k = 4;
-      }
-    } else {
-      st.istep += 1;
-      if (st.istep >= steps) {
-        st.state = kDone;
-        return;
-      }
-      st.li = 0;
-      st.k = 0;
-    }
-    seg_open(st, M, q, c, steps);
-  }
+  st.wp += kBlockBytes;
+  st.sp += kTileCols;
+  st.left -= 1;
 }
 
-DF_DEVICE void fill(Stream& st, const DfPersistModel& M, const Geo& q, const Ctx& c, int steps) {
-  while (st.state == kStreaming && st.issued - st.consumed < kRing) issue_one(st, M, q, c, steps);
+DF_DEVICE void fill(Stream& st, int steps, const Ctx& c) {
+  while (st.state == kStreaming && st.issued - st.consumed < kRing) {
+    if (st.left == 0) {
+      open_run(st, steps);
+      continue;
+    }
+    issue_one(st, c);
+  }
 }
 
 // Wait for the oldest `need` pending blocks (need = 1 or 2). The ring is full except while
@@ -854,7 +833,7 @@ DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPer
     take_pair(st, c, xb + gl * kGroup, xb + gl1 * kGroup, &L.xs[gl], &L.xs[gl1], in);
     const float v0 = block_dot_r(in.w0, in.s0, in.x0, in.xs0, sh);
     const float v1 = block_dot_r(in.w1, in.s1, in.x1, in.xs1, sh);
-    fill(st, M, q, c, steps);
+    fill(st, steps, c);
     add(v0);
     add(v1);
   }
@@ -863,7 +842,7 @@ DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPer
     uint32_t s0;
     take_block(st, c, w0, s0);
     add(block_dot(w0, s0, xb + gl * kGroup, L.xs[gl], c.lane));
-    fill(st, M, q, c, steps);
+    fill(st, steps, c);
   }
   if (n > 0 && gl != 0 && c.lane < 16) L.part[tr][c.wave][c.lane] = acc;
 }
@@ -1522,15 +1501,12 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
   Stream st;
   st.wp = nullptr;
   st.sp = nullptr;
-  st.g = st.ng = st.wjump = st.left = 0;
+  st.left = 0;
   st.issued = st.consumed = st.wslot = st.rslot = 0;
-  st.li = st.k = st.istep = 0;
+  st.ri = st.istep = 0;
   st.state = kStreaming;
-  st.kinds = 0;
-  for (int li = 0; li < M.num_layers; ++li) st.kinds |= static_cast<uint32_t>(LKIND(&g_layers[li]) & 1) << li;
-  desc_init(q, c);  // a wave's LDS accesses complete in order: its own row reads back as written
-  seg_open(st, M, q, c, steps);
-  fill(st, M, q, c, steps);
+  st.nruns = build_runs(M, q, c);
+  fill(st, steps, c);
   auto stop = [&]() { __builtin_amdgcn_s_waitcnt(0); };
 
   for (int step = 0; step < steps; ++step) {
@@ -1630,8 +1606,8 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         // the weight stream resumes with o_proj
         if (st.state == kHeld) {
           st.state = kReleased;
-          seg_open(st, M, q, c, steps);
-          fill(st, M, q, c, steps);
+          open_run(st, steps);
+          fill(st, steps, c);
         }
         // combine the waves' PV partials (into wave 0's row)
 #pragma unroll
@@ -1699,7 +1675,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         take_pair(st, c, xb + gl * kGroup, xb + (gl + 1) * kGroup, &L.xs[gl], &L.xs[gl + 1], in);
         const float v0 = block_dot_r(in.w0, in.s0, in.x0, in.xs0, sh);
         const float v1 = block_dot_r(in.w1, in.s1, in.x1, in.xs1, sh);
-        fill(st, M, q, c, steps);
+        fill(st, steps, c);
         acc += v0;
         acc += v1;
         gl += 2;
