@@ -281,9 +281,6 @@ struct Lds {
       float acc[kPerXcd][16];
       float gate[16];
     } mg;
-    struct {                                     // all-reduce slice
-      float y[kXcd][128];
-    } rd;
     struct {                                     // down: the XCD's gate|up column sums
       __align__(16) float gu[kColparMax];
     } ac;
@@ -352,9 +349,8 @@ struct Geo {
 enum Tag : int { kTProj = 1, kTDelta, kTOut, kTAttn, kTMerge, kTOProj, kTGateUp, kTDown, kTHead, kTEmbed,
                  kTReduce, kTStaged = 20, kTSignal = 30 };
 DF_DEVICE void stamp(Ctx& c, int tag) {
-  if (c.tr) {
-    if (c.control && c.lane == 0 && c.xcd == 0 && c.r == 0 && c.tn < c.tcap)
-      c.tr[c.tn] = (now() << 8) | static_cast<uint64_t>(tag);
+  if (__builtin_expect(c.tr != nullptr, 0)) {  // only workgroup (0, 0)'s control wave, traced step
+    if (c.lane == 0 && c.tn < c.tcap) c.tr[c.tn] = (now() << 8) | static_cast<uint64_t>(tag);
     c.tn += 1;
   }
 }
@@ -1056,30 +1052,26 @@ DF_DEVICE void rowpar_epilogue(const Gemv& g, const Ctx& c, const Lds& L, int hi
 // compute waves.
 DF_DEVICE bool allreduce_residual(Ctx& c, Lds& L, int hidden) {
   fence(c, kTReduce);
-  const int ns = hidden / kPerXcd;  // <= 80
+  const int ns = hidden / kPerXcd;  // columns of this workgroup's slice: even, <= 80
   const int sl0 = c.r * ns;
-  const uint64_t* rp = c.w.rowpar + (size_t)(c.ar & 1) * kXcd * hidden;
+  const auto r = rsrc(c.w.rowpar + (size_t)(c.ar & 1) * kXcd * hidden);
   const uint32_t want = c.epoch;
   c.ar += 1;
   c.epoch += 1;
-  // slice [sl0, sl0 + ns) of the 8 XCD partials: item i = (x = i / ns, column i % ns)
-  constexpr int K = (kXcd * (kMaxHidden / kPerXcd) + 63) / 64;
-  const auto r = rsrc(rp);
-  const int items = kXcd * ns;
-  uint64_t v[K];
+  // lane l < ns / 2 owns columns sl0 + 2 l, + 1: one 16-byte load per XCD holds both
+  // (value, epoch) pairs, so the sum over XCDs stays in registers
+  const bool mine = 2 * c.lane < ns;
+  const int off = (sl0 + 2 * c.lane) * 8;
+  uint4 v[kXcd];
   bool ok = true;
   const uint64_t t0 = now();
   for (int it = 1;; ++it) {
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int i = c.lane + 64 * k;
-      if (i < items) v[k] = ld8<kCpSystem>(r, ((i / ns) * hidden + sl0 + i % ns) * 8);
-    }
     bool ready = true;
+    if (mine) {
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int i = c.lane + 64 * k;
-      if (i < items) ready = ready && static_cast<uint32_t>(v[k] >> 32) == want;
+      for (int x = 0; x < kXcd; ++x) v[x] = ld16<kCpSystem>(r, x * hidden * 8 + off);
+#pragma unroll
+      for (int x = 0; x < kXcd; ++x) ready = ready && v[x].y == want && v[x].w == want;
     }
     if (__all(ready)) break;
     if ((it & 31) == 0 && ld_sys(c.w.ctl + 1)) { ok = false; break; }
@@ -1087,18 +1079,19 @@ DF_DEVICE bool allreduce_residual(Ctx& c, Lds& L, int hidden) {
     __builtin_amdgcn_s_sleep(1);
   }
   if (!ok) return false;
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int i = c.lane + 64 * k;
-    if (i < items) L.u.rd.y[i / ns][i % ns] = __uint_as_float(static_cast<uint32_t>(v[k]));
-  }
   uint16_t* hx = c.w.hloc + (size_t)c.xcd * hidden;
-  for (int j = c.lane; j < ns; j += 64) {
-    float y = 0.0f;
+  if (mine) {
+    float y0 = 0.0f, y1 = 0.0f;
 #pragma unroll
-    for (int x = 0; x < kXcd; ++x) y += L.u.rd.y[x][j];
-    const int k = sl0 + j;
-    hx[k] = f2bf(bf2f(L.h[k]) + round_bf(y));
+    for (int x = 0; x < kXcd; ++x) {  // XCD order
+      y0 += __uint_as_float(v[x].x);
+      y1 += __uint_as_float(v[x].z);
+    }
+    const int k = sl0 + 2 * c.lane;
+    const uint32_t hv = *reinterpret_cast<const uint32_t*>(&L.h[k]);
+    const uint16_t b0 = f2bf(__uint_as_float(hv << 16) + round_bf(y0));
+    const uint16_t b1 = f2bf(__uint_as_float(hv & 0xFFFF0000u) + round_bf(y1));
+    *reinterpret_cast<uint32_t*>(hx + k) = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
   }
   signal_local(c, c.epoch);
   if (!wait_local(c, c.epoch)) return false;
@@ -1306,12 +1299,16 @@ DF_DEVICE void norm_rope4_lds(float x[4], const uint16_t* nw, float eps, const f
 #pragma unroll
   for (int i = 0; i < 4; ++i) partner[i] = dpp<kDppRor8>(n[i]);  // lane ^ 8 = (lane + 8) mod 16 in a row
   static_assert(half / 4 == 8, "the partner of a rotary dim is 8 lanes away");
+  // lane j < half holds the angle of rotary pair j (one cosf / sinf per lane instead of one
+  // per element: the library's argument reduction is large code); lane 4l + i's element reads
+  // pair (4l + i) % half from there
+  const float ang = posf * inv[lane & (half - 1)];
+  const float cs_l = round_bf(cosf(ang)), sn_l = round_bf(sinf(ang));
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int dim = lane * 4 + i;
+    const float cs = __shfl(cs_l, dim & (half - 1), 64), sn = __shfl(sn_l, dim & (half - 1), 64);
     if (dim < kRot) {
-      const float ang = posf * inv[dim % half];
-      const float cs = round_bf(cosf(ang)), sn = round_bf(sinf(ang));
       const float rotated = dim < half ? -partner[i] : partner[i];
       x[i] = round_bf(round_bf(n[i] * cs) + round_bf(rotated * sn));
     } else {
@@ -1726,7 +1723,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
 
   for (int step = 0; step < steps; ++step) {
     c.pos = pos0 + step;
-    c.tr = (M.trace && step == M.trace_step) ? M.trace : nullptr;
+    c.tr = (M.trace && step == M.trace_step && c.xcd == 0 && c.r == 0) ? M.trace : nullptr;
     c.tn = 0;
     c.nb = 0;
     // ---- embedding of the step's token into L.h ---------------------------------------
