@@ -233,7 +233,8 @@ __shared__ __align__(16) uint16_t g_x[kMaxHidden + 8];            // GEMV input 
 
 struct Lds {
   __align__(16) uint16_t h[kMaxHidden];          // the hidden vector (bf16)
-  __align__(16) uint16_t nw[kMaxHidden];         // staged norm weight
+  __align__(16) uint16_t nw[kMaxHidden];         // the next RMSNorm's weight (LDS DMA, a phase ahead)
+  __align__(16) uint16_t gnw[kDk];               // GatedRMSNorm weight (LDS DMA, a phase ahead)
   float xs[kMaxGroups];                          // 136 * sum of each 128-group of g_x
   float part[kMaxWgTiles][kCompute][16];         // per-wave tile partials
   float red[64];
@@ -630,6 +631,10 @@ DF_DEVICE void dma16(const void* gaddr, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(gaddr), "s"(lds_base)
                : "memory", "m0");
 }
+DF_DEVICE void dma4(const void* gaddr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off nt" ::"v"(gaddr), "s"(lds_base)
+               : "memory", "m0");
+}
 // The scale DMA runs on lanes 0..15 only (the lanes that apply scales), 64 bytes per block.
 DF_DEVICE void dma4_16(const void* gaddr, uint32_t lds_base) {
   uint64_t saved;
@@ -886,25 +891,18 @@ DF_DEVICE void stage16(uint16_t* dst, const uint16_t* src, int n, int lane) {
 }
 constexpr int kHidChunks = (kMaxHidden / 8 + 63) / 64;  // 16-byte chunks per lane of a hidden row
 
-// Control wave: the next GEMV phase's norm weight, loaded a phase ahead (after the current
-// phase's signal, so the load overlaps the next hand-off instead of delaying either).
-struct NormPre {
-  uint4 v[kHidChunks];
-};
-DF_DEVICE void norm_fetch(NormPre& p, const uint16_t* src, int n, int lane) {
-  const auto r = rsrc(src);
-#pragma unroll
-  for (int k = 0; k < kHidChunks; ++k) {
-    const int ch = lane + 64 * k;
-    if (ch * 8 < n) p.v[k] = ld16<kCpPlain>(r, ch * 16);
-  }
+// Control wave: parameter rows copied into LDS by DMA a phase ahead of their use, issued
+// while the compute waves consume so the loads are done before the next hand-off wait (the
+// wave's vector memory operations complete in order). Their consumers run after a later
+// vmcnt(0) of the control wave (a hand-off poll) and a barrier.
+DF_DEVICE void dma4(const void* gaddr, uint32_t lds_base);
+// n bf16 (n % 512 == 0), 16 bytes per lane per DMA.
+DF_DEVICE void dma_row(const uint16_t* src, uint16_t* dst, int n, int lane) {
+  for (int k = 0; k * 512 < n; ++k) dma16(src + k * 512 + lane * 8, lds_addr(dst + k * 512));
 }
-DF_DEVICE void norm_put(const NormPre& p, uint16_t* dst, int n, int lane) {
-#pragma unroll
-  for (int k = 0; k < kHidChunks; ++k) {
-    const int ch = lane + 64 * k;
-    if (ch * 8 < n) *reinterpret_cast<uint4*>(dst + ch * 8) = p.v[k];
-  }
+// 128 bf16 (256 bytes), 4 bytes per lane.
+DF_DEVICE void dma_row128(const uint16_t* src, uint16_t* dst, int lane) {
+  dma4(src + lane * 2, lds_addr(dst));
 }
 
 // A run of XCD-local columns [j0, j0 + n) of the column-parallel outputs (j0, n multiples of
@@ -1542,7 +1540,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           const int h = i >> 7;
           const float tot = L.red[2 * h] + L.red[2 * h + 1];
           const float rr = 1.0f / sqrtf(tot / 128.0f + M.eps);
-          const float t = round_bf(bf2f(L.nw[i & 127]) * round_bf(v * rr));
+          const float t = round_bf(bf2f(L.gnw[i & 127]) * round_bf(v * rr));
           const uint16_t xb = f2bf(t * silu(L.u.on.z[i]));
           g_x[i] = xb;
           const float gs = dsum(bf2f(xb));
@@ -1714,8 +1712,8 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
   const int pos0 = *M.position;
   const int step0 = M.step ? *M.step : 0;
   int64_t token = M.tokens[0];
-  NormPre np;
-  norm_fetch(np, LF(layer_at(M, 0), in_norm), hidden, c.lane);
+  dma_row(LF(layer_at(M, 0), in_norm), L.nw, hidden, c.lane);
+  float pre_inv = 0.0f;  // inv_freq of the next attention layer's RoPE
   auto fail = [&](int nbars) {  // pass the barriers the compute waves still wait at, then stop
     if (c.lane == 0) L.ok = 0;
     for (int i = 0; i < nbars; ++i) bar();
@@ -1773,14 +1771,23 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       {
         fence(c, kTProj);
         const Gemv g = gemv_of(Lp, q, 0, c.xcd, c.r);
-        norm_put(np, L.nw, hidden, c.lane);  // in_norm (h is already in LDS)
+        wait_vm<0>();  // in_norm in L.nw (h is already in LDS)
         sync(c);
         for (int i = 0; i < kNormBars; ++i) sync(c);
+        // the next phase's small parameters, while the compute waves consume
+        if (kind == 0) {
+          dma_row128(LF(Lp, gnorm_w), L.gnw, c.lane);
+        } else {
+          dma_row128(LF(Lp, q_norm), L.u.at.qn_w, c.lane);
+          dma_row128(LF(Lp, q_norm) + 128, L.u.at.qn_w + 128, c.lane);
+          dma_row128(LF(Lp, k_norm), L.u.at.kn_w, c.lane);
+          dma_row128(LF(Lp, k_norm) + 128, L.u.at.kn_w + 128, c.lane);
+          pre_inv = c.lane < kRot / 2 ? M.inv_freq[c.lane] : 0.0f;
+        }
         sync(c);  // blocks consumed
         c.epoch += 1;
         colpar_epilogue(g, c, L);
         signal_local(c, c.epoch);
-        norm_fetch(np, LF(Lp, post_norm), hidden, c.lane);
       }
       if (kind == 0) {
         // ================= conv + gated delta step ===================================
@@ -1805,9 +1812,9 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           stage16<1, kCpAgent>(g_x, c.w.core + (size_t)c.xcd * 512, 512, c.lane);
           const Seg seg[1] = {{kLinZ, 512, L.u.on.z}};
           gather_colpar<1, 2>(c, seg);
-          stage16<1, kCpPlain>(L.nw, LF(Lp, gnorm_w), kDk, c.lane);
           sync(c);
           stamp(c, kTStaged);
+          dma_row(LF(Lp, post_norm), L.nw, hidden, c.lane);
           sync(c);
           sync(c);
           sync(c);  // g_x, group sums
@@ -1824,9 +1831,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         {
           const Seg seg[3] = {{0, kHd, A.qraw[0]}, {512, kHd, A.qraw[1]}, {kAttnK, 2 * kHd, A.kraw}};
           gather_colpar<3, 4>(c, seg);  // kraw and vraw are adjacent in LDS
-          stage16<1, kCpPlain>(A.qn_w, LF(Lp, q_norm), kHd, c.lane);
-          stage16<1, kCpPlain>(A.kn_w, LF(Lp, k_norm), kHd, c.lane);
-          if (c.lane < kRot / 2) A.inv[c.lane] = M.inv_freq[c.lane];
+          if (c.lane < kRot / 2) A.inv[c.lane] = pre_inv;
           if (c.lane < 2) {
             A.ml[c.lane][0] = -INFINITY;
             A.ml[c.lane][1] = 0.0f;
@@ -1902,6 +1907,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           stage_core(L, c);
           sync(c);
           stamp(c, kTStaged);
+          dma_row(LF(Lp, post_norm), L.nw, hidden, c.lane);
           sync(c);  // blocks consumed
           rowpar_epilogue(g, c, L, hidden);
           if (!allreduce_residual(c, L, hidden)) return fail(1);
@@ -1912,14 +1918,13 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       {
         fence(c, kTGateUp);
         const Gemv g = gemv_of(Lp, q, 2, c.xcd, c.r);
-        norm_put(np, L.nw, hidden, c.lane);  // post_norm
+        wait_vm<0>();  // post_norm in L.nw
         sync(c);
         for (int i = 0; i < kNormBars; ++i) sync(c);
         sync(c);  // blocks consumed
         c.epoch += 1;
         colpar_epilogue(g, c, L);
         signal_local(c, c.epoch);
-        norm_fetch(np, li + 1 < M.num_layers ? LF(layer_at(M, li + 1), in_norm) : M.final_norm, hidden, c.lane);
       }
       // ================= down (row-parallel) ===========================================
       {
@@ -1929,6 +1934,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         stage_gu<(kColparMax / 4 + 63) / 64>(c, q.inter_x, L.u.ac.gu);
         sync(c);
         stamp(c, kTStaged);
+        dma_row(li + 1 < M.num_layers ? LF(layer_at(M, li + 1), in_norm) : M.final_norm, L.nw, hidden, c.lane);
         for (int i = 0; i < kActBars; ++i) sync(c);
         sync(c);  // blocks consumed
         rowpar_epilogue(g, c, L, hidden);
@@ -1941,7 +1947,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
     {
       fence(c, kTHead);
       auto& H = L.hd;
-      norm_put(np, L.nw, hidden, c.lane);  // final_norm
+      wait_vm<0>();  // final_norm in L.nw
       sync(c);
       for (int i = 0; i < kNormBars; ++i) sync(c);
       sync(c);  // head blocks consumed, per-wave candidates in LDS
@@ -2012,7 +2018,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       if (!ok) return;
       token = bi;
       if (c.lane == 0 && c.xcd == 0 && c.r == 0 && !teacher_forced && M.token_log) M.token_log[step0 + step] = token;
-      norm_fetch(np, LF(layer_at(M, 0), in_norm), hidden, c.lane);  // the next token's first norm
+      dma_row(LF(layer_at(M, 0), in_norm), L.nw, hidden, c.lane);  // the next token's first norm
     }
   }
   __builtin_amdgcn_s_waitcnt(0);
