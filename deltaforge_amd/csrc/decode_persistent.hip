@@ -88,9 +88,10 @@ enum Err : int { kErrNone = 0, kErrTimeout = 1, kErrXcd = 2, kErrPosition = 3, k
 struct Ws {
   int* ctl;          // [16]: epoch, abort, error, -, 8 registration tickets, -
   int* flags;        // [8][32] last epoch each workgroup finished
-  float* colpar;     // [8][2][kColparMax] column-parallel partial outputs, 2 slots
-  uint16_t* hloc;    // [8][hidden] the hidden vector, one copy per XCD
-  uint16_t* core;    // [8][512] DeltaNet core / merged attention output of the XCD
+  uint64_t* colpar;  // [8][2][kColparMax] input-projection partial outputs, 2 slots, (fp32, epoch)
+  float* cpgu;       // [8][2][kColparMax] gate|up partial outputs, 2 slots (flag hand-off)
+  uint16_t* hloc;    // [8][hidden] the hidden vector, one copy per XCD (flag hand-off)
+  uint32_t* core;    // [8][512] DeltaNet core / merged attention output of the XCD, (bf16 | epoch << 16)
   float* apart;      // [8][32 splits][2 heads][kApHead]
   uint64_t* rowpar;  // [2][8][hidden] (fp32 value, u32 epoch) row-parallel partials
   uint64_t* cand;    // [256] argmax candidates (value, index, epoch bits)
@@ -107,18 +108,20 @@ __host__ __device__ inline size_t ws_layout(int hidden, Ws* w, char* base) {
   };
   char* ctl = take(16 * sizeof(int));
   char* flags = take((size_t)kXcd * kPerXcd * sizeof(int));
-  char* colpar = take((size_t)kXcd * 2 * kColparMax * sizeof(float));
+  char* colpar = take((size_t)kXcd * 2 * kColparMax * sizeof(uint64_t));
+  char* cpgu = take((size_t)kXcd * 2 * kColparMax * sizeof(float));
   char* hloc = take((size_t)kXcd * hidden * sizeof(uint16_t));
-  char* core = take((size_t)kXcd * 512 * sizeof(uint16_t));
+  char* core = take((size_t)kXcd * 512 * sizeof(uint32_t));
   char* apart = take((size_t)kXcd * kPerXcd * 2 * kApHead * sizeof(float));
   char* rowpar = take((size_t)2 * kXcd * hidden * sizeof(uint64_t));
   char* cand = take((size_t)kNwg * sizeof(uint64_t));
   if (w) {
     w->ctl = reinterpret_cast<int*>(ctl);
     w->flags = reinterpret_cast<int*>(flags);
-    w->colpar = reinterpret_cast<float*>(colpar);
+    w->colpar = reinterpret_cast<uint64_t*>(colpar);
+    w->cpgu = reinterpret_cast<float*>(cpgu);
     w->hloc = reinterpret_cast<uint16_t*>(hloc);
-    w->core = reinterpret_cast<uint16_t*>(core);
+    w->core = reinterpret_cast<uint32_t*>(core);
     w->apart = reinterpret_cast<float*>(apart);
     w->rowpar = reinterpret_cast<uint64_t*>(rowpar);
     w->cand = reinterpret_cast<uint64_t*>(cand);
@@ -235,6 +238,7 @@ struct Lds {
   __align__(16) uint16_t h[kMaxHidden];          // the hidden vector (bf16)
   __align__(16) uint16_t nw[kMaxHidden];         // the next RMSNorm's weight (LDS DMA, a phase ahead)
   __align__(16) uint16_t gnw[kDk];               // GatedRMSNorm weight (LDS DMA, a phase ahead)
+  __align__(16) float zs[512];                   // out_proj: SiLU inputs of the GatedRMSNorm (staged during delta)
   float xs[kMaxGroups];                          // 136 * sum of each 128-group of g_x
   float part[kMaxWgTiles][kCompute][16];         // per-wave tile partials
   float red[64];
@@ -247,9 +251,6 @@ struct Lds {
     int bi[kCompute];
   } hd;
   union {
-    struct {                                     // out_proj: SiLU inputs of the GatedRMSNorm
-      float z[512];
-    } on;
     struct {                                     // Gated DeltaNet step
       float4 S[kCompute * 64];                   // state slice: row tid/4, columns 4(tid%4)..+3
       uint2 taps[kDnCh];                         // conv taps (bf16 x4)
@@ -413,6 +414,34 @@ DF_DEVICE void signal_local(Ctx& c, uint32_t epoch) {
     // volatile or wider-scope store would write through to memory and wait for that
     __hip_atomic_store((__attribute__((address_space(1))) int*)(c.w.flags + c.xcd * kPerXcd + c.r),
                        static_cast<int>(epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+}
+
+// Tagged hand-off data. Most hand-offs carry their epoch in every word, so the consumer polls
+// the data itself (one L2 round trip after the producer's stores) and the producer never waits
+// for its stores: (fp32 value, u32 epoch) pairs for fp32 data, bf16 | (epoch & 0xFFFF) << 16
+// for bf16 data (a slot is rewritten every token, so a stale word's epoch differs from the one
+// awaited). Single-copy atomicity of aligned 4- and 8-byte stores is all they rely on.
+DF_DEVICE uint32_t tag_bf16(uint16_t v, uint32_t epoch) { return static_cast<uint32_t>(v) | (epoch << 16); }
+DF_DEVICE bool tag_ok(uint32_t w, uint32_t epoch) { return (w >> 16) == (epoch & 0xFFFFu); }
+DF_DEVICE bool tags_ok(const uint4& v, uint32_t epoch) {
+  return tag_ok(v.x, epoch) && tag_ok(v.y, epoch) && tag_ok(v.z, epoch) && tag_ok(v.w, epoch);
+}
+DF_DEVICE bool pairs_ok(const uint4& v, uint32_t epoch) { return v.y == epoch && v.w == epoch; }
+
+// Control wave: repeat `load` (fills the wave's registers, returns whether every tag it read
+// is the awaited one) until every lane's is; false on abort or timeout.
+template <class F>
+DF_DEVICE bool poll_tagged(const Ctx& c, F&& load) {
+  const uint64_t t0 = now();
+  for (int it = 1;; ++it) {
+    if (__all(load())) return true;
+    if ((it & 31) == 0 && ld_sys(c.w.ctl + 1)) return false;
+    if (now() - t0 > kTimeout) {
+      raise_abort(c, kErrTimeout);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
   }
 }
 
@@ -905,55 +934,69 @@ DF_DEVICE void dma_row128(const uint16_t* src, uint16_t* dst, int lane) {
   dma4(src + lane * 2, lds_addr(dst));
 }
 
-// A run of XCD-local columns [j0, j0 + n) of the column-parallel outputs (j0, n multiples of
-// 4), delivered as bf16-rounded slot sums into dst.
+// A run of XCD-local columns [j0, j0 + n) (j0, n even) of the column-parallel outputs,
+// delivered as bf16-rounded slot sums into dst.
 struct Seg {
   int j0, n;
   float* dst;
 };
 
-// Up to NS segments, K 16-byte chunks per lane and slot.
+// Up to NS segments, K 16-byte chunks (2 columns) per lane and slot; polls until every pair
+// carries epoch `want`.
 template <int NS, int K>
-DF_DEVICE void gather_colpar(const Ctx& c, const Seg (&seg)[NS]) {
+DF_DEVICE bool gather_colpar(const Ctx& c, const Seg (&seg)[NS], uint32_t want) {
   const auto r = rsrc(c.w.colpar + (size_t)c.xcd * 2 * kColparMax);
   int start[NS + 1];
   start[0] = 0;
 #pragma unroll
-  for (int s = 0; s < NS; ++s) start[s + 1] = start[s] + seg[s].n / 4;
-  uint4 a[K], b[K];
+  for (int s = 0; s < NS; ++s) start[s + 1] = start[s] + seg[s].n / 2;
+  int col[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const int ch = c.lane + 64 * k;
-    if (ch < start[NS]) {
-      int col = 0;
+    col[k] = -1;
 #pragma unroll
-      for (int s = 0; s < NS; ++s)
-        if (ch >= start[s] && ch < start[s + 1]) col = seg[s].j0 + 4 * (ch - start[s]);
-      a[k] = ld16<kCpAgent>(r, col * 4);
-      b[k] = ld16<kCpAgent>(r, (kColparMax + col) * 4);
-    }
+    for (int s = 0; s < NS; ++s)
+      if (ch >= start[s] && ch < start[s + 1]) col[k] = seg[s].j0 + 2 * (ch - start[s]);
   }
+  uint4 a[K], b[K];
+  const bool ok = poll_tagged(c, [&]() {
+    bool t = true;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      if (col[k] >= 0) {
+        a[k] = ld16<kCpAgent>(r, col[k] * 8);
+        b[k] = ld16<kCpAgent>(r, (kColparMax + col[k]) * 8);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (col[k] >= 0) t = t && pairs_ok(a[k], want) && pairs_ok(b[k], want);
+    return t;
+  });
+  if (!ok) return false;
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const int ch = c.lane + 64 * k;
-    if (ch < start[NS]) {
+    if (col[k] >= 0) {
       float* d = nullptr;
 #pragma unroll
       for (int s = 0; s < NS; ++s)
-        if (ch >= start[s] && ch < start[s + 1]) d = seg[s].dst + 4 * (ch - start[s]);
+        if (ch >= start[s] && ch < start[s + 1]) d = seg[s].dst + 2 * (ch - start[s]);
       d[0] = round_bf(__uint_as_float(a[k].x) + __uint_as_float(b[k].x));
-      d[1] = round_bf(__uint_as_float(a[k].y) + __uint_as_float(b[k].y));
-      d[2] = round_bf(__uint_as_float(a[k].z) + __uint_as_float(b[k].z));
-      d[3] = round_bf(__uint_as_float(a[k].w) + __uint_as_float(b[k].w));
+      d[1] = round_bf(__uint_as_float(a[k].z) + __uint_as_float(b[k].z));
     }
   }
+  return true;
 }
 
-// Control wave: the XCD's 2 inter_x gate|up columns as (unrounded) sums of the two
-// column-parallel slots, into gu.
+// Control wave, after the flag hand-off: the XCD's 2 inter_x gate|up columns as (unrounded)
+// sums of the two column-parallel slots, into gu. This hand-off keeps flags and untagged
+// fp32: polling its data tagged would mean twice the bytes (37 KB per workgroup), more than
+// the flag's round trip costs.
 template <int K>
 DF_DEVICE void stage_gu(const Ctx& c, int inter_x, float* gu) {
-  const auto r = rsrc(c.w.colpar + (size_t)c.xcd * 2 * kColparMax);
+  const auto r = rsrc(c.w.cpgu + (size_t)c.xcd * 2 * kColparMax);
   const int chunks = inter_x / 2;  // 4 columns each
   uint4 a[K], b[K];
 #pragma unroll
@@ -1000,36 +1043,55 @@ DF_DEVICE void swiglu_act(Lds& L, Ctx& c, int inter_x) {
   sync(c);
 }
 
-// Control wave: the XCD's 512 merged attention / delta outputs (bf16, published by the
-// workgroups of the XCD) into g_x with the group sums L.xs of its four 128-groups (a group is
-// one 16-lane row of 8 values per lane).
-DF_DEVICE void stage_core(Lds& L, const Ctx& c) {
+// Control wave: the XCD's 512 merged attention / delta outputs (tagged bf16, published by the
+// workgroups of the XCD at epoch `want`) into g_x, with the group sums L.xs of its four
+// 128-groups when `sums` (a group is one 16-lane row of 8 values per lane).
+DF_DEVICE bool stage_core(Lds& L, const Ctx& c, uint32_t want, bool sums) {
   const auto r = rsrc(c.w.core + (size_t)c.xcd * 512);
-  const uint4 v = ld16<kCpAgent>(r, c.lane * 16);
+  uint4 v0, v1;
+  if (!poll_tagged(c, [&]() {
+        v0 = ld16<kCpAgent>(r, c.lane * 32);
+        v1 = ld16<kCpAgent>(r, c.lane * 32 + 16);
+        return tags_ok(v0, want) && tags_ok(v1, want);
+      }))
+    return false;
+  const uint4 v = make_uint4((v0.x & 0xFFFFu) | (v0.y << 16), (v0.z & 0xFFFFu) | (v0.w << 16),
+                             (v1.x & 0xFFFFu) | (v1.y << 16), (v1.z & 0xFFFFu) | (v1.w << 16));
   *reinterpret_cast<uint4*>(&g_x[c.lane * 8]) = v;
-  float s = 0.0f;
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  if (sums) {
+    float s = 0.0f;
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-  for (int e = 0; e < 4; ++e) s += __uint_as_float(w[e] << 16) + __uint_as_float(w[e] & 0xFFFF0000u);
-  s = row_sum(s);
-  if ((c.lane & 15) == 0) L.xs[c.lane >> 4] = kBias * s;
+    for (int e = 0; e < 4; ++e) s += __uint_as_float(w[e] << 16) + __uint_as_float(w[e] & 0xFFFF0000u);
+    s = row_sum(s);
+    if ((c.lane & 15) == 0) L.xs[c.lane >> 4] = kBias * s;
+  }
+  return true;
 }
 
 // Control wave, column-parallel epilogue: this workgroup's partial of each tile it touched
 // into its slot (r & 1); tiles wholly inside its range also zero the other slot.
+// TAGGED: the input projection's (fp32, epoch) pairs; else gate|up's plain fp32.
+template <bool TAGGED>
 DF_DEVICE void colpar_epilogue(const Gemv& g, const Ctx& c, const Lds& L) {
   const int t_first = g.b_lo / g.ng, t_last = (g.b_hi - 1) / g.ng;
   const int nt = t_last - t_first + 1;
-  float* cp = c.w.colpar + (size_t)c.xcd * 2 * kColparMax;
+  uint64_t* cp = c.w.colpar + (size_t)c.xcd * 2 * kColparMax;
+  float* cg = c.w.cpgu + (size_t)c.xcd * 2 * kColparMax;
   const int mine = c.r & 1;
   for (int e = c.lane; e < nt * 16; e += 64) {
     const int tr = e / 16, col = e % 16;
     const int t = t_first + tr;
     const float v = part_sum(L, tr, col);
     const int j = t * 16 + col;
-    cp[mine * kColparMax + j] = v;
     const bool whole = t * g.ng >= g.b_lo && (t + 1) * g.ng <= g.b_hi;
-    if (whole) cp[(mine ^ 1) * kColparMax + j] = 0.0f;
+    if (TAGGED) {
+      cp[mine * kColparMax + j] = pack_epoch(v, c.epoch);
+      if (whole) cp[(mine ^ 1) * kColparMax + j] = pack_epoch(0.0f, c.epoch);
+    } else {
+      cg[mine * kColparMax + j] = v;
+      if (whole) cg[(mine ^ 1) * kColparMax + j] = 0.0f;
+    }
   }
 }
 
@@ -1091,6 +1153,8 @@ DF_DEVICE bool allreduce_residual(Ctx& c, Lds& L, int hidden) {
     const uint16_t b1 = f2bf(__uint_as_float(hv & 0xFFFF0000u) + round_bf(y1));
     *reinterpret_cast<uint32_t*>(hx + k) = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
   }
+  // the XCD's copy of h by flags: polling its 32 slices tagged measured slower (twice the
+  // bytes, re-read by every workgroup of the XCD while the slices arrive)
   signal_local(c, c.epoch);
   if (!wait_local(c, c.epoch)) return false;
   stage16<kHidChunks, kCpAgent>(L.h, hx, hidden, c.lane);
@@ -1138,15 +1202,12 @@ DF_DEVICE bool dn_stage(Ctx& c, LayerPtr Lp, Lds& L) {
     }
   }
   const float alog = bf2f(LF(Lp, A_log)[hv]), dtb = bf2f(LF(Lp, dt_bias)[hv]);
-  const bool ok = wait_local(c, c.epoch);
-  if (ok) {
-    const int khl = hvl >> 1;
-    const Seg seg[4] = {{kLinQ + khl * 128, 128, D.qkv_in},
-                        {kLinK + khl * 128, 128, D.qkv_in + 128},
-                        {kLinV + hvl * 128 + vs * 16, 16, D.qkv_in + 256},
-                        {kLinA, 8, D.ab8}};
-    gather_colpar<4, 2>(c, seg);
-  }
+  const int khl = hvl >> 1;
+  const Seg seg[4] = {{kLinQ + khl * 128, 128, D.qkv_in},
+                      {kLinK + khl * 128, 128, D.qkv_in + 128},
+                      {kLinV + hvl * 128 + vs * 16, 16, D.qkv_in + 256},
+                      {kLinA, 8, D.ab8}};
+  const bool ok = gather_colpar<4, 3>(c, seg, c.epoch);
 #pragma unroll
   for (int i = 0; i < kSt; ++i) D.S[c.lane + 64 * i] = __builtin_bit_cast(float4, sv[i]);
 #pragma unroll
@@ -1541,7 +1602,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           const float tot = L.red[2 * h] + L.red[2 * h + 1];
           const float rr = 1.0f / sqrtf(tot / 128.0f + M.eps);
           const float t = round_bf(bf2f(L.gnw[i & 127]) * round_bf(v * rr));
-          const uint16_t xb = f2bf(t * silu(L.u.on.z[i]));
+          const uint16_t xb = f2bf(t * silu(L.zs[i]));
           g_x[i] = xb;
           const float gs = dsum(bf2f(xb));
           if (c.lane == 0) L.red[16 + c.wave] = gs;
@@ -1786,8 +1847,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         }
         sync(c);  // blocks consumed
         c.epoch += 1;
-        colpar_epilogue(g, c, L);
-        signal_local(c, c.epoch);
+        colpar_epilogue<true>(g, c, L);
       }
       if (kind == 0) {
         // ================= conv + gated delta step ===================================
@@ -1796,22 +1856,23 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         if (!ok) return fail(1);
         sync(c);
         stamp(c, kTStaged);
+        {  // z of the XCD's four value heads for out_proj's gated norm, while the delta step runs
+          const Seg seg[1] = {{kLinZ, 512, L.zs}};
+          if (!gather_colpar<1, 4>(c, seg, c.epoch)) return fail(kDnBars + 1);  // through out_proj's first
+        }
         for (int i = 0; i < kDnBars; ++i) sync(c);
         c.epoch += 1;
         {
           const int hvl = c.r >> 3, vs = c.r & 7;
-          if (c.lane < 16) c.w.core[(size_t)c.xcd * 512 + hvl * kDk + vs * 16 + c.lane] = L.u.dn.core[c.lane];
+          if (c.lane < 16)
+            c.w.core[(size_t)c.xcd * 512 + hvl * kDk + vs * 16 + c.lane] = tag_bf16(L.u.dn.core[c.lane], c.epoch);
         }
-        signal_local(c, c.epoch);
         // ================= gated norm + out_proj (row-parallel) ======================
         {
           fence(c, kTOut);
           const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
-          if (!wait_local(c, c.epoch)) return fail(1);
-          // core (512) and z (512) of the XCD's four value heads
-          stage16<1, kCpAgent>(g_x, c.w.core + (size_t)c.xcd * 512, 512, c.lane);
-          const Seg seg[1] = {{kLinZ, 512, L.u.on.z}};
-          gather_colpar<1, 2>(c, seg);
+          // core (512) of the XCD's four value heads
+          if (!stage_core(L, c, c.epoch, false)) return fail(1);
           sync(c);
           stamp(c, kTStaged);
           dma_row(LF(Lp, post_norm), L.nw, hidden, c.lane);
@@ -1827,10 +1888,9 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         // ================= attention split ===========================================
         fence(c, kTAttn);
         auto& A = L.u.at;
-        if (!wait_local(c, c.epoch)) return fail(1);
         {
           const Seg seg[3] = {{0, kHd, A.qraw[0]}, {512, kHd, A.qraw[1]}, {kAttnK, 2 * kHd, A.kraw}};
-          gather_colpar<3, 4>(c, seg);  // kraw and vraw are adjacent in LDS
+          if (!gather_colpar<3, 8>(c, seg, c.epoch)) return fail(1);  // kraw and vraw are adjacent in LDS
           if (c.lane < kRot / 2) A.inv[c.lane] = pre_inv;
           if (c.lane < 2) {
             A.ml[c.lane][0] = -INFINITY;
@@ -1875,7 +1935,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
             av[k] = ld16<kCpAgent>(r, ((ch / 4) * 2 * kApHead + d0 + 4 * (ch % 4)) * 4);
           }
           const Seg seg[1] = {{hl * 512 + kHd + d0, 16, Mg.gate}};
-          gather_colpar<1, 1>(c, seg);
+          if (!gather_colpar<1, 1>(c, seg, c.epoch - 2)) return fail(1);  // the input projection's
 #pragma unroll
           for (int k = 0; k < 2; ++k) {
             const int ch = c.lane + 64 * k;
@@ -1895,16 +1955,14 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
             const float o = round_bf(num / den);
             const float gx = Mg.gate[c.lane];
             const float gate = round_bf(M.gate_kind == 0 ? sigmoid(gx) : silu(gx));
-            c.w.core[(size_t)c.xcd * 512 + hl * kHd + d0 + c.lane] = f2bf(o * gate);
+            c.w.core[(size_t)c.xcd * 512 + hl * kHd + d0 + c.lane] = tag_bf16(f2bf(o * gate), c.epoch);
           }
-          signal_local(c, c.epoch);
         }
         // ================= o_proj (row-parallel) =====================================
         {
           fence(c, kTOProj);
           const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
-          if (!wait_local(c, c.epoch)) return fail(1);
-          stage_core(L, c);
+          if (!stage_core(L, c, c.epoch, true)) return fail(1);
           sync(c);
           stamp(c, kTStaged);
           dma_row(LF(Lp, post_norm), L.nw, hidden, c.lane);
@@ -1923,7 +1981,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         for (int i = 0; i < kNormBars; ++i) sync(c);
         sync(c);  // blocks consumed
         c.epoch += 1;
-        colpar_epilogue(g, c, L);
+        colpar_epilogue<false>(g, c, L);
         signal_local(c, c.epoch);
       }
       // ================= down (row-parallel) ===========================================
