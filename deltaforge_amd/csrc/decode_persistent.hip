@@ -60,6 +60,7 @@ constexpr int kMaxHidden = 2560;
 #define DF_RING 8
 #endif
 constexpr int kRing = DF_RING;                      // weight blocks in flight per compute wave
+static_assert(kRing >= 4 && (kRing & (kRing - 1)) == 0, "ring slots wrap with a mask");
 constexpr int kMaxWgTiles = 8;                      // output tiles of a workgroup's GEMV range
 constexpr int kMaxGroups = 24;                      // 128-groups of a GEMV phase's input row
 constexpr int kMaxHeadTiles = 64;                   // head tiles per workgroup
@@ -687,7 +688,7 @@ DF_DEVICE void issue_one(Stream& st, const Ctx& c) {
   dma16(st.wp + c.lane * 16, lds_addr(&g_ring_w[c.wave][st.wslot][0]));
   dma4_16(st.sp + (c.lane & 14), lds_addr(&g_ring_s[c.wave][st.wslot][0]));
   st.issued += 1;
-  st.wslot = st.wslot + 1 == kRing ? 0 : st.wslot + 1;
+  st.wslot = (st.wslot + 1) & (kRing - 1);
   st.wp += kBlockBytes;
   st.sp += kTileCols;
   st.left -= 1;
@@ -703,6 +704,48 @@ DF_DEVICE void fill(Stream& st, int steps, const Ctx& c) {
   }
 }
 
+// The same DMAs with the global address as a scalar base plus the lane's offset (no vector
+// address arithmetic per block).
+DF_DEVICE void dma16s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase),
+               "s"(lds_base)
+               : "memory", "m0");
+}
+DF_DEVICE void dma4_16s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  uint64_t saved;
+  asm volatile(
+      "s_mov_b64 %0, exec\n\t"
+      "s_mov_b32 exec_lo, 0xffff\n\t"
+      "s_mov_b32 exec_hi, 0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %1, %2 nt\n\t"
+      "s_mov_b64 exec, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(sbase), "s"(lds_base)
+      : "memory", "m0");
+}
+
+// After the consumer took two blocks from a full ring: refill both slots. The common case
+// (two more blocks in the current run) is straight-line code; anything else goes through fill.
+DF_DEVICE void refill2(Stream& st, int steps, const Ctx& c) {
+  if (__builtin_expect(st.state == kStreaming && st.left >= 2 && st.issued - st.consumed == kRing - 2, 1)) {
+    const uint32_t voff = c.lane * 16, soff = (c.lane & 14) * 2;
+    const int s0 = st.wslot, s1 = (st.wslot + 1) & (kRing - 1);
+    dma16s(st.wp, voff, lds_addr(&g_ring_w[c.wave][s0][0]));
+    dma4_16s(st.sp, soff, lds_addr(&g_ring_s[c.wave][s0][0]));
+    dma16s(st.wp + kBlockBytes, voff, lds_addr(&g_ring_w[c.wave][s1][0]));
+    dma4_16s(st.sp + kTileCols, soff, lds_addr(&g_ring_s[c.wave][s1][0]));
+    st.issued += 2;
+    st.wslot = (st.wslot + 2) & (kRing - 1);
+    st.wp += 2 * kBlockBytes;
+    st.sp += 2 * kTileCols;
+    st.left -= 2;
+    return;
+  }
+  fill(st, steps, c);
+}
+
 // Wait for the oldest `need` pending blocks (need = 1 or 2). The ring is full except while
 // it drains before an attention layer's hold or at the end of a launch, where waiting for
 // every block in flight costs nothing extra.
@@ -712,7 +755,7 @@ DF_DEVICE void wait_oldest(const Stream& st) {
   else wait_vm<0>();
 }
 
-DF_DEVICE int next_slot(int s) { return s + 1 == kRing ? 0 : s + 1; }
+DF_DEVICE int next_slot(int s) { return (s + 1) & (kRing - 1); }
 
 // One block's weights and scale dword from ring slot `slot` of this wave.
 DF_DEVICE void ring_read1(int slot, const Ctx& c, uint4& wv, uint32_t& sd) {
@@ -863,7 +906,7 @@ DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPer
     take_pair(st, c, xb + gl * kGroup, xb + gl1 * kGroup, &L.xs[gl], &L.xs[gl1], in);
     const float v0 = block_dot_r(in.w0, in.s0, in.x0, in.xs0, sh);
     const float v1 = block_dot_r(in.w1, in.s1, in.x1, in.xs1, sh);
-    fill(st, steps, c);
+    refill2(st, steps, c);
     add(v0);
     add(v1);
   }
@@ -1731,7 +1774,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         take_pair(st, c, xb + gl * kGroup, xb + (gl + 1) * kGroup, &L.xs[gl], &L.xs[gl + 1], in);
         const float v0 = block_dot_r(in.w0, in.s0, in.x0, in.xs0, sh);
         const float v1 = block_dot_r(in.w1, in.s1, in.x1, in.xs1, sh);
-        fill(st, steps, c);
+        refill2(st, steps, c);
         acc += v0;
         acc += v1;
         gl += 2;
