@@ -241,7 +241,8 @@ struct Lds {
   __align__(16) uint16_t gnw[kDk];               // GatedRMSNorm weight (LDS DMA, a phase ahead)
   __align__(16) float zs[512];                   // out_proj: SiLU inputs of the GatedRMSNorm (staged during delta)
   float xs[kMaxGroups];                          // 136 * sum of each 128-group of g_x
-  float part[kMaxWgTiles][kCompute][16];         // per-wave tile partials
+  float ss;                                      // sum of squares of h (for the next RMSNorm)
+  __align__(16) float part[kMaxWgTiles][16][kCompute];  // per-wave tile partials (a column's 8 adjacent)
   float red[64];
   int ok;
   int token;
@@ -457,19 +458,7 @@ DF_DEVICE bool poll_tagged(const Ctx& c, F&& load) {
 // (2 elements per lane).
 constexpr int kNormBars = 1;
 DF_DEVICE void norm_w(Lds& L, Ctx& c, int hidden, float eps) {
-  float ss = 0.0f;
-  for (int k = c.lane * 8; k < hidden; k += 64 * 8) {
-    const uint4 v = *reinterpret_cast<const uint4*>(&L.h[k]);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xFFFF0000u);
-      ss += lo * lo;
-      ss += hi * hi;
-    }
-  }
-  ss = dsum(ss);
-  const float r = 1.0f / sqrtf(ss / static_cast<float>(hidden) + eps);
+  const float r = 1.0f / sqrtf(L.ss / static_cast<float>(hidden) + eps);
   const int G = hidden / kGroup;
   for (int g = c.wave; g < G; g += kCompute) {
     const int k = g * kGroup + 2 * c.lane;
@@ -883,7 +872,7 @@ DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPer
   wave_range(g, c.wave, lo, n);
   // this wave's partial of every tile starts at zero (only this wave writes its column, and
   // the control wave read the previous phase's partials before the barrier that began this one)
-  for (int e = c.lane; e < kMaxWgTiles * 16; e += 64) L.part[e / 16][c.wave][e % 16] = 0.0f;
+  for (int e = c.lane; e < kMaxWgTiles * 16; e += 64) L.part[e / 16][e % 16][c.wave] = 0.0f;
   const uint16_t* xb = g_x + (c.lane >> 4) * 32;
   int tr = lo / g.ng - g.b_lo / g.ng;
   int gl = lo % g.ng;
@@ -891,7 +880,7 @@ DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPer
   auto add = [&](float v) {
     acc += v;
     if (++gl == g.ng) {
-      if (c.lane < 16) L.part[tr][c.wave][c.lane] = acc;
+      if (c.lane < 16) L.part[tr][c.lane][c.wave] = acc;
       acc = 0.0f;
       gl = 0;
       ++tr;
@@ -917,15 +906,15 @@ DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPer
     add(block_dot(w0, s0, xb + gl * kGroup, L.xs[gl], c.lane));
     fill(st, steps, c);
   }
-  if (n > 0 && gl != 0 && c.lane < 16) L.part[tr][c.wave][c.lane] = acc;
+  if (n > 0 && gl != 0 && c.lane < 16) L.part[tr][c.lane][c.wave] = acc;
 }
 
 // Sum of the waves' partials for relative tile t (fixed wave order).
 DF_DEVICE float part_sum(const Lds& L, int t, int col) {
-  float v = 0.0f;
-#pragma unroll
-  for (int wv = 0; wv < kCompute; ++wv) v += L.part[t][wv][col];
-  return v;
+  static_assert(kCompute == 8, "two 16-byte reads per column");
+  const float4 a = *reinterpret_cast<const float4*>(&L.part[t][col][0]);
+  const float4 b = *reinterpret_cast<const float4*>(&L.part[t][col][4]);
+  return ((((((a.x + a.y) + a.z) + a.w) + b.x) + b.y) + b.z) + b.w;  // wave order
 }
 
 // ---- control-wave staging: every load of a hand-off is issued before any is used -------
@@ -1200,7 +1189,32 @@ DF_DEVICE bool allreduce_residual(Ctx& c, Lds& L, int hidden) {
   // bytes, re-read by every workgroup of the XCD while the slices arrive)
   signal_local(c, c.epoch);
   if (!wait_local(c, c.epoch)) return false;
-  stage16<kHidChunks, kCpAgent>(L.h, hx, hidden, c.lane);
+  // h into LDS with its sum of squares for the next RMSNorm (the same order in every
+  // workgroup, so all agree)
+  const auto rh = rsrc(hx);
+  uint4 hv[kHidChunks];
+#pragma unroll
+  for (int k = 0; k < kHidChunks; ++k) {
+    const int ch = c.lane + 64 * k;
+    if (ch * 8 < hidden) hv[k] = ld16<kCpAgent>(rh, ch * 16);
+  }
+  float sq = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kHidChunks; ++k) {
+    const int ch = c.lane + 64 * k;
+    if (ch * 8 < hidden) {
+      *reinterpret_cast<uint4*>(&L.h[ch * 8]) = hv[k];
+      const uint32_t w[4] = {hv[k].x, hv[k].y, hv[k].z, hv[k].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xFFFF0000u);
+        sq += lo * lo;
+        sq += hi * hi;
+      }
+    }
+  }
+  sq = dsum(sq);
+  if (c.lane == 0) L.ss = sq;
   return true;
 }
 
@@ -1850,6 +1864,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           sc[k] = M.head_s[block * 16 + cc];
         }
       }
+      float sq = 0.0f;
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         const int idx = c.lane + 64 * k;
@@ -1860,10 +1875,14 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           for (int e = 0; e < 8; ++e) {
             const int sh = (e & 1) ? 16 + 4 * (e >> 1) : 4 * (e >> 1);
             const int qv = static_cast<int>((wd[k] >> sh) & 15u) - 8;
-            L.h[g * 128 + s * 32 + d * 8 + e] = f2bf(static_cast<float>(qv) * scv);
+            const uint16_t hb = f2bf(static_cast<float>(qv) * scv);
+            L.h[g * 128 + s * 32 + d * 8 + e] = hb;
+            sq += bf2f(hb) * bf2f(hb);
           }
         }
       }
+      sq = dsum(sq);
+      if (c.lane == 0) L.ss = sq;
     }
     if (c.lane == 0) L.ok = 1;
     sync(c);
