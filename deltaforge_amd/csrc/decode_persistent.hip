@@ -253,17 +253,12 @@ struct Lds {
     int bi[kCompute];
   } hd;
   union {
-    struct {                                     // Gated DeltaNet step
-      float4 S[kCompute * 64];                   // state slice: row tid/4, columns 4(tid%4)..+3
-      uint2 taps[kDnCh];                         // conv taps (bf16 x4)
-      uint2 hist[kDnCh];                         // conv history ring (bf16 x4, slot position % 4)
+    struct {                                     // Gated DeltaNet step (control wave)
+      __align__(16) float4 S[kDk / 16][64];      // state slice by DMA: [row block][lane]
       float qkv_in[kDnCh];                       // pre-conv inputs: q 128, k 128, v 16
-      float q[kDk], k[kDk], v[16];
-      float sred[kCompute][4][16];               // per wave and 16-lane row
+      __align__(16) float q[kDk], k[kDk], v[16];
+      float sred[4][16];                         // per 16-lane row: column sums
       float ab8[8];                              // a of the XCD's 4 value heads, then b
-      float gpar[2];                             // A_log, dt_bias of the unit's value head
-      float scal[4];
-      uint16_t core[16];
     } dn;
     struct {                                     // attention split
       __align__(16) uint16_t q[2][kHd];
@@ -1231,21 +1226,28 @@ DF_DEVICE int dn_channel(const Ctx& c, int i) {
   return 2 * kKeyDim + hv * kDk + vs * 16 + (i - 256);
 }
 
-// Control wave: the unit's state slice, conv taps and history, the gate parameters and,
-// after the in_proj hand-off, its pre-conv inputs and gates, all into LDS.
-DF_DEVICE bool dn_stage(Ctx& c, LayerPtr Lp, Lds& L) {
+// Control wave: the whole Gated DeltaNet step of this workgroup's unit (value head hv, value
+// columns 16 vs .. 16 vs + 15) in one wave, with no barrier: the 4-tap conv + SiLU over its
+// 272 channels (q, k of the key head, its 16 v), q/k L2 norms, the gates and the delta rule on
+// its 128 x 16 fp32 state slice, held in registers (lane l: columns 4 (l % 4) .. + 3 of rows
+// l / 4 + 16 j, j < 8). Publishes the 16 core outputs tagged with `epoch_out`, and stages the
+// XCD's z columns (out_proj's gated-norm gates) from the same hand-off poll. The arithmetic and
+// rounding points are the reference's (reference.py:407-461, 496-545); fp32 sums over the
+// state rows run in a fixed order of their own.
+DF_DEVICE bool dn_step(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_in, uint32_t epoch_out) {
+#pragma clang fp contract(off)
   auto& D = L.u.dn;
   const int hvl = c.r >> 3, vs = c.r & 7;
   const int hv = 4 * c.xcd + hvl;
-  constexpr int kSt = kCompute;              // float4 of the state slice per lane
+  constexpr int kRows = kDk / 16;            // state rows per lane
   constexpr int kCh = (kDnCh + 63) / 64;     // conv channels per lane
-  uint4 sv[kSt];
-  const float* state = LF(Lp, state);
+  // loads that do not depend on the hand-off go out first
+  float* state = LF(Lp, state);
+  const int row0 = c.lane >> 2, col4 = (c.lane & 3) * 4;
+  float* sbase = state + ((size_t)hv * kDk + row0) * kDk + vs * 16 + col4;
+  // the state slice goes to LDS by DMA (no registers held across the hand-off poll)
 #pragma unroll
-  for (int i = 0; i < kSt; ++i) {
-    const int e = c.lane + 64 * i;  // row e / 4, columns 4 (e % 4)
-    sv[i] = *reinterpret_cast<const uint4*>(state + ((size_t)hv * kDk + (e >> 2)) * kDk + vs * 16 + (e & 3) * 4);
-  }
+  for (int i = 0; i < kRows; ++i) dma16(sbase + (size_t)16 * i * kDk, lds_addr(&D.S[i][0]));
   uint2 tp[kCh];
   uint64_t hs[kCh];
 #pragma unroll
@@ -1260,142 +1262,112 @@ DF_DEVICE bool dn_stage(Ctx& c, LayerPtr Lp, Lds& L) {
   }
   const float alog = bf2f(LF(Lp, A_log)[hv]), dtb = bf2f(LF(Lp, dt_bias)[hv]);
   const int khl = hvl >> 1;
-  const Seg seg[4] = {{kLinQ + khl * 128, 128, D.qkv_in},
+  const Seg seg[5] = {{kLinQ + khl * 128, 128, D.qkv_in},
                       {kLinK + khl * 128, 128, D.qkv_in + 128},
                       {kLinV + hvl * 128 + vs * 16, 16, D.qkv_in + 256},
-                      {kLinA, 8, D.ab8}};
-  const bool ok = gather_colpar<4, 3>(c, seg, c.epoch);
-#pragma unroll
-  for (int i = 0; i < kSt; ++i) D.S[c.lane + 64 * i] = __builtin_bit_cast(float4, sv[i]);
+                      {kLinA, 8, D.ab8},
+                      {kLinZ, 512, L.zs}};
+  if (!gather_colpar<5, 7>(c, seg, epoch_in)) return false;
+  // conv + SiLU (fp32 sum in tap order, bf16, SiLU, bf16); history slots (pos+1)&3, (pos+2)&3,
+  // (pos+3)&3 hold positions pos-3, pos-2, pos-1. This unit owns its v slice; the (even value
+  // head, slice 0) unit owns the key head's q/k channels.
+  float y[kCh];
 #pragma unroll
   for (int i = 0; i < kCh; ++i) {
     const int ch = c.lane + 64 * i;
+    y[i] = 0.0f;
     if (ch < kDnCh) {
-      D.taps[ch] = tp[i];
-      D.hist[ch] = __builtin_bit_cast(uint2, hs[i]);
+      const uint2 wt = tp[i];
+      const uint2 hr = __builtin_bit_cast(uint2, hs[i]);
+      const float w0 = __uint_as_float(wt.x << 16), w1 = __uint_as_float(wt.x & 0xFFFF0000u);
+      const float w2 = __uint_as_float(wt.y << 16), w3 = __uint_as_float(wt.y & 0xFFFF0000u);
+      const uint16_t sl[4] = {static_cast<uint16_t>(hr.x), static_cast<uint16_t>(hr.x >> 16),
+                              static_cast<uint16_t>(hr.y), static_cast<uint16_t>(hr.y >> 16)};
+      const float h0 = bf2f(sl[(c.pos + 1) & 3]), h1 = bf2f(sl[(c.pos + 2) & 3]), h2 = bf2f(sl[(c.pos + 3) & 3]);
+      const float x = D.qkv_in[ch];
+      float acc = h0 * w0;
+      acc = acc + h1 * w1;
+      acc = acc + h2 * w2;
+      acc = acc + x * w3;
+      y[i] = round_bf(silu(round_bf(acc)));
+      const bool owner = ch >= 2 * kDk || ((hvl & 1) == 0 && vs == 0);
+      if (owner) LF(Lp, conv_ring)[(size_t)dn_channel(c, ch) * 4 + (c.pos & 3)] = f2bf(x);
     }
   }
-  if (c.lane == 0) {
-    D.gpar[0] = alog;
-    D.gpar[1] = dtb;
+  static_assert(kCh == 5 && kDk == 128, "q = channels l, l + 64; k = 128 + l, 192 + l; v = 256 + l");
+  // L2 norms of q (then scaled by dk^-1/2) and k
+  {
+    const float rq = 1.0f / sqrtf(dsum(y[0] * y[0] + y[1] * y[1]) + 1e-6f);
+    const float rk = 1.0f / sqrtf(dsum(y[2] * y[2] + y[3] * y[3]) + 1e-6f);
+    const float scale = sqrtf(static_cast<float>(kDk));
+    D.q[c.lane] = (y[0] * rq) / scale;
+    D.q[c.lane + 64] = (y[1] * rq) / scale;
+    D.k[c.lane] = y[2] * rk;
+    D.k[c.lane + 64] = y[3] * rk;
+    if (c.lane < 16) D.v[c.lane] = y[4];
   }
-  return ok;
-}
-
-// Compute waves (kDnBars barriers), after dn_stage: conv + SiLU, gates, L2 norms, the delta
-// rule. They write the new state and the conv history themselves (nothing reads them
-// before the next token); the core output goes to L.u.dn.core for the control wave.
-constexpr int kDnBars = 6;
-DF_DEVICE void dn_compute(Ctx& c, LayerPtr Lp, Lds& L) {
-#pragma clang fp contract(off)
-  const int hvl = c.r >> 3, vs = c.r & 7;
-  const int hv = 4 * c.xcd + hvl;
-  auto& D = L.u.dn;
-  // conv + SiLU (fp32 sum in tap order, bf16, SiLU, bf16); history slots (pos+1)&3,
-  // (pos+2)&3, (pos+3)&3 hold positions pos-3, pos-2, pos-1
-  if (c.tid < kDnCh) {
-    const uint2 wt = D.taps[c.tid], hr = D.hist[c.tid];
-    const float w0 = __uint_as_float(wt.x << 16), w1 = __uint_as_float(wt.x & 0xFFFF0000u);
-    const float w2 = __uint_as_float(wt.y << 16), w3 = __uint_as_float(wt.y & 0xFFFF0000u);
-    const uint16_t sl[4] = {static_cast<uint16_t>(hr.x), static_cast<uint16_t>(hr.x >> 16),
-                            static_cast<uint16_t>(hr.y), static_cast<uint16_t>(hr.y >> 16)};
-    const float h0 = bf2f(sl[(c.pos + 1) & 3]), h1 = bf2f(sl[(c.pos + 2) & 3]), h2 = bf2f(sl[(c.pos + 3) & 3]);
-    const float x = D.qkv_in[c.tid];
-    float acc = h0 * w0;
-    acc = acc + h1 * w1;
-    acc = acc + h2 * w2;
-    acc = acc + x * w3;
-    const float y = round_bf(silu(round_bf(acc)));
-    if (c.tid < 128) D.q[c.tid] = y;
-    else if (c.tid < 256) D.k[c.tid - 128] = y;
-    else D.v[c.tid - 256] = y;
-    // history: this unit owns its v slice; the (even value head, slice 0) unit owns the
-    // key head's q/k channels
-    const bool owner = c.tid >= 256 || ((hvl & 1) == 0 && vs == 0);
-    if (owner) LF(Lp, conv_ring)[(size_t)dn_channel(c, c.tid) * 4 + (c.pos & 3)] = f2bf(x);
-  }
-  if (c.tid == 0) {
-    const float a = D.ab8[hvl], b = D.ab8[4 + hvl];
-    const float beta = round_bf(sigmoid(b));
-    const float g = -expf(D.gpar[0]) * softplus(a + D.gpar[1]);
-    D.scal[0] = expf(g);
-    D.scal[1] = beta;
-  }
-  sync(c);
-  // L2 norms: wave 0 q, wave 1 k (2 values per lane)
-  if (c.wave < 2) {
-    float* vec = c.wave == 0 ? D.q : D.k;
-    const float x0 = vec[c.lane * 2], x1 = vec[c.lane * 2 + 1];
-    const float ss = dsum(x0 * x0 + x1 * x1);
-    const float rr = 1.0f / sqrtf(ss + 1e-6f);
-    float y0 = x0 * rr, y1 = x1 * rr;
-    if (c.wave == 0) {
-      const float scale = sqrtf(static_cast<float>(kDk));
-      y0 = y0 / scale;
-      y1 = y1 / scale;
-    }
-    vec[c.lane * 2] = y0;
-    vec[c.lane * 2 + 1] = y1;
-  }
-  sync(c);
-  const float eg = D.scal[0], beta = D.scal[1];
-  const int k = c.tid >> 2, c4 = c.tid & 3;
-  float4 S = make_float4(0.f, 0.f, 0.f, 0.f);
-  float kr = 0.f, qr = 0.f;
-  if (!c.control) {
-    S = D.S[c.tid];
-    kr = D.k[k];
-    qr = D.q[k];
-    S.x = S.x * eg;
-    S.y = S.y * eg;
-    S.z = S.z * eg;
-    S.w = S.w * eg;
-    float part[4] = {S.x * kr, S.y * kr, S.z * kr, S.w * kr};
-    // sums over the rows k of this wave's 16-lane row that share the column (lane % 4)
+  // gates
+  const float a = D.ab8[hvl], b = D.ab8[4 + hvl];
+  const float beta = round_bf(sigmoid(b));
+  const float eg = expf(-expf(alog) * softplus(a + dtb));
+  // state decay, and the recall k^T S over the unit's rows
+  float kr[kRows], qr[kRows];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) part[j] = row_sum_mod4(part[j]);
+  for (int i = 0; i < kRows; ++i) {
+    kr[i] = D.k[row0 + 16 * i];
+    qr[i] = D.q[row0 + 16 * i];
+  }
+  float4 S[kRows];
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) S[i] = D.S[i][c.lane];  // the poll's vmcnt(0) covered the DMA
+  float p[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    S[i].x = S[i].x * eg;
+    S[i].y = S[i].y * eg;
+    S[i].z = S[i].z * eg;
+    S[i].w = S[i].w * eg;
+    p[0] = p[0] + S[i].x * kr[i];
+    p[1] = p[1] + S[i].y * kr[i];
+    p[2] = p[2] + S[i].z * kr[i];
+    p[3] = p[3] + S[i].w * kr[i];
+  }
+  // column sums over the 64 lanes' rows: lanes l, l+4, l+8, l+12 of a 16-lane row (DPP),
+  // then the 4 rows through LDS (the wave's own LDS accesses complete in order)
+  auto col_sums = [&](float (&v)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = row_sum_mod4(v[j]);
     if ((c.lane & 15) < 4) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) D.sred[c.wave][c.lane >> 4][c4 * 4 + j] = part[j];
+      for (int j = 0; j < 4; ++j) D.sred[c.lane >> 4][col4 + j] = v[j];
     }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = ((D.sred[0][col4 + j] + D.sred[1][col4 + j]) + D.sred[2][col4 + j]) + D.sred[3][col4 + j];
+  };
+  col_sums(p);
+  const float4 vv = *reinterpret_cast<const float4*>(&D.v[col4]);
+  const float delta[4] = {(vv.x - p[0]) * beta, (vv.y - p[1]) * beta, (vv.z - p[2]) * beta, (vv.w - p[3]) * beta};
+  // rank-1 update, the new state out, and o = S^T q
+  float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    S[i].x = S[i].x + kr[i] * delta[0];
+    S[i].y = S[i].y + kr[i] * delta[1];
+    S[i].z = S[i].z + kr[i] * delta[2];
+    S[i].w = S[i].w + kr[i] * delta[3];
+    *reinterpret_cast<float4*>(sbase + (size_t)16 * i * kDk) = S[i];
+    o[0] = o[0] + S[i].x * qr[i];
+    o[1] = o[1] + S[i].y * qr[i];
+    o[2] = o[2] + S[i].z * qr[i];
+    o[3] = o[3] + S[i].w * qr[i];
   }
-  sync(c);
-  float delta[4];
+  col_sums(o);
+  if (c.lane < 4) {
+    uint32_t* cp = c.w.core + (size_t)c.xcd * 512 + hvl * kDk + vs * 16 + col4;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int col = c4 * 4 + j;
-    float recalled = 0.0f;
-#pragma unroll
-    for (int wv = 0; wv < kCompute; ++wv)
-#pragma unroll
-      for (int rw = 0; rw < 4; ++rw) recalled += D.sred[wv][rw][col];
-    delta[j] = (D.v[col] - recalled) * beta;
+    for (int j = 0; j < 4; ++j) cp[j] = tag_bf16(f2bf(o[j]), epoch_out);
   }
-  sync(c);  // sred is reused below
-  if (!c.control) {
-    S.x = S.x + kr * delta[0];
-    S.y = S.y + kr * delta[1];
-    S.z = S.z + kr * delta[2];
-    S.w = S.w + kr * delta[3];
-    float o[4] = {S.x * qr, S.y * qr, S.z * qr, S.w * qr};
-    *reinterpret_cast<float4*>(LF(Lp, state) + ((size_t)hv * kDk + k) * kDk + vs * 16 + c4 * 4) = S;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) o[j] = row_sum_mod4(o[j]);
-    if ((c.lane & 15) < 4) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) D.sred[c.wave][c.lane >> 4][c4 * 4 + j] = o[j];
-    }
-  }
-  sync(c);
-  if (c.tid < 16) {
-    float o = 0.0f;
-#pragma unroll
-    for (int wv = 0; wv < kCompute; ++wv)
-#pragma unroll
-      for (int rw = 0; rw < 4; ++rw) o += D.sred[wv][rw][c.tid];
-    D.core[c.tid] = f2bf(o);
-  }
-  sync(c);
+  return true;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1575,12 +1547,11 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, floa
 // Barrier schedule per token (C = control wave, W = compute waves; every step below ends
 // at one barrier that both pass):
 //   embed      C: token row into L.h                                   | 1
-//   in_proj    C: stage norm weight                                    | 1
+//   in_proj    C: norm weight landed in LDS                            | 1
 //              W: RMSNorm -> g_x, group sums                           | kNormBars
-//              W: consume blocks                                       | 1, then C: epilogue, signal
-//   delta      C: state, conv, inputs after the hand-off               | 1
-//              W: conv, gates, delta rule                              | kDnBars, then C: publish core
-//   out_proj   C: hand-off, core / z / norm weight                     | 1
+//              W: consume blocks                                       | 1, then C: epilogue (tagged)
+//   delta      C only: hand-off, conv, gates, delta rule, z; publishes the core (tagged)
+//   out_proj   C: hand-off, core                                       | 1
 //              W: GatedRMSNorm -> g_x, group sums                      | 3
 //              W: consume                                              | 1
 //              C: row-parallel partials, all-reduce, h into LDS        | 1
@@ -1640,10 +1611,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         sync(c);
       }
       if (kind == 0) {
-        fence(c);
-        sync(c);  // delta inputs staged
-        if (!L.ok) return stop();
-        dn_compute(c, Lp, L);
+        // the control wave runs the delta step meanwhile
         {  // gated norm + out_proj
           fence(c);
           const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
@@ -1914,21 +1882,9 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       if (kind == 0) {
         // ================= conv + gated delta step ===================================
         fence(c, kTDelta);
-        const bool ok = dn_stage(c, Lp, L);
-        if (!ok) return fail(1);
-        sync(c);
-        stamp(c, kTStaged);
-        {  // z of the XCD's four value heads for out_proj's gated norm, while the delta step runs
-          const Seg seg[1] = {{kLinZ, 512, L.zs}};
-          if (!gather_colpar<1, 4>(c, seg, c.epoch)) return fail(kDnBars + 1);  // through out_proj's first
-        }
-        for (int i = 0; i < kDnBars; ++i) sync(c);
         c.epoch += 1;
-        {
-          const int hvl = c.r >> 3, vs = c.r & 7;
-          if (c.lane < 16)
-            c.w.core[(size_t)c.xcd * 512 + hvl * kDk + vs * 16 + c.lane] = tag_bf16(L.u.dn.core[c.lane], c.epoch);
-        }
+        // the compute waves wait at out_proj's first barrier meanwhile
+        if (!dn_step(c, Lp, L, c.epoch - 1, c.epoch)) return fail(1);
         // ================= gated norm + out_proj (row-parallel) ======================
         {
           fence(c, kTOut);
