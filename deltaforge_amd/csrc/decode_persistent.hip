@@ -1547,8 +1547,8 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, floa
 // Barrier schedule per token (C = control wave, W = compute waves; every step below ends
 // at one barrier that both pass):
 //   embed      C: token row into L.h                                   | 1
-//   in_proj    C: norm weight landed in LDS                            | 1
-//              W: RMSNorm -> g_x, group sums                           | kNormBars
+//   in_proj    W: RMSNorm -> g_x, group sums (h, its sum of squares and| kNormBars
+//                 the norm weight are in LDS since the last barrier)
 //              W: consume blocks                                       | 1, then C: epilogue (tagged)
 //   delta      C only: hand-off, conv, gates, delta rule, z; publishes the core (tagged)
 //   out_proj   C: hand-off, core                                       | 1
@@ -1567,8 +1567,7 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, floa
 //   down       C: hand-off, gate|up column sums                        | 1
 //              W: SwiGLU -> g_x, group sums                            | kActBars
 //              then as o_proj
-//   head       C: stage norm weight                                    | 1
-//              W: RMSNorm                                              | kNormBars
+//   head       W: RMSNorm                                              | kNormBars
 //              W: consume head blocks, argmax per wave                 | 1
 //              C: logits, candidate, global argmax                     | 1
 // The control wave works on a phase's outputs (partials, logits) after that phase's last
@@ -1605,7 +1604,6 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       {  // input projection
         fence(c);
         const Gemv g = gemv_of(Lp, q, 0, c.xcd, c.r);
-        sync(c);
         norm_w(L, c, hidden, M.eps);
         gemv_consume(g, c, st, M, q, steps, L);
         sync(c);
@@ -1719,7 +1717,6 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       {  // gate|up + SwiGLU
         fence(c);
         const Gemv g = gemv_of(Lp, q, 2, c.xcd, c.r);
-        sync(c);
         norm_w(L, c, hidden, M.eps);
         gemv_consume(g, c, st, M, q, steps, L);
         sync(c);
@@ -1739,7 +1736,6 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
     {  // final norm + tied head
       fence(c);
       auto& H = L.hd;
-      sync(c);
       norm_w(L, c, hidden, M.eps);
       // tiles t_lo + wave + 8 j, all groups, from the weight stream
       const int ntw = head_tiles_of_wave(q, c.wave);
@@ -1862,8 +1858,8 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       {
         fence(c, kTProj);
         const Gemv g = gemv_of(Lp, q, 0, c.xcd, c.r);
-        wait_vm<0>();  // in_norm in L.nw (h is already in LDS)
-        sync(c);
+        // in_norm is in L.nw: its DMA was issued before the previous all-reduce's polls (or
+        // the embedding's loads), whose waits it completed by (in-order vmcnt)
         for (int i = 0; i < kNormBars; ++i) sync(c);
         // the next phase's small parameters, while the compute waves consume
         if (kind == 0) {
@@ -1994,8 +1990,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       {
         fence(c, kTGateUp);
         const Gemv g = gemv_of(Lp, q, 2, c.xcd, c.r);
-        wait_vm<0>();  // post_norm in L.nw
-        sync(c);
+        // post_norm is in L.nw (its DMA preceded the all-reduce's polls)
         for (int i = 0; i < kNormBars; ++i) sync(c);
         sync(c);  // blocks consumed
         c.epoch += 1;
@@ -2023,8 +2018,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
     {
       fence(c, kTHead);
       auto& H = L.hd;
-      wait_vm<0>();  // final_norm in L.nw
-      sync(c);
+      // final_norm is in L.nw (its DMA preceded the last all-reduce's polls)
       for (int i = 0; i < kNormBars; ++i) sync(c);
       sync(c);  // head blocks consumed, per-wave candidates in LDS
       c.epoch += 1;
