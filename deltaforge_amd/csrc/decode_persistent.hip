@@ -1552,7 +1552,7 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, floa
 //              W: consume blocks                                       | 1, then C: epilogue (tagged)
 //   delta      C only: hand-off, conv, gates, delta rule, z; publishes the core (tagged)
 //   out_proj   C: hand-off, core                                       | 1
-//              W: GatedRMSNorm -> g_x, group sums                      | 3
+//              W: GatedRMSNorm -> g_x, group sums                      | 1
 //              W: consume                                              | 1
 //              C: row-parallel partials, all-reduce, h into LDS        | 1
 //   attention  C: hand-off, q/k/v / norm weights; W: first KV tile     | 1
@@ -1615,22 +1615,22 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
             sync(c);
           if (!L.ok) return stop();
-          // GatedRMSNorm per 128-head, one element per thread (a head = 2 waves)
-          const int i = c.tid;
-          const float v = bf2f(g_x[i]);
-          const float ss = dsum(v * v);
-          if (c.lane == 0) L.red[c.wave] = ss;
-          sync(c);
-          const int h = i >> 7;
-          const float tot = L.red[2 * h] + L.red[2 * h + 1];
-          const float rr = 1.0f / sqrtf(tot / 128.0f + M.eps);
-          const float t = round_bf(bf2f(L.gnw[i & 127]) * round_bf(v * rr));
-          const uint16_t xb = f2bf(t * silu(L.zs[i]));
-          g_x[i] = xb;
-          const float gs = dsum(bf2f(xb));
-          if (c.lane == 0) L.red[16 + c.wave] = gs;
-          sync(c);
-          if (c.tid < 4) L.xs[c.tid] = kBias * (L.red[16 + 2 * c.tid] + L.red[16 + 2 * c.tid + 1]);
+          // GatedRMSNorm: wave h < 4 takes head h whole (elements 128 h + lane and + 64), so
+          // no partial crosses waves; each sum is the two 64-lane halves added in order
+          if (c.wave < 4) {
+            const int i0 = 128 * c.wave + c.lane, i1 = i0 + 64;
+            const float v0 = bf2f(g_x[i0]), v1 = bf2f(g_x[i1]);
+            const float tot = dsum(v0 * v0) + dsum(v1 * v1);
+            const float rr = 1.0f / sqrtf(tot / 128.0f + M.eps);
+            const float t0 = round_bf(bf2f(L.gnw[c.lane]) * round_bf(v0 * rr));
+            const float t1 = round_bf(bf2f(L.gnw[64 + c.lane]) * round_bf(v1 * rr));
+            const uint16_t xb0 = f2bf(t0 * silu(L.zs[i0]));
+            const uint16_t xb1 = f2bf(t1 * silu(L.zs[i1]));
+            g_x[i0] = xb0;
+            g_x[i1] = xb1;
+            const float gs = dsum(bf2f(xb0)) + dsum(bf2f(xb1));
+            if (c.lane == 0) L.xs[c.wave] = kBias * gs;
+          }
           sync(c);
           gemv_consume(g, c, st, M, q, steps, L);
           sync(c);
@@ -1890,8 +1890,6 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           sync(c);
           stamp(c, kTStaged);
           dma_row(LF(Lp, post_norm), L.nw, hidden, c.lane);
-          sync(c);
-          sync(c);
           sync(c);  // g_x, group sums
           sync(c);  // blocks consumed
           rowpar_epilogue(g, c, L, hidden);
