@@ -678,8 +678,8 @@ DF_DEVICE void issue_one(Stream& st, const Ctx& c) {
   st.left -= 1;
 }
 
-DF_DEVICE void fill(Stream& st, int steps, const Ctx& c) {
-  while (st.state == kStreaming && st.issued - st.consumed < kRing) {
+DF_DEVICE void fill(Stream& st, int steps, const Ctx& c, int upto = kRing) {
+  while (st.state == kStreaming && st.issued - st.consumed < upto) {
     if (st.left == 0) {
       open_run(st, steps);
       continue;
@@ -1682,12 +1682,6 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         // the split's KV loads are consumed (wait unconditionally: the compiler cannot pair
         // the first tile's prefetch with the loop, and the held stream has nothing in flight)
         wait_vm<0>();
-        // the weight stream resumes with o_proj
-        if (st.state == kHeld) {
-          st.state = kReleased;
-          open_run(st, steps);
-          fill(st, steps, c);
-        }
         // combine the waves' PV partials (into wave 0's row)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
@@ -1703,6 +1697,18 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           A.red[0][hh][d] = sum;
         }
         sync(c);
+        // the weight stream resumes with o_proj while the control wave merges the splits: two
+        // blocks per wave at a time, spaced out, so the refill (64 KB per CU) does not hold up
+        // the control wave's hand-off loads, which share the CU's memory pipeline
+        if (st.state == kHeld) {
+          st.state = kReleased;
+          open_run(st, steps);
+#pragma unroll 1
+          for (int k = 2; k <= kRing; k += 2) {
+            fill(st, steps, c, k);
+            if (k < kRing) __builtin_amdgcn_s_sleep(20);
+          }
+        }
         {  // o_proj (the merge runs on the control wave meanwhile)
           fence(c);
           const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
