@@ -1706,7 +1706,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
 #pragma unroll 1
           for (int k = 2; k <= kRing; k += 2) {
             fill(st, steps, c, k);
-            if (k < kRing) __builtin_amdgcn_s_sleep(20);
+            if (k < kRing) __builtin_amdgcn_s_sleep(10);
           }
         }
         {  // o_proj (the merge runs on the control wave meanwhile)
