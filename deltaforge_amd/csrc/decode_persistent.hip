@@ -1269,8 +1269,7 @@ DF_DEVICE bool dn_step(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_in, uint32_t 
                       {kLinZ, 512, L.zs}};
   if (!gather_colpar<5, 7>(c, seg, epoch_in)) return false;
   // conv + SiLU (fp32 sum in tap order, bf16, SiLU, bf16); history slots (pos+1)&3, (pos+2)&3,
-  // (pos+3)&3 hold positions pos-3, pos-2, pos-1. This unit owns its v slice; the (even value
-  // head, slice 0) unit owns the key head's q/k channels.
+  // (pos+3)&3 hold positions pos-3, pos-2, pos-1 (slot pos&3 is written at the end).
   float y[kCh];
 #pragma unroll
   for (int i = 0; i < kCh; ++i) {
@@ -1290,8 +1289,6 @@ DF_DEVICE bool dn_step(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_in, uint32_t 
       acc = acc + h2 * w2;
       acc = acc + x * w3;
       y[i] = round_bf(silu(round_bf(acc)));
-      const bool owner = ch >= 2 * kDk || ((hvl & 1) == 0 && vs == 0);
-      if (owner) LF(Lp, conv_ring)[(size_t)dn_channel(c, ch) * 4 + (c.pos & 3)] = f2bf(x);
     }
   }
   static_assert(kCh == 5 && kDk == 128, "q = channels l, l + 64; k = 128 + l, 192 + l; v = 256 + l");
@@ -1355,7 +1352,6 @@ DF_DEVICE bool dn_step(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_in, uint32_t 
     S[i].y = S[i].y + kr[i] * delta[1];
     S[i].z = S[i].z + kr[i] * delta[2];
     S[i].w = S[i].w + kr[i] * delta[3];
-    *reinterpret_cast<float4*>(sbase + (size_t)16 * i * kDk) = S[i];
     o[0] = o[0] + S[i].x * qr[i];
     o[1] = o[1] + S[i].y * qr[i];
     o[2] = o[2] + S[i].z * qr[i];
@@ -1366,6 +1362,17 @@ DF_DEVICE bool dn_step(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_in, uint32_t 
     uint32_t* cp = c.w.core + (size_t)c.xcd * 512 + hvl * kDk + vs * 16 + col4;
 #pragma unroll
     for (int j = 0; j < 4; ++j) cp[j] = tag_bf16(f2bf(o[j]), epoch_out);
+  }
+  // the stores nobody waits for go out after the core (a wave's memory operations leave in
+  // order): the new state slice, and this position's conv history slot of the channels this
+  // unit owns (its v slice; the key head's q/k for the (even value head, slice 0) unit)
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) *reinterpret_cast<float4*>(sbase + (size_t)16 * i * kDk) = S[i];
+#pragma unroll
+  for (int i = 0; i < kCh; ++i) {
+    const int ch = c.lane + 64 * i;
+    const bool owner = ch >= 2 * kDk || ((hvl & 1) == 0 && vs == 0);
+    if (ch < kDnCh && owner) LF(Lp, conv_ring)[(size_t)dn_channel(c, ch) * 4 + (c.pos & 3)] = f2bf(D.qkv_in[ch]);
   }
   return true;
 }
