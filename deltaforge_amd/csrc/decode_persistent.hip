@@ -1245,9 +1245,6 @@ DF_DEVICE bool dn_step(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_in, uint32_t 
   float* state = LF(Lp, state);
   const int row0 = c.lane >> 2, col4 = (c.lane & 3) * 4;
   float* sbase = state + ((size_t)hv * kDk + row0) * kDk + vs * 16 + col4;
-  // the state slice goes to LDS by DMA (no registers held across the hand-off poll)
-#pragma unroll
-  for (int i = 0; i < kRows; ++i) dma16(sbase + (size_t)16 * i * kDk, lds_addr(&D.S[i][0]));
   uint2 tp[kCh];
   uint64_t hs[kCh];
 #pragma unroll
@@ -1268,6 +1265,11 @@ DF_DEVICE bool dn_step(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_in, uint32_t 
                       {kLinA, 8, D.ab8},
                       {kLinZ, 512, L.zs}};
   if (!gather_colpar<5, 7>(c, seg, epoch_in)) return false;
+  // the state slice goes to LDS by DMA once the hand-off has landed: issued before the poll,
+  // its HBM round trip would be one more thing the poll's first round waits for (a wave's
+  // memory operations complete in order); here it overlaps the conv, norms and gates
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) dma16(sbase + (size_t)16 * i * kDk, lds_addr(&D.S[i][0]));
   // conv + SiLU (fp32 sum in tap order, bf16, SiLU, bf16); history slots (pos+1)&3, (pos+2)&3,
   // (pos+3)&3 hold positions pos-3, pos-2, pos-1 (slot pos&3 is written at the end).
   float y[kCh];
@@ -1315,8 +1317,9 @@ DF_DEVICE bool dn_step(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_in, uint32_t 
     qr[i] = D.q[row0 + 16 * i];
   }
   float4 S[kRows];
+  wait_vm<0>();  // the state DMA (the only memory operation since the poll)
 #pragma unroll
-  for (int i = 0; i < kRows; ++i) S[i] = D.S[i][c.lane];  // the poll's vmcnt(0) covered the DMA
+  for (int i = 0; i < kRows; ++i) S[i] = D.S[i][c.lane];
   float p[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < kRows; ++i) {
