@@ -64,9 +64,9 @@ GATE_UP_KERNEL = "w4_gemv_kernel<RMSNORM, SWIGLU> (post-attention norm + gate/up
 # WRITE_SIZE). Re-measure when the kernel changes.
 GATE_UP_TRAFFIC_BYTES = 12049 * 1024 * 2 + 18 * 1024
 # HBM bytes per decode token of the persistent kernel from the same calibrated PMC passes over
-# the timed 256-token launch (332,971,581 KiB fetched x 1.9998, 17,662,583 KiB written, / 256).
+# the timed 256-token launch (332,680,602 KiB fetched x 1.9998, 17,664,056 KiB written, / 256).
 # Re-measure when the kernel changes.
-PERSISTENT_TRAFFIC_BYTES_PER_TOKEN = 2734161517
+PERSISTENT_TRAFFIC_BYTES_PER_TOKEN = 2731843864
 
 
 def gate_up_bytes(cfg) -> int:
