@@ -44,6 +44,14 @@ class GatedDeltaArgs(C.Structure):
     ]
 
 
+class DeltaRuleArgs(C.Structure):
+    _fields_ = [
+        ("state_in", _vp), ("state_out", _vp), ("query", _vp), ("key", _vp), ("value", _vp), ("g", _vp),
+        ("beta", _vp), ("out", _vp),
+        ("batch", _i), ("heads", _i), ("key_dim", _i), ("value_dim", _i),
+    ]
+
+
 class AttnDecodeArgs(C.Structure):
     _fields_ = [
         ("q", _vp), ("k", _vp), ("v", _vp), ("q_norm_w", _vp), ("k_norm_w", _vp), ("inv_freq", _vp),
@@ -84,6 +92,8 @@ SIGNATURES = {
     "df_int4_repack": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
     "df_int4_dequant": (_i, [_vp, _vp, _i, _i, _vp, _vp]),
     "df_gated_delta_step": (_i, [C.POINTER(GatedDeltaArgs), _vp]),
+    "df_delta_rule_step": (_i, [C.POINTER(DeltaRuleArgs), _vp]),
+    "df_split_kv_decode_attention": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _sz, _vp]),
     "df_attention_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "df_attention_decode_splits": (_i, [_i, _i, _i]),
     "df_attention_decode": (_i, [C.POINTER(AttnDecodeArgs), _vp, _sz, _vp]),

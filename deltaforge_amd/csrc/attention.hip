@@ -59,6 +59,8 @@ DF_DEVICE void norm_rope4(float x[4], const uint16_t* norm_w, float eps, const f
     n[i] = round_bf(scaled * (1.0f + bf2f(norm_w[lane * 4 + i])));
   }
   const int half = rot / 2;
+  // dim d's partner d +- half sits half/4 lanes away; the xor reaches lane +- half/4 because
+  // the launcher admits only rotary dims with rot/8 a power of two
   float partner[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) partner[i] = __shfl_xor(n[i], half / 4, 64);
@@ -76,7 +78,16 @@ DF_DEVICE void norm_rope4(float x[4], const uint16_t* norm_w, float eps, const f
   }
 }
 
-__global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, AttnWs ws) {
+// What the plain entry point (no prologue, no gate: df_split_kv_decode_attention) changes in
+// the kernel: the query comes ready as [B][Hq][D], every one of key_len cached keys is
+// attended (no new key), the caller's scale applies, and the merged output is stored as is.
+struct PlainAttn {
+  int key_len;
+  float scale;
+};
+
+template <bool PLAIN>
+__global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, AttnWs ws, PlainAttn pl) {
   __shared__ __align__(16) uint16_t q_s[kQPerKv][kHd];
   __shared__ __align__(16) uint16_t knew[kHd];
   __shared__ __align__(16) uint16_t vnew[kHd];
@@ -89,11 +100,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int S = p.splits;
-  const int pos = *p.position;
+  // PLAIN: no new key (pos -1 matches no cache row), key_len keys.
+  const int pos = PLAIN ? -1 : *p.position;
   // A position past the cache would write out of bounds; the host cannot see the device
   // scalar, so every workgroup refuses here (the output is left unwritten).
-  if (pos < 0 || pos >= p.max_len) return;
-  const int nkeys = pos + 1;
+  if (!PLAIN && (pos < 0 || pos >= p.max_len)) return;
+  const int nkeys = PLAIN ? pl.key_len : pos + 1;
   const int per = (nkeys + S - 1) / S;
   const int j0 = min(split * per, nkeys);
   const int j1 = min(j0 + per, nkeys);
@@ -101,7 +113,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
   const size_t kv_base = ((size_t)b * p.num_kv_heads + kvh) * p.max_len;
 
   // Prologue: queries, new key, new value.
-  {
+  if (PLAIN) {
+    const int hq = kvh * kQPerKv + wave;
+    *reinterpret_cast<uint2*>(&q_s[wave][lane * 4]) =
+        *reinterpret_cast<const uint2*>(p.q + ((size_t)b * p.num_q_heads + hq) * kHd + lane * 4);
+  } else {
     const int hq = kvh * kQPerKv + wave;
     const uint16_t* src = p.q + (size_t)b * p.ld_q + (size_t)hq * 2 * kHd + lane * 4;
     float x[4];
@@ -125,7 +141,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
     }
   }
   __syncthreads();
-  const bool owner = pos >= j0 && pos < j1;
+  const bool owner = !PLAIN && pos >= j0 && pos < j1;
   if (owner) {
     uint16_t* kd = p.k_cache + (kv_base + pos) * kHd;
     uint16_t* vd = p.v_cache + (kv_base + pos) * kHd;
@@ -134,7 +150,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
   }
 
   const int col = lane & 15, slot = lane >> 4;
-  const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
+  const float scale = PLAIN ? pl.scale : 1.0f / sqrtf(static_cast<float>(kHd));
   float m_run = -INFINITY, l_run = 0.0f;  // for head `wave`
   float acc[kQPerKv][4];
 #pragma unroll
@@ -292,6 +308,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
     }
     for (; s < S; ++s) num0 += w[s] * load_through(accp + (size_t)s * kHd);
     const float o = round_bf(((num0 + num1) + (num2 + num3)) / den_s[h]);
+    if (PLAIN) {
+      p.out[((size_t)b * p.num_q_heads + hq0 + h) * kHd + tid] = f2bf(o);
+      continue;
+    }
     const float gx = bf2f(p.q[(size_t)b * p.ld_q + (size_t)(hq0 + h) * 2 * kHd + kHd + tid]);
     const float gate = round_bf(p.gate == 0 ? sigmoid(gx) : silu(gx));
     p.out[(size_t)b * p.num_q_heads * kHd + (size_t)(hq0 + h) * kHd + tid] = f2bf(o * gate);
@@ -326,7 +346,8 @@ int df_attention_decode(const DfAttnDecodeArgs* args, void* workspace, size_t wo
   if (!args) return DF_BAD_ARGUMENT;
   const DfAttnDecodeArgs& a = *args;
   if (a.head_dim != kHd || a.num_kv_heads < 1 || a.num_q_heads != a.num_kv_heads * kQPerKv || a.batch < 1 ||
-      a.splits < 1 || a.splits > kMaxSplits || a.rotary_dim % 8 || a.rotary_dim > kHd || a.rotary_dim < 8 || a.max_len < 1 ||
+      a.splits < 1 || a.splits > kMaxSplits || a.rotary_dim % 8 || a.rotary_dim > kHd || a.rotary_dim < 8 ||
+      ((a.rotary_dim / 8) & (a.rotary_dim / 8 - 1)) || a.max_len < 1 ||
       !a.q || !a.k || !a.v || !a.q_norm_w || !a.k_norm_w || !a.inv_freq || !a.k_cache || !a.v_cache ||
       !a.position || !a.out || (a.gate != 0 && a.gate != 1))
     return DF_BAD_ARGUMENT;
@@ -342,7 +363,42 @@ int df_attention_decode(const DfAttnDecodeArgs* args, void* workspace, size_t wo
     ws.acc = reinterpret_cast<float*>(p + counters);
     ws.ml = ws.acc + (size_t)a.batch * a.num_q_heads * a.splits * kHd;
   }
-  hipLaunchKernelGGL(attn_decode_kernel, dim3(a.splits, a.num_kv_heads, a.batch), dim3(256), 0, stream, a, ws);
+  hipLaunchKernelGGL(attn_decode_kernel<false>, dim3(a.splits, a.num_kv_heads, a.batch), dim3(256), 0, stream, a,
+                     ws, PlainAttn{0, 0.0f});
+  DF_RETURN_LAUNCH_STATUS();
+}
+
+int df_split_kv_decode_attention(const uint16_t* query, const uint16_t* key, const uint16_t* value, int batch,
+                                 int num_q_heads, int num_kv_heads, int key_len, int head_dim, float scale,
+                                 int splits, uint16_t* out, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream) {
+  if (!query || !key || !value || !out || batch < 1 || num_kv_heads < 1 || num_q_heads != num_kv_heads * kQPerKv ||
+      head_dim != kHd || key_len < 1 || splits < 1 || splits > kMaxSplits || !(scale == scale))
+    return DF_BAD_ARGUMENT;
+  if (!workspace ||
+      workspace_bytes < df_attention_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, kHd, splits))
+    return DF_WORKSPACE_TOO_SMALL;
+  DfAttnDecodeArgs a{};
+  a.q = query;
+  a.k_cache = const_cast<uint16_t*>(key);  // read only in the plain kernel
+  a.v_cache = const_cast<uint16_t*>(value);
+  a.out = out;
+  a.batch = batch;
+  a.num_q_heads = num_q_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.head_dim = kHd;
+  a.max_len = key_len;
+  a.splits = splits;
+  AttnWs ws;
+  {
+    char* p = reinterpret_cast<char*>(workspace);
+    const size_t counters = ((size_t)batch * num_kv_heads * sizeof(int) + 255) & ~(size_t)255;
+    ws.counters = reinterpret_cast<int*>(p);
+    ws.acc = reinterpret_cast<float*>(p + counters);
+    ws.ml = ws.acc + (size_t)batch * num_q_heads * splits * kHd;
+  }
+  hipLaunchKernelGGL(attn_decode_kernel<true>, dim3(splits, num_kv_heads, batch), dim3(256), 0, stream, a, ws,
+                     PlainAttn{key_len, scale});
   DF_RETURN_LAUNCH_STATUS();
 }
 

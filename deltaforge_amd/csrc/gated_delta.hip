@@ -24,6 +24,92 @@ constexpr int kDk = 128;
 constexpr int kVSlice = 32;
 constexpr int kDeltaThreads = 256;
 
+// The rule on one workgroup's 128 x 32 fp32 state slice, S held 4 rows x 4 columns per
+// thread (thread t: rows 4 (t >> 3) .. +3, columns 4 (t & 7) .. +3), with q/k (128) and the
+// slice's v (32) in LDS: S *= eg; r = k^T S; delta = (v - r) beta; S += k delta^T; o = q^T S
+// (reference.py:450-458, in the reference's rounding: separate products and sums, no fused
+// multiply-add). The updated slice goes to `sout` (row stride `ld`), o to store(col, o) for
+// the slice's 32 columns.
+template <class Store>
+DF_DEVICE void delta_rule_slice(float4 (&S)[4], float* sout, int ld, const float* q_s, const float* k_s,
+                                const float* v_s, float eg, float beta, float (&red)[2][4][kVSlice], int tid,
+                                Store&& store) {
+#pragma clang fp contract(off)
+  const int lane = tid & 63, wave = tid >> 6;
+  const int c4 = tid & 7, rg = tid >> 3;
+  // Decay and recall.
+  float kr[4], qr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    kr[r] = k_s[rg * 4 + r];
+    qr[r] = q_s[rg * 4 + r];
+  }
+  float part[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    S[r].x = S[r].x * eg;
+    S[r].y = S[r].y * eg;
+    S[r].z = S[r].z * eg;
+    S[r].w = S[r].w * eg;
+    part[0] += S[r].x * kr[r];
+    part[1] += S[r].y * kr[r];
+    part[2] += S[r].z * kr[r];
+    part[3] += S[r].w * kr[r];
+  }
+  // Reduce over the 8 row groups of a wave (lanes c4 + 8j), then over the 4 waves.
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float v = part[j];
+    v += __shfl_xor(v, 8, 64);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    part[j] = v;
+  }
+  if (lane < 8) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[0][wave][c4 * 4 + j] = part[j];
+  }
+  __syncthreads();
+  float delta[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int col = c4 * 4 + j;
+    const float recalled = red[0][0][col] + red[0][1][col] + red[0][2][col] + red[0][3][col];
+    delta[j] = (v_s[col] - recalled) * beta;
+  }
+
+  // Rank-1 update and readout.
+  float outp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float kv0 = kr[r] * delta[0], kv1 = kr[r] * delta[1], kv2 = kr[r] * delta[2], kv3 = kr[r] * delta[3];
+    S[r].x = S[r].x + kv0;
+    S[r].y = S[r].y + kv1;
+    S[r].z = S[r].z + kv2;
+    S[r].w = S[r].w + kv3;
+    outp[0] += S[r].x * qr[r];
+    outp[1] += S[r].y * qr[r];
+    outp[2] += S[r].z * qr[r];
+    outp[3] += S[r].w * qr[r];
+    *reinterpret_cast<float4*>(sout + (size_t)(rg * 4 + r) * ld) = S[r];
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float v = outp[j];
+    v += __shfl_xor(v, 8, 64);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    outp[j] = v;
+  }
+  if (lane < 8) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[1][wave][c4 * 4 + j] = outp[j];
+  }
+  __syncthreads();
+  if (tid < kVSlice) store(tid, red[1][0][tid] + red[1][1][tid] + red[1][2][tid] + red[1][3][tid]);
+}
+
+
 __global__ __launch_bounds__(kDeltaThreads) void gated_delta_step_kernel(DfGatedDeltaArgs p) {
 #pragma clang fp contract(off)
   __shared__ float q_s[kDk], k_s[kDk], v_s[kVSlice];
@@ -122,80 +208,43 @@ __global__ __launch_bounds__(kDeltaThreads) void gated_delta_step_kernel(DfGated
   }
   __syncthreads();
 
-  // 4. Decay and recall.
-  const float eg = scal[0], beta = scal[1];
-  float kr[4], qr[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    kr[r] = k_s[rg * 4 + r];
-    qr[r] = q_s[rg * 4 + r];
-  }
-  float part[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    S[r].x = S[r].x * eg;
-    S[r].y = S[r].y * eg;
-    S[r].z = S[r].z * eg;
-    S[r].w = S[r].w * eg;
-    part[0] += S[r].x * kr[r];
-    part[1] += S[r].y * kr[r];
-    part[2] += S[r].z * kr[r];
-    part[3] += S[r].w * kr[r];
-  }
-  // Reduce over the 8 row groups of a wave (lanes c4 + 8j), then over the 4 waves.
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float v = part[j];
-    v += __shfl_xor(v, 8, 64);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    part[j] = v;
-  }
-  if (lane < 8) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) red[0][wave][c4 * 4 + j] = part[j];
-  }
-  __syncthreads();
-  float delta[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int col = c4 * 4 + j;
-    const float recalled = red[0][0][col] + red[0][1][col] + red[0][2][col] + red[0][3][col];
-    delta[j] = (v_s[col] - recalled) * beta;
-  }
+  // 4-5. The rule itself, shared with delta_rule_step_kernel.
+  delta_rule_slice(S, sbase, p.head_v_dim, q_s, k_s, v_s, scal[0], scal[1], red, tid,
+                   [&](int col, float o) {
+                     p.out[((size_t)b * p.num_v_heads + h) * p.head_v_dim + vs * kVSlice + col] = f2bf(o);
+                   });
+}
 
-  // 5. Rank-1 update and readout.
-  float outp[4] = {0.f, 0.f, 0.f, 0.f};
+// One delta-rule step on already-normalised fp32 inputs (the reference's
+// deltaforge::delta_rule_step, kernels/gated_delta_step.py:109-186): per workgroup
+// (batch b, head h, value slice vs of 32 columns), S = state_in slice; S *= exp(g);
+// r = k^T S; delta = (v - r) beta; S += k delta^T; o = q^T S; state_out slice = S, out = o
+// (fp32). state_out may alias state_in: each workgroup reads its slice before writing it.
+__global__ __launch_bounds__(kDeltaThreads) void delta_rule_step_kernel(DfDeltaRuleArgs p) {
+#pragma clang fp contract(off)
+  __shared__ float q_s[kDk], k_s[kDk], v_s[kVSlice];
+  __shared__ float red[2][4][kVSlice];
+  const int tid = threadIdx.x;
+  const int vsplits = p.value_dim / kVSlice;
+  const int vs = blockIdx.x % vsplits;
+  const int bh = blockIdx.x / vsplits;  // b * heads + h
+  const int c4 = tid & 7, rg = tid >> 3;
+  const size_t head = (size_t)bh * kDk * p.value_dim;
+  const float* sin = p.state_in + head + vs * kVSlice + c4 * 4;
+  float4 S[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const float kv0 = kr[r] * delta[0], kv1 = kr[r] * delta[1], kv2 = kr[r] * delta[2], kv3 = kr[r] * delta[3];
-    S[r].x = S[r].x + kv0;
-    S[r].y = S[r].y + kv1;
-    S[r].z = S[r].z + kv2;
-    S[r].w = S[r].w + kv3;
-    outp[0] += S[r].x * qr[r];
-    outp[1] += S[r].y * qr[r];
-    outp[2] += S[r].z * qr[r];
-    outp[3] += S[r].w * qr[r];
-    *reinterpret_cast<float4*>(sbase + (size_t)(rg * 4 + r) * p.head_v_dim) = S[r];
+  for (int r = 0; r < 4; ++r) S[r] = *reinterpret_cast<const float4*>(sin + (size_t)(rg * 4 + r) * p.value_dim);
+  if (tid < kDk) {
+    q_s[tid] = p.query[(size_t)bh * kDk + tid];
+    k_s[tid] = p.key[(size_t)bh * kDk + tid];
   }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float v = outp[j];
-    v += __shfl_xor(v, 8, 64);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    outp[j] = v;
-  }
-  if (lane < 8) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) red[1][wave][c4 * 4 + j] = outp[j];
-  }
+  if (tid < kVSlice) v_s[tid] = p.value[(size_t)bh * p.value_dim + vs * kVSlice + tid];
+  const float eg = expf(p.g[bh]);
+  const float beta = p.beta[bh];
   __syncthreads();
-  if (tid < kVSlice) {
-    const float o = red[1][0][tid] + red[1][1][tid] + red[1][2][tid] + red[1][3][tid];
-    p.out[((size_t)b * p.num_v_heads + h) * p.head_v_dim + vs * kVSlice + tid] = f2bf(o);
-  }
+  float* sout = p.state_out + head + vs * kVSlice + c4 * 4;
+  delta_rule_slice(S, sout, p.value_dim, q_s, k_s, v_s, eg, beta, red, tid,
+                   [&](int col, float o) { p.out[(size_t)bh * p.value_dim + vs * kVSlice + col] = o; });
 }
 
 }  // namespace df
@@ -219,5 +268,17 @@ extern "C" int df_gated_delta_step(const DfGatedDeltaArgs* args, hipStream_t str
   if (a.ld_qkv < C || a.ld_ab < a.num_v_heads) return DF_BAD_ARGUMENT;
   const int grid = a.batch * a.num_v_heads * (a.head_v_dim / kVSlice);
   hipLaunchKernelGGL(gated_delta_step_kernel, dim3(grid), dim3(kDeltaThreads), 0, stream, a);
+  DF_RETURN_LAUNCH_STATUS();
+}
+
+extern "C" int df_delta_rule_step(const DfDeltaRuleArgs* args, hipStream_t stream) {
+  using namespace df;
+  if (!args) return DF_BAD_ARGUMENT;
+  const DfDeltaRuleArgs& a = *args;
+  if (a.batch < 1 || a.heads < 1 || a.key_dim != kDk || a.value_dim < kVSlice || a.value_dim % kVSlice ||
+      !a.state_in || !a.state_out || !a.query || !a.key || !a.value || !a.g || !a.beta || !a.out)
+    return DF_BAD_ARGUMENT;
+  const int grid = a.batch * a.heads * (a.value_dim / kVSlice);
+  hipLaunchKernelGGL(delta_rule_step_kernel, dim3(grid), dim3(kDeltaThreads), 0, stream, a);
   DF_RETURN_LAUNCH_STATUS();
 }

@@ -53,7 +53,7 @@ REPLACEABLE_OPS = frozenset(
 
 
 class RegistryError(RuntimeError):
-    """Raised when a registration would violate a registry invariant."""
+    """A registration or lookup that would break the registry's rules."""
 
 
 @dataclass(frozen=True)
@@ -67,11 +67,30 @@ class KernelEntry:
 
 
 class KernelRegistry:
-    """Kernel name -> entry, with the one-champion-per-operation invariant enforced."""
+    """Kernels by name, plus an index ``operation -> champion name``.
+
+    The index is the only place a champion is recorded, so "at most one champion per
+    operation" holds by construction: every status change goes through ``_set_status``,
+    which keeps the entry and the index in step. ``check_invariants`` re-derives the index
+    from the entries and compares, which catches an entry edited behind the registry's back.
+    """
 
     def __init__(self, replaceable_ops: frozenset[str] = REPLACEABLE_OPS) -> None:
-        self._replaceable_ops = replaceable_ops
+        self._replaceable_ops = frozenset(replaceable_ops)
         self._entries: dict[str, KernelEntry] = {}
+        self._champion_of: dict[str, str] = {}  # operation -> name of its champion
+
+    # -- mutation ------------------------------------------------------------------------
+
+    def _set_status(self, entry: KernelEntry, status: KernelStatus) -> KernelEntry:
+        op = entry.replaces
+        if self._champion_of.get(op) == entry.name and status is not KernelStatus.CHAMPION:
+            del self._champion_of[op]
+        if status is KernelStatus.CHAMPION:
+            self._champion_of[op] = entry.name
+        updated = entry if entry.status is status else replace(entry, status=status)
+        self._entries[entry.name] = updated
+        return updated
 
     def register(
         self,
@@ -83,74 +102,84 @@ class KernelRegistry:
         hypothesis: str | None = None,
         notes: str = "",
     ) -> KernelEntry:
+        """Add a kernel. A new champion may only take an operation that has none; use
+        ``promote`` to replace a sitting champion."""
         if name in self._entries:
-            raise RegistryError(f"kernel {name!r} is already registered")
+            raise RegistryError(f"{name!r} is registered already; unregister it first to replace it")
         if replaces not in self._replaceable_ops:
-            raise RegistryError(
-                f"kernel {name!r} replaces unknown operation {replaces!r}; "
-                f"known operations: {sorted(self._replaceable_ops)}"
-            )
+            known = ", ".join(sorted(self._replaceable_ops))
+            raise RegistryError(f"{name!r}: {replaces!r} is not a replaceable operation (one of: {known})")
         status = KernelStatus(status)
-        if status is KernelStatus.CHAMPION:
-            incumbent = self.champion(replaces)
-            if incumbent is not None:
-                raise RegistryError(
-                    f"cannot register {name!r} as champion of {replaces!r}: {incumbent.name!r} already "
-                    "holds it; promote() demotes the incumbent in the same step"
-                )
-        entry = KernelEntry(name=name, impl=impl, replaces=replaces, status=status, hypothesis=hypothesis, notes=notes)
-        self._entries[name] = entry
-        return entry
+        sitting = self._champion_of.get(replaces)
+        if status is KernelStatus.CHAMPION and sitting is not None:
+            raise RegistryError(
+                f"{replaces!r} already has the champion {sitting!r}; register {name!r} as a candidate "
+                "and promote() it, which retires the sitting champion in the same step"
+            )
+        entry = KernelEntry(name=name, impl=impl, replaces=replaces, status=KernelStatus.CANDIDATE,
+                            hypothesis=hypothesis, notes=notes)
+        return self._set_status(entry, status)
 
     def promote(self, name: str) -> KernelEntry:
-        """Make ``name`` the champion of its operation, retiring the incumbent (never two, never none)."""
+        """Make ``name`` its operation's champion; the previous champion (if any) is retired
+        in the same call, so the operation never has two champions or, in between, none."""
         entry = self.get(name)
-        if entry.status is KernelStatus.CHAMPION:
+        sitting = self._champion_of.get(entry.replaces)
+        if sitting == name:
             return entry
-        incumbent = self.champion(entry.replaces)
-        if incumbent is not None:
-            self._entries[incumbent.name] = replace(incumbent, status=KernelStatus.RETIRED)
-        promoted = replace(entry, status=KernelStatus.CHAMPION)
-        self._entries[name] = promoted
-        return promoted
+        if sitting is not None:
+            self._set_status(self._entries[sitting], KernelStatus.RETIRED)
+        return self._set_status(entry, KernelStatus.CHAMPION)
 
     def retire(self, name: str) -> KernelEntry:
-        retired = replace(self.get(name), status=KernelStatus.RETIRED)
-        self._entries[name] = retired
-        return retired
+        return self._set_status(self.get(name), KernelStatus.RETIRED)
 
     def unregister(self, name: str) -> None:
+        entry = self.get(name)
+        if self._champion_of.get(entry.replaces) == name:
+            del self._champion_of[entry.replaces]
         del self._entries[name]
 
     def clear(self) -> None:
-        self._entries.clear()
+        self._entries = {}
+        self._champion_of = {}
+
+    # -- queries -------------------------------------------------------------------------
 
     def get(self, name: str) -> KernelEntry:
-        try:
-            return self._entries[name]
-        except KeyError:
-            raise RegistryError(f"no kernel registered as {name!r}") from None
+        entry = self._entries.get(name)
+        if entry is None:
+            raise RegistryError(f"unknown kernel {name!r}")
+        return entry
 
     def champion(self, replaces: str) -> KernelEntry | None:
-        found = [e for e in self._entries.values() if e.replaces == replaces and e.status is KernelStatus.CHAMPION]
-        if len(found) > 1:  # pragma: no cover - register/promote make this unreachable
-            raise RegistryError(f"registry invariant violated: {len(found)} champions for {replaces!r}")
-        return found[0] if found else None
+        name = self._champion_of.get(replaces)
+        return None if name is None else self._entries[name]
 
     def champions(self) -> dict[str, KernelEntry]:
-        return {op: e for op in sorted(self._replaceable_ops) if (e := self.champion(op)) is not None}
+        """``operation -> champion`` for every operation that has one, in name order."""
+        return {op: self._entries[self._champion_of[op]] for op in sorted(self._champion_of)}
 
     def for_op(self, replaces: str) -> tuple[KernelEntry, ...]:
+        """Every kernel registered against ``replaces``, whatever its status, in
+        registration order."""
         return tuple(e for e in self._entries.values() if e.replaces == replaces)
 
     def check_invariants(self) -> None:
-        for op in self._replaceable_ops:
-            self.champion(op)
-        for name, entry in self._entries.items():
-            if entry.name != name:
-                raise RegistryError(f"entry keyed {name!r} carries name {entry.name!r}")
+        """Rebuild the champion index from the entries and compare it with the stored one."""
+        derived: dict[str, str] = {}
+        for key, entry in self._entries.items():
+            if key != entry.name:
+                raise RegistryError(f"the entry stored under {key!r} is named {entry.name!r}")
             if entry.replaces not in self._replaceable_ops:
-                raise RegistryError(f"kernel {name!r} replaces unknown operation {entry.replaces!r}")
+                raise RegistryError(f"{key!r} replaces {entry.replaces!r}, which is not a replaceable operation")
+            if entry.status is KernelStatus.CHAMPION:
+                if entry.replaces in derived:
+                    raise RegistryError(
+                        f"{entry.replaces!r} has two champions: {derived[entry.replaces]!r} and {key!r}")
+                derived[entry.replaces] = key
+        if derived != self._champion_of:
+            raise RegistryError(f"champion index {self._champion_of} disagrees with the entries {derived}")
 
     def __len__(self) -> int:
         return len(self._entries)
@@ -159,10 +188,10 @@ class KernelRegistry:
         return name in self._entries
 
     def __iter__(self) -> Iterator[KernelEntry]:
-        return iter(self._entries.values())
+        return iter(tuple(self._entries.values()))
 
     def __repr__(self) -> str:
-        return f"KernelRegistry({len(self._entries)} kernels, {len(self.champions())} champions)"
+        return f"<KernelRegistry: {len(self)} kernels, champions for {len(self._champion_of)} operations>"
 
 
 #: The process-wide registry.
@@ -173,20 +202,18 @@ CHECK_BUILDERS: dict[str, Callable[..., tuple]] = {}
 
 
 def register_checks(kernel_name: str, builder: Callable[..., tuple]) -> None:
-    if kernel_name in CHECK_BUILDERS:
-        raise ValueError(f"checks for kernel {kernel_name!r} are already registered")
-    CHECK_BUILDERS[kernel_name] = builder
+    """Attach the per-op correctness checks of ``kernel_name`` (one builder per kernel)."""
+    previous = CHECK_BUILDERS.setdefault(kernel_name, builder)
+    if previous is not builder:
+        raise ValueError(f"{kernel_name!r} has a check builder already")
 
 
 def build_kernel_checks(model, *, registry: KernelRegistry | None = None, **kwargs) -> tuple:
-    """Every champion's per-op checks against ``model`` (kernels without a builder are skipped)."""
-    registry = REGISTRY if registry is None else registry
-    checks: list = []
-    for entry in registry.champions().values():
-        builder = CHECK_BUILDERS.get(entry.name)
-        if builder is not None:
-            checks.extend(builder(model, **kwargs))
-    return tuple(checks)
+    """The checks of every champion that has a builder, champions in operation order;
+    ``kwargs`` (device, dtype, seed) go to each builder unchanged."""
+    reg = REGISTRY if registry is None else registry
+    builders = [CHECK_BUILDERS[e.name] for e in reg.champions().values() if e.name in CHECK_BUILDERS]
+    return tuple(check for build in builders for check in build(model, **kwargs))
 
 
 # -- registered kernels --------------------------------------------------------------------
@@ -224,4 +251,19 @@ REGISTRY.register(
     notes="Every layer of every decode step in one persistent launch; the 8 XCDs act as 8 tensor-parallel "
           "ranks (column-parallel projections, row-parallel out/down with a cross-XCD all-reduce).")
 
+# The reference's two standalone ops with their own signatures (its hypotheses 007 and 008):
+# candidates beside the fused champions of the same operations, for call sites written
+# against deltaforge::delta_rule_step / deltaforge::split_kv_decode_attention.
+REGISTRY.register(
+    "hip_delta_rule_step", impl=_hip.delta_rule_step, replaces="gated_delta_rule", status=KernelStatus.CANDIDATE,
+    notes="deltaforge::delta_rule_step's signature: one step on normalised fp32 q/k/v, g, beta; "
+          "(out, new_state) fp32.")
+REGISTRY.register(
+    "hip_split_kv_decode_attention", impl=_hip.split_kv_decode_attention, replaces="gqa_attention",
+    status=KernelStatus.CANDIDATE,
+    notes="deltaforge::split_kv_decode_attention's signature: single-token GQA over a whole cache, KV scan split "
+          "and merged by log-sum-exp.")
+
 register_checks("hip_tiled_gemv_int4", _hip.tiled_gemv_int4_checks)
+register_checks("hip_delta_rule_step", _hip.delta_rule_step_checks)
+register_checks("hip_split_kv_decode_attention", _hip.split_kv_decode_attention_checks)

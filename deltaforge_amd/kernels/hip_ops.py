@@ -14,6 +14,8 @@ the C ABI of ``libdeltaforge_hip.so`` on the current stream.
 | ``add_rms_norm``           | ``deltaforge::add_rms_norm`` (kernels/fused_rmsnorm_residual.py:164-198) |
 | ``partial_rope``           | ``deltaforge::partial_rope`` (kernels/fused_rope.py:97-158) |
 | ``fused_causal_conv_step`` | ``deltaforge::fused_causal_conv_step`` (kernels/fused_causal_conv.py:136-181) |
+| ``delta_rule_step``        | ``deltaforge::delta_rule_step`` (kernels/gated_delta_step.py:109-186) |
+| ``split_kv_decode_attention`` | ``deltaforge::split_kv_decode_attention`` (kernels/flash_decode_splitkv.py:177-261) |
 | ``gated_delta_decode``     | ``GatedDeltaNet.forward``'s decode middle (reference.py:512-550) |
 | ``gated_attention_decode`` | ``GatedAttention.forward``'s decode branch (reference.py:610-677) |
 """
@@ -30,11 +32,15 @@ from .. import ops
 __all__ = [
     "add_rms_norm",
     "apply_partial_rope",
+    "delta_rule_step",
+    "delta_rule_step_checks",
     "fused_causal_conv_step",
     "gated_attention_decode",
     "gated_delta_decode",
     "rms_norm",
     "silu_mul",
+    "split_kv_decode_attention",
+    "split_kv_decode_attention_checks",
     "static_decode_engine",
     "tiled_gemv_int4",
     "tiled_gemv_int4_checks",
@@ -242,6 +248,83 @@ def gated_attention_decode(
 @gated_attention_decode.register_fake
 def _(q_gate, k, v, q_norm_w, k_norm_w, inv_freq, k_cache, v_cache, position, num_q_heads, sigmoid_gate, eps):
     return q_gate.new_empty((q_gate.shape[0], num_q_heads * k_cache.shape[-1]))
+
+
+@torch.library.custom_op("deltaforge_amd::delta_rule_step", mutates_args=())
+def delta_rule_step(state: Tensor, query: Tensor, key: Tensor, value: Tensor, g: Tensor,
+                    beta: Tensor) -> tuple[Tensor, Tensor]:
+    """One delta-rule step, ``(output, new_state)``: ``state (B, H, Dk, Dv)`` fp32,
+    ``query``/``key`` ``(B, H, Dk)`` already l2-normed (the query scaled by ``Dk**-0.5``),
+    ``value (B, H, Dv)``, log-space decay ``g`` and ``beta`` ``(B, H)``; the output is fp32."""
+    return ops.delta_rule_step(state, query, key, value, g, beta)
+
+
+@delta_rule_step.register_fake
+def _(state, query, key, value, g, beta):
+    batch, heads, _, value_dim = state.shape
+    return state.new_empty((batch, heads, value_dim)), torch.empty_like(state)
+
+
+@torch.library.custom_op("deltaforge_amd::split_kv_decode_attention", mutates_args=())
+def split_kv_decode_attention(query: Tensor, key: Tensor, value: Tensor, scale: float, splits: int) -> Tensor:
+    """Single-token GQA attention, ``query (B, Hq, D)`` over ``key``/``value``
+    ``(B, Hkv, L, D)`` with the KV scan split ``splits`` ways and merged by log-sum-exp."""
+    return ops.split_kv_decode_attention(query, key, value, scale, splits)
+
+
+@split_kv_decode_attention.register_fake
+def _(query, key, value, scale, splits):
+    return torch.empty_like(query)
+
+
+def delta_rule_step_checks(model=None, *, device="cuda", dtype=None, seed: int = 0) -> tuple:
+    """The step against the oracle's restatement of the reference loop body
+    (reference.py:450-458) at Qwen3.5's DeltaNet head shape, batch 1 and 8: state within 1e-4
+    (the north star's bar for the fp32 state), output within atol 2e-2 / rtol 1e-2."""
+    from oracle.model import delta_rule_step as oracle_step
+
+    from ..harness.correctness import check_kernel
+
+    gen = torch.Generator().manual_seed(seed)
+    checks = []
+    for batch in (1, 8):
+        state = torch.randn((batch, 32, 128, 128), generator=gen) * 0.1
+        q = torch.nn.functional.normalize(torch.randn((batch, 32, 128), generator=gen), dim=-1) / 128 ** 0.5
+        k = torch.nn.functional.normalize(torch.randn((batch, 32, 128), generator=gen), dim=-1)
+        v = torch.randn((batch, 32, 128), generator=gen)
+        g = -torch.nn.functional.softplus(torch.randn((batch, 32), generator=gen))
+        beta = torch.sigmoid(torch.randn((batch, 32), generator=gen))
+        want_out, want_state = oracle_step(state, q, k, v, g, beta)
+        got_out, got_state = delta_rule_step(*(t.to(device) for t in (state, q, k, v, g, beta)))
+        checks.append(check_kernel(f"hip_delta_rule_step state B={batch}", lambda: want_state, lambda: got_state.cpu(),
+                                   replaces="gated_delta_rule", atol=1e-4, rtol=0.0))
+        checks.append(check_kernel(f"hip_delta_rule_step out B={batch}", lambda: want_out, lambda: got_out.cpu(),
+                                   replaces="gated_delta_rule", atol=2e-2, rtol=1e-2))
+    return tuple(checks)
+
+
+def split_kv_decode_attention_checks(model=None, *, device="cuda", dtype=None, seed: int = 0) -> tuple:
+    """The reference's own cases for the op (flash_decode_splitkv.py:365-372: batch 1 and 32
+    at 2048 keys, fewer keys than splits, a key count no tile divides) at Qwen3.5's attention
+    head shape, against the oracle's expression of the reference layer (gqa_decode.py:322-335)."""
+    from oracle.ops import decode_attention
+
+    from ..harness.correctness import check_kernel
+
+    gen = torch.Generator().manual_seed(seed)
+    scale = 256 ** -0.5
+    checks = []
+    for batch, key_len, label in ((1, 2048, "batch 1, context 2048"), (32, 2048, "batch 32, context 2048"),
+                                  (1, 3, "context shorter than the split count"),
+                                  (1, 33, "context that is not a multiple of the tile")):
+        q = torch.randn((batch, 16, 256), generator=gen).to(BF16)
+        k = torch.randn((batch, 4, key_len, 256), generator=gen).to(BF16)
+        v = torch.randn((batch, 4, key_len, 256), generator=gen).to(BF16)
+        want = decode_attention(q, k, v, scale)
+        got = split_kv_decode_attention(q.to(device), k.to(device), v.to(device), scale, 8).cpu()
+        checks.append(check_kernel(f"hip_split_kv_decode_attention {label}", lambda: want, lambda: got,
+                                   replaces="gqa_attention", atol=2e-2, rtol=1e-2))
+    return tuple(checks)
 
 
 def static_decode_engine(model, *, batch: int = 1, max_seq_len: int, device="cuda", max_new_tokens: int = 0):

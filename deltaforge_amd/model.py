@@ -232,3 +232,5 @@ register_installer("hip_gated_delta_decode", _install_delta)
 register_installer("hip_gated_attention_decode", _install_attention)
 register_installer("hip_decode_engine", _install_decode_loop)
 register_installer("hip_persistent_decode", _install_persistent_loop)
+register_installer("hip_delta_rule_step", _install_delta)
+register_installer("hip_split_kv_decode_attention", _install_attention)

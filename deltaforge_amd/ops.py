@@ -32,6 +32,7 @@ __all__ = [
     "attention_decode",
     "attention_splits",
     "causal_conv_step",
+    "delta_rule_step",
     "embed_int4",
     "gated_delta_step",
     "int4_dequant",
@@ -41,6 +42,7 @@ __all__ = [
     "require_gpu",
     "rms_norm",
     "silu_mul",
+    "split_kv_decode_attention",
     "workspace",
 ]
 
@@ -54,6 +56,27 @@ def require_gpu(t: Tensor, op: str) -> None:
             f"deltaforge::{op} requires a GPU tensor and has no PyTorch fallback, on purpose: "
             "falling back would run the reference while the caller believes it ran the kernel."
         )
+
+
+def require_gpus(op: str, *tensors: Tensor | None) -> None:
+    """``require_gpu`` for every tensor a kernel dereferences, all on one device: a host
+    pointer (or another device's) handed to a kernel is a memory fault, not an error."""
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        require_gpu(t, op)
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise RuntimeError(f"deltaforge::{op}: tensors on {device} and {t.device}; one device per call")
+
+
+def _check_dtype(op: str, name: str, t: Tensor, dtype: torch.dtype, numel: int | None = None) -> None:
+    if t.dtype != dtype:
+        raise ValueError(f"{op}: {name} must be {dtype}, got {t.dtype}")
+    if numel is not None and t.numel() != numel:
+        raise ValueError(f"{op}: {name} must hold {numel} elements, got {t.numel()}")
 
 
 def _stream(t: Tensor) -> int:
@@ -248,15 +271,32 @@ def gated_delta_step(
     conv_w = conv_w.reshape(conv_w.shape[0], -1)
     if tuple(conv_w.shape) != (channels, 4):
         raise ValueError(f"conv weight must be [{channels}, 4] taps, got {tuple(conv_w.shape)}")
+    op = "gated_delta_step"
+    # the kernel reads every one of these as bf16 (A_log too: the reference model is cast to
+    # bf16 as a whole, model.py:98); an fp32 tensor would be misread, not rejected, on the GPU
+    for name, t in (("qkv", qkv), ("a", a), ("b", b), ("conv_w", conv_w)):
+        _check_dtype(op, name, t, BF16)
+    _check_dtype(op, "A_log", A_log, BF16, hv)
+    _check_dtype(op, "dt_bias", dt_bias, BF16, hv)
     if not state.is_contiguous():
         raise ValueError("state must be contiguous (it is updated in place)")
     mode = 1 if conv_ring is not None else 0
     if mode == 0:
-        if conv_in is None or conv_out is None or tuple(conv_in.shape) != (batch, channels, 3):
+        if conv_in is None or conv_out is None or tuple(conv_in.shape) != (batch, channels, 3) \
+                or tuple(conv_out.shape) != (batch, channels, 3):
             raise ValueError(f"conv history must be [B, {channels}, 3] in and out")
-    elif position is None or tuple(conv_ring.shape) != (batch, channels, 4):
-        raise ValueError(f"conv ring must be [B, {channels}, 4] with a device position")
-    require_gpu(state, "gated_delta_step")
+        if not conv_in.is_contiguous() or not conv_out.is_contiguous():
+            raise ValueError("conv history must be contiguous")
+        _check_dtype(op, "conv_in", conv_in, BF16)
+        _check_dtype(op, "conv_out", conv_out, BF16)
+    else:
+        if position is None or tuple(conv_ring.shape) != (batch, channels, 4) or not conv_ring.is_contiguous():
+            raise ValueError(f"conv ring must be a contiguous [B, {channels}, 4] with a device position")
+        _check_dtype(op, "conv_ring", conv_ring, BF16)
+        _check_dtype(op, "position", position, torch.int32, 1)
+    if out is not None and (out.dtype != BF16 or tuple(out.shape) != (batch, hv, dv) or not out.is_contiguous()):
+        raise ValueError(f"out must be a contiguous bf16 [{batch}, {hv}, {dv}]")
+    require_gpus(op, state, qkv, a, b, A_log, dt_bias, conv_w, conv_in, conv_out, conv_ring, position, out)
     if out is None:
         out = torch.empty((batch, hv, dv), dtype=BF16, device=state.device)
     args = N.GatedDeltaArgs(
@@ -270,9 +310,104 @@ def gated_delta_step(
     return out
 
 
+def delta_rule_step(state: Tensor, query: Tensor, key: Tensor, value: Tensor, g: Tensor, beta: Tensor,
+                    *, state_out: Tensor | None = None, out: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """One delta-rule step on normalised fp32 inputs; returns ``(out, new_state)``.
+
+    The contract of the reference's ``deltaforge::delta_rule_step``
+    (kernels/gated_delta_step.py:109-186) and its checks in the same order: ``state``
+    ``(B, H, Dk, Dv)`` fp32, ``query``/``key`` ``(B, H, Dk)`` (already l2-normed, the query
+    already scaled by ``Dk**-0.5``), ``value (B, H, Dv)``, ``g``/``beta`` ``(B, H)``. The
+    kernel is written for Dk = 128 and Dv a multiple of 32. ``state_out`` may be ``state``
+    itself (an in-place step).
+    """
+    if state.dim() != 4:
+        raise ValueError(f"expected state (batch, heads, key_dim, value_dim), got {tuple(state.shape)}")
+    batch, heads, key_dim, value_dim = state.shape
+    for name, t, shape in (("query", query, (batch, heads, key_dim)), ("key", key, (batch, heads, key_dim)),
+                           ("value", value, (batch, heads, value_dim)), ("g", g, (batch, heads)),
+                           ("beta", beta, (batch, heads))):
+        if tuple(t.shape) != shape:
+            raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {shape}")
+    if state.dtype != torch.float32:
+        raise ValueError(f"the recurrent state is fp32 by config (mamba_ssm_dtype), got {state.dtype}")
+    if key_dim != 128 or value_dim < 32 or value_dim % 32:
+        raise ValueError(f"the HIP step is written for key_dim 128 and value_dim % 32 == 0, got {key_dim}, {value_dim}")
+    for name, t in (("state_out", state_out), ("out", out)):
+        if t is not None and (t.dtype != torch.float32 or not t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous fp32 tensor")
+    if state_out is not None and state_out.shape != state.shape:
+        raise ValueError(f"state_out {tuple(state_out.shape)} must match state {tuple(state.shape)}")
+    if out is not None and tuple(out.shape) != (batch, heads, value_dim):
+        raise ValueError(f"out must be ({batch}, {heads}, {value_dim})")
+    require_gpus("delta_rule_step", state, query, key, value, g, beta, state_out, out)
+    state = state.contiguous()
+    query, key, value, g, beta = (t.contiguous().float() for t in (query, key, value, g, beta))
+    if state_out is None:
+        state_out = torch.empty_like(state)
+    if out is None:
+        out = torch.empty((batch, heads, value_dim), dtype=torch.float32, device=state.device)
+    args = N.DeltaRuleArgs(
+        state_in=state.data_ptr(), state_out=state_out.data_ptr(), query=query.data_ptr(), key=key.data_ptr(),
+        value=value.data_ptr(), g=g.data_ptr(), beta=beta.data_ptr(), out=out.data_ptr(),
+        batch=batch, heads=heads, key_dim=key_dim, value_dim=value_dim,
+    )
+    N.check(N.lib().df_delta_rule_step(C.byref(args), _stream(state)), "delta_rule_step")
+    return out, state_out
+
+
 # ---------------------------------------------------------------------------------------
 # Attention decode
 # ---------------------------------------------------------------------------------------
+
+
+def split_kv_decode_attention(query: Tensor, key: Tensor, value: Tensor, scale: float, splits: int,
+                              *, out: Tensor | None = None, ws: Tensor | None = None) -> Tensor:
+    """Single-token GQA attention over a whole cache with the scan split ``splits`` ways.
+
+    The contract of the reference's ``deltaforge::split_kv_decode_attention``
+    (kernels/flash_decode_splitkv.py:177-261), checks in its order: ``query (B, Hq, D)``,
+    ``key``/``value`` ``(B, Hkv, L, D)``, output ``(B, Hq, D)`` in the query's dtype. The HIP
+    kernel takes bf16 with D = 256 and 4 query heads per KV head.
+    """
+    if query.dim() != 3:
+        raise ValueError(f"expected query (batch, heads_q, head_dim), got {tuple(query.shape)}")
+    if key.shape != value.shape:
+        raise ValueError(f"key {tuple(key.shape)} and value {tuple(value.shape)} must match")
+    batch, heads_q, head_dim = query.shape
+    if key.dim() != 4:
+        raise ValueError(f"expected key (batch, heads_kv, key_len, head_dim), got {tuple(key.shape)}")
+    kv_batch, heads_kv, key_len, kv_dim = key.shape
+    if kv_batch != batch or kv_dim != head_dim:
+        raise ValueError(f"key {tuple(key.shape)} does not match query {tuple(query.shape)}")
+    if heads_kv == 0 or heads_q % heads_kv:
+        raise ValueError(f"{heads_q} query heads do not divide into {heads_kv} KV heads")
+    if key_len < 1:
+        raise ValueError("cannot attend over an empty KV cache")
+    if splits < 1 or splits & (splits - 1):
+        raise ValueError(f"splits must be a power of two so the merge can index it, got {splits}")
+    if splits > 256:
+        raise ValueError(f"the HIP merge takes at most 256 splits, got {splits}")
+    if query.dtype != BF16 or key.dtype != BF16 or value.dtype != BF16:
+        raise ValueError("the HIP split-KV kernel takes bf16 query, key and value")
+    if head_dim != 256 or heads_q != 4 * heads_kv:
+        raise ValueError(f"written for head_dim 256 and 4 query heads per KV head, got {head_dim}, {heads_q}/{heads_kv}")
+    if out is not None and (out.shape != query.shape or out.dtype != BF16 or not out.is_contiguous()):
+        raise ValueError(f"out must be a contiguous bf16 {tuple(query.shape)}")
+    nbytes = int(N.lib().df_attention_decode_workspace_bytes(batch, heads_q, heads_kv, head_dim, splits))
+    if ws is not None and ws.numel() < nbytes:
+        raise ValueError(f"workspace holds {ws.numel()} bytes, the launch needs {nbytes}")
+    require_gpus("split_kv_decode_attention", query, key, value, out, ws)
+    query, key, value = query.contiguous(), key.contiguous(), value.contiguous()
+    if ws is None:
+        ws = workspace(query.device, nbytes, "split_kv")
+    if out is None:
+        out = torch.empty_like(query)
+    N.check(N.lib().df_split_kv_decode_attention(query.data_ptr(), key.data_ptr(), value.data_ptr(), batch, heads_q,
+                                                 heads_kv, key_len, head_dim, float(scale), splits, out.data_ptr(),
+                                                 ws.data_ptr(), ws.numel(), _stream(query)),
+            "split_kv_decode_attention")
+    return out
 
 
 def attention_splits(batch: int, num_kv_heads: int, max_keys: int) -> int:
@@ -304,10 +439,25 @@ def attention_decode(
         raise ValueError("position must be a single int32 device scalar")
     if inv_freq.dtype != torch.float32:
         raise ValueError("inv_freq must be fp32 (the values the model stores)")
-    require_gpu(q, "attention_decode")
+    half = inv_freq.numel()
+    # each lane finds its rotary partner half/4 lanes away with an xor shuffle, which is the
+    # lane + half/4 only when half/4 is a power of two (8, 16, ..., 256 rotary dims)
+    if half < 4 or half * 2 > d or half & (half - 1):
+        raise ValueError(f"rotary_dim = 2 * inv_freq.numel() must be a power of two in [8, {d}], got {2 * half}")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache and v_cache must be contiguous (the new key is written in place)")
+    for name, t in (("q_norm_w", q_norm_w), ("k_norm_w", k_norm_w)):
+        if t.dtype != BF16 or t.numel() != d or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous bf16 [{d}], got {t.dtype} {tuple(t.shape)}")
+    if out is not None and (out.dtype != BF16 or tuple(out.shape) != (batch, num_q_heads * d) or out.stride(1) != 1
+                            or out.stride(0) != num_q_heads * d):
+        raise ValueError(f"out must be a contiguous bf16 [{batch}, {num_q_heads * d}]")
     if splits is None:
         splits = attention_splits(batch, hkv, max_len)
     nbytes = int(N.lib().df_attention_decode_workspace_bytes(batch, num_q_heads, hkv, d, splits))
+    if ws is not None and ws.numel() < nbytes:
+        raise ValueError(f"workspace holds {ws.numel()} bytes, the launch needs {nbytes}")
+    require_gpus("attention_decode", q, k, v, q_norm_w, k_norm_w, inv_freq, k_cache, v_cache, position, out, ws)
     if ws is None:
         ws = workspace(q.device, nbytes, "attention")
     if out is None:

@@ -29,7 +29,8 @@ XCD = 8
 LIN_COLS = 1552  # per XCD: q 256, k 256, v 512, z 512, a 4, b 4, 8 zero columns
 ATTN_COLS = 1536  # per XCD: 2 x (query 256 | gate 256), k 256, v 256
 ERRORS = {1: "a cross-workgroup hand-off timed out", 2: "a workgroup ran on an unexpected XCD",
-          3: "position, prompt or token log out of range", 4: "token id out of range"}
+          3: "position, prompt or token log out of range", 4: "token id out of range",
+          5: "control/compute barrier schedules disagree"}
 
 
 def linear_proj_columns(c: ModelConfig) -> torch.Tensor:
@@ -238,9 +239,16 @@ class PersistentDecoder:
     # -- the DecodeEngine surface ----------------------------------------------------------
 
     def reset(self) -> None:
+        """Empty caches at position 0 and a cleared hand-off workspace.
+
+        The workspace is cleared whole, not just its abort word: an aborted launch leaves
+        tagged hand-off words at epochs above the stored epoch, which a launch that kept them
+        would take for fresh data. So after an abort (``check`` raises) the decoder is usable
+        again from the next ``reset`` / ``prefill``."""
         for st in self.layer_state:
             for t in st.values():
                 t.zero_()
+        self.workspace.zero_()
         self.position.zero_()
         self.step_index.zero_()
         self.tokens.zero_()

@@ -51,11 +51,20 @@ class CanonicalInt4:
         return self.K // self.scale.shape[0]
 
 
-def draw_int4(gen: torch.Generator, k: int, n: int, scale_std: float = 0.02) -> CanonicalInt4:
-    """Uniform bytes (two uniform nibbles each), drawn as 32-bit words for speed."""
+def draw_int4(gen: torch.Generator, k: int, n: int, scale_std: float = 0.02, symmetric: bool = False) -> CanonicalInt4:
+    """Uniform bytes (two uniform nibbles each), drawn as 32-bit words for speed.
+
+    ``symmetric`` maps nibble 0 to 8, so ``n - 8`` lies in -7..7 with mean 0, the range of the
+    reference's symmetric quantiser (kernels/tiled_gemv.py:242-278). The default keeps
+    BASELINE's uniform 0..15, whose ``n - 8`` has mean -1/2."""
     nbytes = (k // 2) * n
     words = torch.randint(-(2**31), 2**31 - 1, ((nbytes + 3) // 4,), generator=gen, dtype=torch.int32)
     packed = words.view(torch.uint8)[:nbytes].reshape(k // 2, n)
+    if symmetric:
+        lo, hi = packed & 0x0F, packed >> 4
+        lo = torch.where(lo == 0, 8, lo)
+        hi = torch.where(hi == 0, 8, hi)
+        packed = (lo | (hi << 4)).to(torch.uint8)
     scale = (torch.randn((k // 128, n), generator=gen).abs() * scale_std).to(BF16)
     return CanonicalInt4(packed, scale)
 
@@ -193,12 +202,17 @@ def linear_shapes(c: ModelConfig) -> list[tuple[str, int, int]]:
     return out
 
 
-def synth_model(config: ModelConfig | None = None, seed: int = 0) -> SynthModel:
+def synth_model(config: ModelConfig | None = None, seed: int = 0, symmetric: bool = False) -> SynthModel:
+    """The seeded random-init model. BASELINE's nibbles (uniform 0..15, zero point 8) give every
+    int4 output a bias of -s/2 * sum(x); through 32 residual layers it grows into a constant
+    vector that fixes the argmax whatever the input. ``symmetric=True`` draws the reference
+    quantiser's -7..7 instead, whose logits follow the input (a model for greedy-token
+    checks); the benchmark uses the default."""
     c = config or qwen3_5_4b_config()
     gen = torch.Generator().manual_seed(seed)
     model = SynthModel(c)
     for name, k, n in linear_shapes(c):
-        model.linears[name] = draw_int4(gen, k, n)
+        model.linears[name] = draw_int4(gen, k, n, symmetric=symmetric)
     for i, kind in enumerate(c.layer_types):
         p = f"layers.{i}."
         model.params[p + "input_layernorm.weight"] = _normal(gen, (c.hidden_size,), 0.02)

@@ -109,6 +109,23 @@ typedef struct DfGatedDeltaArgs {
  * kernels/gated_delta_step.py:109-186). Requires Dk == Dv == 128, 4 taps. */
 int df_gated_delta_step(const DfGatedDeltaArgs* args, hipStream_t stream);
 
+typedef struct DfDeltaRuleArgs {
+  const float* state_in;     /* [B][H][Dk][Dv] fp32                                    */
+  float* state_out;          /* [B][H][Dk][Dv] fp32; may alias state_in                */
+  const float* query;        /* [B][H][Dk] fp32, already L2-normed and scaled by Dk^-1/2 */
+  const float* key;          /* [B][H][Dk] fp32, already L2-normed                     */
+  const float* value;        /* [B][H][Dv] fp32                                        */
+  const float* g;            /* [B][H] fp32 log-space decay (<= 0)                     */
+  const float* beta;         /* [B][H] fp32                                            */
+  float* out;                /* [B][H][Dv] fp32                                        */
+  int batch, heads, key_dim, value_dim;  /* Dk == 128, Dv % 32 == 0                    */
+} DfDeltaRuleArgs;
+
+/* One gated delta-rule step on normalised inputs, all contiguous:
+ * S *= exp(g); r = k^T S; delta = (v - r) beta; S += k delta^T; out = q^T S.
+ * Replaces deltaforge::delta_rule_step (kernels/gated_delta_step.py:109-186). */
+int df_delta_rule_step(const DfDeltaRuleArgs* args, hipStream_t stream);
+
 /* ---- GQA attention decode (split-KV) -------------------------------------------- */
 
 typedef struct DfAttnDecodeArgs {
@@ -139,6 +156,18 @@ int df_attention_decode_splits(int batch, int num_kv_heads, int max_keys);
  * kernels/gqa_decode.py:322-335). head_dim 256, 4 q heads per KV head. */
 int df_attention_decode(const DfAttnDecodeArgs* args, void* workspace, size_t workspace_bytes,
                         hipStream_t stream);
+
+/* Single-token GQA attention over a whole cache, without prologue or gate: query
+ * [B][Hq][D] bf16 (already normed and rotated), key/value [B][Hkv][L][D] bf16 contiguous,
+ * out[b][h] = sum_j softmax_j(scale q.k_j) v_j as bf16, split over `splits` (1..256) KV
+ * ranges merged by the log-sum-exp identity. D == 256 and Hq == 4 Hkv. The workspace is
+ * df_attention_decode_workspace_bytes(B, Hq, Hkv, D, splits), zero-filled before first use
+ * and left zeroed. Replaces deltaforge::split_kv_decode_attention
+ * (kernels/flash_decode_splitkv.py:177-261). */
+int df_split_kv_decode_attention(const uint16_t* query, const uint16_t* key, const uint16_t* value, int batch,
+                                 int num_q_heads, int num_kv_heads, int key_len, int head_dim, float scale,
+                                 int splits, uint16_t* out, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream);
 
 /* ---- elementwise ops of the slot surface ---------------------------------------- */
 

@@ -25,6 +25,7 @@ __all__ = [
     "OracleModel",
     "apply_partial_rope",
     "causal_conv",
+    "delta_rule_step",
     "gated_delta_rule",
     "gated_rms_norm",
     "l2norm",
@@ -128,12 +129,20 @@ def gated_delta_rule(query, key, value, g, beta, initial_state=None):
         state = initial_state.to(torch.float32)
     out = torch.zeros_like(v)
     for t in range(steps):
-        state = state * gg[:, :, t].exp()[..., None, None]
-        recalled = (state * k[:, :, t].unsqueeze(-1)).sum(dim=-2)
-        delta = (v[:, :, t] - recalled) * b[:, :, t].unsqueeze(-1)
-        state = state + k[:, :, t].unsqueeze(-1) * delta.unsqueeze(-2)
-        out[:, :, t] = (state * q[:, :, t].unsqueeze(-1)).sum(dim=-2)
+        out[:, :, t], state = delta_rule_step(state, q[:, :, t], k[:, :, t], v[:, :, t], gg[:, :, t], b[:, :, t])
     return out.transpose(1, 2).contiguous().to(in_dtype), state
+
+
+def delta_rule_step(state, q, k, v, g, beta):
+    """One token of the rule on normalised fp32 inputs (the loop body of reference.py:450-458;
+    the contract of deltaforge::delta_rule_step, kernels/gated_delta_step.py:109-186):
+    ``state (B, H, Dk, Dv)``, ``q``/``k`` ``(B, H, Dk)``, ``v (B, H, Dv)``, ``g``/``beta``
+    ``(B, H)``. Returns ``(out (B, H, Dv), new_state)``."""
+    state = state * g.exp()[..., None, None]
+    recalled = (state * k.unsqueeze(-1)).sum(dim=-2)
+    delta = (v - recalled) * beta.unsqueeze(-1)
+    state = state + k.unsqueeze(-1) * delta.unsqueeze(-2)
+    return (state * q.unsqueeze(-1)).sum(dim=-2), state
 
 
 def causal_conv(x: torch.Tensor, history: torch.Tensor | None, weight: torch.Tensor):

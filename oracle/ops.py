@@ -11,6 +11,8 @@ the reference's rounding points (pinned through ``oracle.model`` by the golden v
 * ``attention_decode`` reference.py:621-676 at seq_len 1 between the projections and
                  o_proj (q/gate split, q/k norm, partial RoPE, cache write, GQA
                  expansion, bf16 scores, fp32 softmax, bf16 PV, output gate).
+* ``decode_attention`` the attention core of the same lines (gqa_decode.py:322-335), the
+                 contract of deltaforge::split_kv_decode_attention.
 """
 
 from __future__ import annotations
@@ -23,7 +25,7 @@ from deltaforge_amd.config import ModelConfig
 from .int4 import dequant_gemv
 from .model import apply_partial_rope, causal_conv, gated_delta_rule, output_gate, rms_norm, rope_cos_sin
 
-__all__ = ["attention_decode", "delta_step", "head", "mlp_block"]
+__all__ = ["attention_decode", "decode_attention", "delta_step", "head", "mlp_block"]
 
 
 def head(x, residual, norm_w, packed, scale, group=128, eps=1e-6):
@@ -79,13 +81,22 @@ def attention_decode(q_proj, k_raw, v_raw, q_norm_w, k_norm_w, k_cache, v_cache,
     end = position + 1
     k_cache[:, :, position:end] = key
     v_cache[:, :, position:end] = value
-    outs = []
-    groups = c.num_key_value_groups
-    for bi in range(batch):  # one sequence at a time keeps the GQA expansion small
-        kk = k_cache[bi:bi + 1, :, :end].repeat_interleave(groups, dim=1)
-        vv = v_cache[bi:bi + 1, :, :end].repeat_interleave(groups, dim=1)
-        scores = torch.matmul(query[bi:bi + 1], kk.transpose(2, 3)) * (d ** -0.5)
-        weights = F.softmax(scores, dim=-1, dtype=torch.float32).to(query.dtype)
-        outs.append(torch.matmul(weights, vv))
-    attn = torch.cat(outs, dim=0).transpose(1, 2).reshape(batch, 1, -1)
+    attn = decode_attention(query[:, :, 0], k_cache[:, :, :end], v_cache[:, :, :end], d ** -0.5)
+    attn = attn.unsqueeze(1).reshape(batch, 1, -1)
     return (attn * output_gate(gate, c.output_gate_type)).reshape(batch, -1)
+
+
+def decode_attention(query, key, value, scale):
+    """Single-token GQA attention as the reference's layer computes it, expansion and all
+    (reference.py:652-672; restated as gqa_decode.py:322-335 for the split-KV op's check):
+    ``query (B, Hq, D)``, ``key``/``value`` ``(B, Hkv, L, D)``: bf16 scores, fp32 softmax
+    rounded to the query dtype, bf16 PV. Returns ``(B, Hq, D)``."""
+    groups = query.shape[1] // key.shape[1]
+    outs = []
+    for bi in range(query.shape[0]):  # one sequence at a time keeps the GQA expansion small
+        kk = key[bi:bi + 1].repeat_interleave(groups, dim=1)
+        vv = value[bi:bi + 1].repeat_interleave(groups, dim=1)
+        scores = torch.matmul(query[bi:bi + 1].unsqueeze(2), kk.transpose(2, 3)) * scale
+        weights = F.softmax(scores, dim=-1, dtype=torch.float32).to(query.dtype)
+        outs.append(torch.matmul(weights, vv).squeeze(2))
+    return torch.cat(outs, dim=0)

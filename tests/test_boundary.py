@@ -259,3 +259,108 @@ def test_fake_kernels_give_the_output_shapes():
                                      torch.empty(4, dtype=BF16, device=m), torch.empty((2048, 1, 4), dtype=BF16, device=m),
                                      torch.empty((2, 2048, 3), dtype=BF16, device=m), st, 4)
     assert out.shape == (2, 4, 128)
+
+
+# -- argument checks that guard the kernels' pointers ----------------------------------------
+
+
+def _delta_args(hv=32, hk=16, dk=128):
+    from deltaforge_amd import ops
+
+    ch = 2 * hk * dk + hv * dk
+    return ops, dict(qkv=torch.zeros((1, ch), dtype=BF16), a=torch.zeros((1, hv), dtype=BF16),
+                     b=torch.zeros((1, hv), dtype=BF16), A_log=torch.zeros(hv, dtype=BF16),
+                     dt_bias=torch.zeros(hv, dtype=BF16), conv_w=torch.zeros((ch, 1, 4), dtype=BF16),
+                     state=torch.zeros((1, hv, dk, dk), dtype=torch.float32), num_k_heads=hk,
+                     conv_ring=torch.zeros((1, ch, 4), dtype=BF16), position=torch.zeros(1, dtype=torch.int32))
+
+
+def test_gated_delta_step_rejects_misread_dtypes_before_the_device():
+    ops, args = _delta_args()
+    for name in ("A_log", "dt_bias", "a", "b", "qkv"):
+        bad = {**args, name: args[name].float()}
+        with pytest.raises(ValueError, match=name):
+            ops.gated_delta_step(**bad)
+    with pytest.raises(ValueError):
+        ops.gated_delta_step(**{**args, "A_log": torch.zeros(31, dtype=BF16)})
+    with pytest.raises(ValueError):
+        ops.gated_delta_step(**{**args, "position": torch.zeros(1, dtype=torch.int64)})
+    with pytest.raises(RuntimeError, match="no PyTorch fallback"):
+        ops.gated_delta_step(**args)
+
+
+def test_attention_decode_checks_rotary_width_and_caches():
+    from deltaforge_amd import ops
+
+    d, hkv = 256, 4
+    base = dict(q=torch.zeros((1, 16 * 2 * d), dtype=BF16), k=torch.zeros((1, hkv * d), dtype=BF16),
+                v=torch.zeros((1, hkv * d), dtype=BF16), q_norm_w=torch.zeros(d, dtype=BF16),
+                k_norm_w=torch.zeros(d, dtype=BF16), inv_freq=torch.zeros(32, dtype=torch.float32),
+                k_cache=torch.zeros((1, hkv, 16, d), dtype=BF16), v_cache=torch.zeros((1, hkv, 16, d), dtype=BF16),
+                position=torch.zeros(1, dtype=torch.int32), num_q_heads=16)
+    # rotary 48 and 96: rotary/8 not a power of two, the xor partner shuffle would pair wrong dims
+    for half in (24, 48, 3):
+        with pytest.raises(ValueError, match="rotary_dim"):
+            ops.attention_decode(**{**base, "inv_freq": torch.zeros(half, dtype=torch.float32)})
+    with pytest.raises(ValueError, match="contiguous"):
+        kc = torch.zeros((1, hkv, d, 16), dtype=BF16).transpose(2, 3)
+        ops.attention_decode(**{**base, "k_cache": kc})
+    with pytest.raises(ValueError):
+        ops.attention_decode(**{**base, "q_norm_w": torch.zeros(d, dtype=torch.float32)})
+    # every tensor the kernel dereferences must be on the GPU: a CPU position alone is refused
+    with pytest.raises(RuntimeError, match="no PyTorch fallback"):
+        ops.attention_decode(**base)
+
+
+def test_reference_signature_ops_validate_in_reference_order():
+    ops_mod = hip_ops
+    state = torch.zeros((1, 4, 128, 128))
+    q = torch.zeros((1, 4, 128))
+    with pytest.raises(ValueError, match="query"):
+        ops_mod.delta_rule_step(state, torch.zeros((1, 4, 64)), q, q, torch.zeros((1, 4)), torch.zeros((1, 4)))
+    with pytest.raises(ValueError, match="fp32"):
+        ops_mod.delta_rule_step(state.to(BF16), q, q, q, torch.zeros((1, 4)), torch.zeros((1, 4)))
+    with pytest.raises(RuntimeError, match="no PyTorch fallback"):
+        ops_mod.delta_rule_step(state, q, q, q, torch.zeros((1, 4)), torch.zeros((1, 4)))
+    qa = torch.zeros((1, 16, 256), dtype=BF16)
+    kv = torch.zeros((1, 4, 8, 256), dtype=BF16)
+    with pytest.raises(ValueError, match="power of two"):
+        ops_mod.split_kv_decode_attention(qa, kv, kv, 0.0625, 3)
+    with pytest.raises(ValueError, match="empty"):
+        ops_mod.split_kv_decode_attention(qa, kv[:, :, :0], kv[:, :, :0], 0.0625, 8)
+    with pytest.raises(ValueError, match="divide"):
+        ops_mod.split_kv_decode_attention(torch.zeros((1, 6, 256), dtype=BF16), kv, kv, 0.0625, 8)
+    with pytest.raises(RuntimeError, match="no PyTorch fallback"):
+        ops_mod.split_kv_decode_attention(qa, kv, kv, 0.0625, 8)
+    meta = "meta"
+    o, s = ops_mod.delta_rule_step(*(torch.empty(t.shape, device=meta) for t in (state, q, q, q)),
+                                   torch.empty((1, 4), device=meta), torch.empty((1, 4), device=meta))
+    assert o.shape == (1, 4, 128) and s.shape == state.shape
+    assert ops_mod.split_kv_decode_attention(qa.to(meta), kv.to(meta), kv.to(meta), 0.0625, 8).shape == qa.shape
+
+
+def test_standalone_ops_are_registered_candidates_with_checks():
+    from deltaforge_amd.kernels import CHECK_BUILDERS
+
+    for name, op in (("hip_delta_rule_step", "gated_delta_rule"), ("hip_split_kv_decode_attention", "gqa_attention")):
+        e = REGISTRY.get(name)
+        assert e.replaces == op and e.status is KernelStatus.CANDIDATE
+        assert name in INSTALLERS and name in CHECK_BUILDERS
+
+
+def test_registry_index_detects_an_entry_changed_behind_its_back():
+    import dataclasses
+
+    reg = KernelRegistry()
+    reg.register("a", impl=lambda: None, replaces="rms_norm", status=KernelStatus.CHAMPION)
+    reg.register("b", impl=lambda: None, replaces="rms_norm")
+    reg.check_invariants()
+    reg._entries["b"] = dataclasses.replace(reg._entries["b"], status=KernelStatus.CHAMPION)
+    with pytest.raises(RegistryError):
+        reg.check_invariants()
+    reg.unregister("a")
+    reg._entries["b"] = dataclasses.replace(reg._entries["b"], status=KernelStatus.CANDIDATE)
+    reg.check_invariants()
+    assert reg.champion("rms_norm") is None
+    reg.promote("b")
+    assert reg.champion("rms_norm").name == "b"

@@ -123,6 +123,27 @@ def test_config4_mlp_block(rows):
     assert err <= ATOL + RTOL * float(want.abs().max()), f"mlp block rows={rows}: max abs err {err:.4g}"
 
 
+@pytest.mark.parametrize("rows", [1, 8])
+def test_gated_rmsnorm_out_proj_residual(rows):
+    """GatedDeltaNet's tail as one GEMV launch: the per-head GatedRMSNorm prologue
+    (``DF_PRO_GATED_RMSNORM``: norm over each 128-wide head, plain weight, SiLU(z) gate;
+    reference.py:115-121, 546-550), the int4 out_proj 4096 -> 2560 and the residual epilogue
+    (reference.py:730). Against the oracle's gated_rms_norm -> dequant_gemv -> bf16 add."""
+    from oracle.model import gated_rms_norm
+
+    gen = torch.Generator().manual_seed(40 + rows)
+    w = synth.draw_int4(gen, 4096, 2560)
+    core = torch.randn((rows, 4096), generator=gen).to(torch.bfloat16)
+    z = torch.randn((rows, 4096), generator=gen).to(torch.bfloat16)
+    gw = (1.0 + 0.02 * torch.randn(128, generator=gen)).to(torch.bfloat16)
+    res = torch.randn((rows, 2560), generator=gen).to(torch.bfloat16)
+    got = ops.int4_gemv(core.to(DEV), repack(w), prologue=N.PRO_GATED_RMSNORM, epilogue=N.EPI_RESIDUAL,
+                        x2=z.to(DEV), norm_w=gw.to(DEV), res=res.to(DEV), eps=1e-6)
+    normed = gated_rms_norm(core.reshape(-1, 128), z.reshape(-1, 128), gw, 1e-6).reshape(rows, 4096)
+    y = dequant_gemv(normed, w.packed, w.scale, 128)
+    close(got, res + y, what=f"gated norm + out_proj + residual rows={rows}")
+
+
 # -- gated delta --------------------------------------------------------------------------
 
 
@@ -182,8 +203,9 @@ def _attention_case(batch, context, slack=64):
     assert torch.equal(vc[:, :, context].cpu(), wv[:, :, context])
 
 
-@pytest.mark.parametrize("batch,context", [(1, 4096), (8, 4096), (1, 32768), (1, 131072)])
+@pytest.mark.parametrize("batch,context", [(1, 4096), (8, 4096), (1, 32768), (8, 32768), (1, 131072), (8, 131072)])
 def test_config3_split_kv_decode(batch, context):
+    print(f"attention case B={batch} L={context}", flush=True)
     _attention_case(batch, context)
 
 
