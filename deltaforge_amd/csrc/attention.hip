@@ -36,12 +36,19 @@ struct AttnWs {
   float* ml;   // [B][Hq][S][2]
 };
 
-DF_DEVICE AttnWs attn_ws(void* base, int batch, int hq, int hkv, int splits) {
+// Workspace layout: a fixed block of merge counters, then the partials. The counter block has
+// the same size and place for every call shape: the kernel leaves its counters at zero, and a
+// workspace reused by a call of another shape must find zeros there, not an earlier call's
+// partials (with a shape-sized counter block, a later call with more (batch, KV head) pairs
+// read a previous call's partials as counters, and its merge never ran).
+constexpr int kMaxCounters = 4096;  // batch * num_kv_heads per launch
+constexpr size_t kCounterBytes = kMaxCounters * sizeof(int);
+
+inline AttnWs attn_ws(void* base, int batch, int hq, int splits) {
   AttnWs w;
   char* p = reinterpret_cast<char*>(base);
-  const size_t counters = ((size_t)batch * hkv * sizeof(int) + 255) & ~(size_t)255;
   w.counters = reinterpret_cast<int*>(p);
-  w.acc = reinterpret_cast<float*>(p + counters);
+  w.acc = reinterpret_cast<float*>(p + kCounterBytes);
   w.ml = w.acc + (size_t)batch * hq * splits * kHd;
   return w;
 }
@@ -327,8 +334,8 @@ extern "C" {
 
 size_t df_attention_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                            int splits) {
-  const size_t counters = ((size_t)batch * num_kv_heads * sizeof(int) + 255) & ~(size_t)255;
-  return counters + (size_t)batch * num_q_heads * splits * (head_dim + 2) * sizeof(float);
+  (void)num_kv_heads;
+  return kCounterBytes + (size_t)batch * num_q_heads * splits * (head_dim + 2) * sizeof(float);
 }
 
 int df_attention_decode_splits(int batch, int num_kv_heads, int max_keys) {
@@ -355,14 +362,8 @@ int df_attention_decode(const DfAttnDecodeArgs* args, void* workspace, size_t wo
   if (!workspace ||
       workspace_bytes < df_attention_decode_workspace_bytes(a.batch, a.num_q_heads, a.num_kv_heads, kHd, a.splits))
     return DF_WORKSPACE_TOO_SMALL;
-  AttnWs ws;
-  {
-    char* p = reinterpret_cast<char*>(workspace);
-    const size_t counters = ((size_t)a.batch * a.num_kv_heads * sizeof(int) + 255) & ~(size_t)255;
-    ws.counters = reinterpret_cast<int*>(p);
-    ws.acc = reinterpret_cast<float*>(p + counters);
-    ws.ml = ws.acc + (size_t)a.batch * a.num_q_heads * a.splits * kHd;
-  }
+  if ((size_t)a.batch * a.num_kv_heads > (size_t)kMaxCounters) return DF_BAD_ARGUMENT;
+  const AttnWs ws = attn_ws(workspace, a.batch, a.num_q_heads, a.splits);
   hipLaunchKernelGGL(attn_decode_kernel<false>, dim3(a.splits, a.num_kv_heads, a.batch), dim3(256), 0, stream, a,
                      ws, PlainAttn{0, 0.0f});
   DF_RETURN_LAUNCH_STATUS();
@@ -389,14 +390,8 @@ int df_split_kv_decode_attention(const uint16_t* query, const uint16_t* key, con
   a.head_dim = kHd;
   a.max_len = key_len;
   a.splits = splits;
-  AttnWs ws;
-  {
-    char* p = reinterpret_cast<char*>(workspace);
-    const size_t counters = ((size_t)batch * num_kv_heads * sizeof(int) + 255) & ~(size_t)255;
-    ws.counters = reinterpret_cast<int*>(p);
-    ws.acc = reinterpret_cast<float*>(p + counters);
-    ws.ml = ws.acc + (size_t)batch * num_q_heads * splits * kHd;
-  }
+  if ((size_t)batch * num_kv_heads > (size_t)kMaxCounters) return DF_BAD_ARGUMENT;
+  const AttnWs ws = attn_ws(workspace, batch, num_q_heads, splits);
   hipLaunchKernelGGL(attn_decode_kernel<true>, dim3(splits, num_kv_heads, batch), dim3(256), 0, stream, a, ws,
                      PlainAttn{key_len, scale});
   DF_RETURN_LAUNCH_STATUS();

@@ -65,8 +65,16 @@ DF_DEVICE int load_through(const int* p) {
   return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 DF_DEVICE void publish_wait() { __builtin_amdgcn_s_waitcnt(0); }
+// The "last workgroup merges" count: an agent-scope acquire-release add. The release half
+// makes this workgroup's partials (written before the barrier that precedes the call)
+// visible device-wide before the count moves; the acquire half, taken by the workgroup
+// that sees the final count and passed on to its other threads by the barrier after the
+// call, keeps its loads of the other workgroups' partials from returning values older than
+// their counts. A relaxed add plus write-through stores is not enough: a partial's store
+// can be acknowledged before a load that bypasses the caches sees it, and the merge then
+// reads the previous call's value from the reused workspace.
 DF_DEVICE int arrive(int* counter) {
-  return __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Block-wide sum for blockDim.x == 64 * waves; `scratch` holds >= waves floats.

@@ -145,6 +145,10 @@ typedef struct DfAttnDecodeArgs {
   float eps;
 } DfAttnDecodeArgs;
 
+/* Workspace of df_attention_decode / df_split_kv_decode_attention: a fixed 16 KB block of
+ * merge counters (batch * num_kv_heads <= 4096), then the per-split partials. Zero-fill it
+ * once before first use; every call leaves the counters at zero, whatever its shape, so one
+ * workspace serves calls of any shape on one stream (calls that overlap must not share it). */
 size_t df_attention_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads,
                                            int head_dim, int splits);
 int df_attention_decode_splits(int batch, int num_kv_heads, int max_keys);

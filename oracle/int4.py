@@ -22,6 +22,7 @@ import torch
 __all__ = [
     "bf16_bits_from_f32",
     "dequant_gemv",
+    "dequant_gemv_variant",
     "dequantise_int4_k_major",
     "dequantise_int4_k_major_np",
     "f32_from_bf16_bits",
@@ -94,6 +95,27 @@ def dequant_gemv(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, gro
     rows = x.reshape(-1, k)
     weight = dequantise_int4_k_major(packed, scale, group_size).to(x.dtype)
     out = rows.float() @ weight.float()
+    return out.to(x.dtype).reshape(*x.shape[:-1], n)
+
+
+def dequant_gemv_variant(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_size: int, *,
+                         round_weights: bool = True, accumulate: torch.dtype = torch.float32) -> torch.Tensor:
+    """``dequant_gemv`` with one of its two arithmetic choices changed, for measuring how far a
+    model's outputs move under a change of that size (not a restatement of the reference):
+
+    * ``accumulate=torch.float64``: the same bf16 weights, summed in float64 -- any fp32
+      implementation differs from the reference by at most a summation-order change;
+    * ``round_weights=False``: ``(nibble - 8) * scale`` kept exact (no bf16 rounding of the
+      weight before the product), the arithmetic of a kernel that applies each group's scale
+      once to an integer dot product.
+    """
+    k = packed.shape[0] * 2
+    n = packed.shape[1]
+    rows = x.reshape(-1, k)
+    weight = dequantise_int4_k_major(packed, scale, group_size)
+    if round_weights:
+        weight = weight.to(x.dtype)
+    out = rows.to(accumulate) @ weight.to(accumulate)
     return out.to(x.dtype).reshape(*x.shape[:-1], n)
 
 

@@ -204,10 +204,12 @@ class OracleModel:
     head) run the int4 champion expression.
     """
 
-    def __init__(self, config: ModelConfig, params: dict, int4: dict | None = None) -> None:
+    def __init__(self, config: ModelConfig, params: dict, int4: dict | None = None, gemv=None) -> None:
         self.config = config
         self.params = params
         self.int4 = int4 or {}
+        # the int4 linear's expression: the reference's unless a sensitivity probe swaps it
+        self.gemv = gemv or dequant_gemv
 
     def new_cache(self, batch: int, max_seq_len: int) -> OracleCache:
         return OracleCache(self.config, batch, max_seq_len, dtype=self.params["embed_tokens.weight"].dtype)
@@ -215,14 +217,14 @@ class OracleModel:
     def linear(self, x: torch.Tensor, name: str) -> torch.Tensor:
         if name in self.int4:
             packed, scale, group = self.int4[name]
-            return dequant_gemv(x, packed, scale, group)
+            return self.gemv(x, packed, scale, group)
         return F.linear(x, self.params[name])
 
     def project_logits(self, h: torch.Tensor) -> torch.Tensor:
         """reference.py:764-777 (tied head); the int4 head when quantised."""
         if "lm_head" in self.int4:
             packed, scale, group = self.int4["lm_head"]
-            return dequant_gemv(h, packed, scale, group)
+            return self.gemv(h, packed, scale, group)
         return F.linear(h, self.params["embed_tokens.weight"].to(h.dtype))
 
     def _delta_net(self, i: int, h: torch.Tensor, cache: dict | None) -> torch.Tensor:

@@ -162,3 +162,20 @@ def test_standalone_op_check_builders_pass():
         for chk in CHECK_BUILDERS[name](None, device=DEV):
             print(chk.name, chk.passed, f"{chk.max_abs_err:.3g}", flush=True)
             assert chk.passed, chk
+
+
+def test_split_kv_workspace_reused_across_shapes():
+    """Regression: calls of different shapes share one workspace. Its merge counters must sit
+    where no shape puts partials: with a counter block sized by batch * KV heads, a
+    (batch 1, 256 splits) call wrote partials over the slots a later (batch 32) call used as
+    counters, whose merge then never ran and left the output unwritten. Alternating shapes,
+    each call against the oracle."""
+    gen = torch.Generator().manual_seed(11)
+    scale = 256 ** -0.5
+    for batch, key_len, splits in ((1, 4097, 256), (32, 2048, 8), (1, 4097, 256), (32, 2048, 8), (8, 300, 64)):
+        q = torch.randn((batch, 16, 256), generator=gen).to(BF16)
+        k = torch.randn((batch, 4, key_len, 256), generator=gen).to(BF16)
+        v = torch.randn((batch, 4, key_len, 256), generator=gen).to(BF16)
+        want = oracle_ops.decode_attention(q, k, v, scale)
+        got = hip_ops.split_kv_decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), scale, splits)
+        close(got, want, what=f"split_kv B={batch} L={key_len} S={splits}")

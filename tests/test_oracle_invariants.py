@@ -295,3 +295,27 @@ def test_ops_mlp_and_head_are_the_model_path():
     want = model.project_logits(rms_norm(r + x, fn, cfg.rms_norm_eps))
     got = oracle_ops.head(x, r, fn, lin["lm_head"].packed, lin["lm_head"].scale, 128, cfg.rms_norm_eps)
     assert torch.equal(got, want)
+
+
+def test_dequant_gemv_variants_are_the_stated_changes():
+    """The sensitivity probes of the full-size parity test change one arithmetic choice each:
+    the default variant is the reference expression bit for bit; float64 accumulation of the
+    same bf16 weights and the exact (unrounded) weights agree with a float64 dense product."""
+    import functools
+
+    from deltaforge_amd.synth import draw_int4
+    from oracle.int4 import dequant_gemv, dequant_gemv_variant, dequantise_int4_k_major
+
+    gen = torch.Generator().manual_seed(9)
+    w = draw_int4(gen, 512, 96, symmetric=True)
+    x = torch.randn((3, 512), generator=gen).to(torch.bfloat16)
+    assert torch.equal(dequant_gemv_variant(x, w.packed, w.scale, 128), dequant_gemv(x, w.packed, w.scale, 128))
+    exact = dequantise_int4_k_major(w.packed, w.scale, 128).double()
+    rounded = exact.to(torch.bfloat16).double()
+    f64 = functools.partial(dequant_gemv_variant, accumulate=torch.float64)
+    assert torch.equal(f64(x, w.packed, w.scale, 128), (x.double() @ rounded).to(torch.bfloat16))
+    ex = dequant_gemv_variant(x, w.packed, w.scale, 128, round_weights=False).double()
+    want = x.double() @ exact
+    assert float((ex - want).abs().max()) <= float(want.abs().max()) * 2 ** -8
+    # symmetric draws never hold nibble 0 (n - 8 = -8)
+    assert int((w.packed & 0x0F).min()) >= 1 and int((w.packed >> 4).min()) >= 1
