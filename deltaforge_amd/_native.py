@@ -97,6 +97,8 @@ SIGNATURES = {
     "df_attention_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "df_attention_decode_splits": (_i, [_i, _i, _i]),
     "df_attention_decode": (_i, [C.POINTER(AttnDecodeArgs), _vp, _sz, _vp]),
+    "df_attention_decode_static_capacity": (_sz, []),
+    "df_attention_decode_static": (_i, [C.POINTER(AttnDecodeArgs), _vp]),
     "df_rms_norm": (_i, [_vp, _vp, _f, _i, _i, _vp, _vp]),
     "df_add_rms_norm": (_i, [_vp, _vp, _vp, _f, _i, _i, _vp, _vp, _vp]),
     "df_silu_mul": (_i, [_vp, _vp, _sz, _vp, _vp]),

@@ -23,6 +23,8 @@
 #include "common.h"
 #include "deltaforge_hip.h"
 
+#include <mutex>
+
 namespace df {
 
 constexpr int kHd = 256;
@@ -326,6 +328,48 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
   if (S > 1 && tid == 0) ws.counters[b * p.num_kv_heads + kvh] = 0;
 }
 
+// ---- the allocation-free variant -------------------------------------------------------
+//
+// df_attention_decode_static runs the same kernel with its workspace in this file-scope
+// device array instead of a caller's buffer: the merge counters (first kCounterBytes) and
+// room for kStaticPartialRows (batch x query head x split) partials of 258 floats. Each GPU
+// the library runs on holds its own copy until the process ends. In host code the name
+// `scratch` is only a stand-in: its device address comes from hipGetSymbolAddress, once per
+// device, and only that address is handed to kernels.
+constexpr int kStaticPartialRows = 8192;
+constexpr size_t kStaticScratchBytes = kCounterBytes + (size_t)kStaticPartialRows * (kHd + 2) * sizeof(float);
+__device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+__global__ void clear_counters_kernel(int* counters) {
+  for (int i = threadIdx.x; i < kMaxCounters; i += blockDim.x) counters[i] = 0;
+}
+
+constexpr int kMaxDevices = 64;
+struct StaticScratch {
+  std::mutex lock;
+  void* ptr[kMaxDevices] = {};
+  bool cleared[kMaxDevices] = {};
+};
+inline StaticScratch& static_scratch() {
+  static StaticScratch s;
+  return s;
+}
+
+// The current device's scratch address, looked up on the first call on that device.
+inline void* scratch_for_current_device(int* device) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  StaticScratch& s = static_scratch();
+  std::lock_guard<std::mutex> guard(s.lock);
+  if (!s.ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    s.ptr[dev] = p;
+  }
+  *device = dev;
+  return s.ptr[dev];
+}
+
 }  // namespace df
 
 using namespace df;
@@ -395,6 +439,31 @@ int df_split_kv_decode_attention(const uint16_t* query, const uint16_t* key, con
   hipLaunchKernelGGL(attn_decode_kernel<true>, dim3(splits, num_kv_heads, batch), dim3(256), 0, stream, a, ws,
                      PlainAttn{key_len, scale});
   DF_RETURN_LAUNCH_STATUS();
+}
+
+size_t df_attention_decode_static_capacity(void) { return kStaticScratchBytes; }
+
+int df_attention_decode_static(const DfAttnDecodeArgs* args, hipStream_t stream) {
+  if (!args) return DF_BAD_ARGUMENT;
+  const DfAttnDecodeArgs& a = *args;
+  if ((size_t)a.batch * a.num_q_heads * a.splits > (size_t)kStaticPartialRows ||
+      (size_t)a.batch * a.num_kv_heads > (size_t)kMaxCounters)
+    return DF_WORKSPACE_TOO_SMALL;
+  int dev = -1;
+  void* base = scratch_for_current_device(&dev);
+  if (!base) return DF_LAUNCH_FAILED;
+  {
+    // the counters start at zero on the first call on a device (the kernel leaves them at
+    // zero after every call); cleared by a kernel, not a memset, so the call can be captured
+    StaticScratch& s = static_scratch();
+    std::lock_guard<std::mutex> guard(s.lock);
+    if (!s.cleared[dev]) {
+      hipLaunchKernelGGL(clear_counters_kernel, dim3(1), dim3(256), 0, stream, reinterpret_cast<int*>(base));
+      if (hipGetLastError() != hipSuccess) return DF_LAUNCH_FAILED;
+      s.cleared[dev] = true;
+    }
+  }
+  return df_attention_decode(args, base, kStaticScratchBytes, stream);
 }
 
 }  // extern "C"

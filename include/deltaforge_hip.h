@@ -173,6 +173,17 @@ int df_split_kv_decode_attention(const uint16_t* query, const uint16_t* key, con
                                  int splits, uint16_t* out, void* workspace, size_t workspace_bytes,
                                  hipStream_t stream);
 
+/* df_attention_decode without a workspace argument, for callers that cannot allocate (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc). It has no
+ * counterpart in the reference. Its scratch (merge counters and split partials) is a
+ * file-scope device array of df_attention_decode_static_capacity() bytes (about 8.5 MB),
+ * one per GPU, held until the process ends; calls with batch * num_q_heads * splits > 8192
+ * or batch * num_kv_heads > 4096 return DF_WORKSPACE_TOO_SMALL. No call allocates. Every
+ * call on a GPU shares that GPU's array, so calls that overlap on one GPU (two streams, or
+ * two threads) race: serialise them. */
+size_t df_attention_decode_static_capacity(void);
+int df_attention_decode_static(const DfAttnDecodeArgs* args, hipStream_t stream);
+
 /* ---- elementwise ops of the slot surface ---------------------------------------- */
 
 /* rms_norm (kernels/fused_rmsnorm_residual.py:201-226; reference.py:92-96). */
