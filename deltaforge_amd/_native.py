@@ -118,21 +118,30 @@ class NativeError(RuntimeError):
     """A library entry point returned a non-zero status."""
 
 
+def load(path: str | Path, names=None) -> C.CDLL:
+    """A library file with the declared signatures bound (all of them, or ``names``): the
+    in-tree build, or another build of the same sources for an A/B comparison."""
+    path = Path(path)
+    if not path.exists():
+        raise RuntimeError(
+            f"{path} is missing; build it with `python -m deltaforge_amd.build`. "
+            "deltaforge_amd has no fallback path."
+        )
+    handle = C.CDLL(str(path))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        if names is not None and name not in names:
+            continue
+        fn = getattr(handle, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    return handle
+
+
 def lib() -> C.CDLL:
-    """Load the HIP library once. Raises if it is missing: there is no CPU fallback."""
+    """Load the in-tree HIP library once. Raises if it is missing: there is no CPU fallback."""
     global _LIB
     if _LIB is None:
-        if not LIB_PATH.exists():
-            raise RuntimeError(
-                f"{LIB_PATH} is missing; build it with `python -m deltaforge_amd.build`. "
-                "deltaforge_amd has no fallback path."
-            )
-        handle = C.CDLL(str(LIB_PATH))
-        for name, (restype, argtypes) in SIGNATURES.items():
-            fn = getattr(handle, name)
-            fn.restype = restype
-            fn.argtypes = argtypes
-        _LIB = handle
+        _LIB = load(LIB_PATH)
     return _LIB
 
 

@@ -90,7 +90,7 @@ class PersistentDecoder:
     """Greedy bs=1 decode of a ``SynthModel`` (canonical int4 weights) in persistent launches."""
 
     def __init__(self, model: SynthModel, *, max_seq_len: int, device: str | torch.device = "cuda",
-                 max_new_tokens: int = 256) -> None:
+                 max_new_tokens: int = 256, lib=None) -> None:
         c = model.config
         check_geometry(c)
         if c.output_gate_type not in (SIGMOID_GATE, "swish"):
@@ -178,7 +178,10 @@ class PersistentDecoder:
         self.prompt_len = 0
         self._trace: torch.Tensor | None = None
         self._trace_step = 0
-        nbytes = int(N.lib().df_decode_persistent_workspace_bytes(c.hidden_size))
+        # the library whose decode kernel this decoder launches (another build of the same
+        # sources for an A/B comparison; the in-tree build by default)
+        self.lib = lib if lib is not None else N.lib()
+        nbytes = int(self.lib.df_decode_persistent_workspace_bytes(c.hidden_size))
         self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
 
     # -- launches -----------------------------------------------------------------------
@@ -221,7 +224,7 @@ class PersistentDecoder:
         """Enqueue ``steps`` decode steps on the current stream (no host synchronisation)."""
         m = self._model()
         stream = torch.cuda.current_stream(self.device).cuda_stream
-        N.check(N.lib().df_decode_persistent(C.byref(m), steps, int(teacher_forced), self.workspace.data_ptr(),
+        N.check(self.lib.df_decode_persistent(C.byref(m), steps, int(teacher_forced), self.workspace.data_ptr(),
                                              self.workspace.numel(), stream), "decode_persistent")
 
     def check(self) -> None:
