@@ -80,7 +80,7 @@ class PersistModel(C.Structure):
         ("layers", _vp), ("head_w", _vp), ("head_s", _vp), ("final_norm", _vp), ("inv_freq", _vp),
         ("position", _vp), ("tokens", _vp), ("prompt", _vp), ("prompt_len", _i),
         ("token_log", _vp), ("log_capacity", _i), ("step", _vp), ("logits", _vp),
-        ("trace", _vp), ("trace_step", _i), ("trace_capacity", _i),
+        ("trace", _vp), ("trace_step", _i), ("trace_capacity", _i), ("embed_table", _vp),
     ]
 
 
@@ -105,6 +105,7 @@ SIGNATURES = {
     "df_partial_rope": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp]),
     "df_causal_conv_step": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp]),
     "df_embed_int4": (_i, [_vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i, _vp, _vp]),
+    "df_embed_bf16": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i, _i, _vp, _vp]),
     "df_argmax_workspace_bytes": (_sz, [_i, _i]),
     "df_argmax": (_i, [_vp, _i, _i, _vp, _vp, _i, _vp, _i, _vp, _vp, _sz, _vp]),
     "df_decode_persistent_workspace_bytes": (_sz, [_i]),

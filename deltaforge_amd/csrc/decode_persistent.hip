@@ -1829,7 +1829,34 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       if (c.lane == 0 && c.xcd == 0 && c.r == 0) raise_abort(c, kErrToken);
       return fail(1);
     }
-    {
+    if (M.embed_table) {
+      // the checkpoint's bf16 row, 16 bytes per lane per chunk, and its sum of squares (the
+      // same order in every workgroup)
+      const auto rt = rsrc(M.embed_table + (size_t)token * hidden);
+      uint4 hv[kHidChunks];
+#pragma unroll
+      for (int k = 0; k < kHidChunks; ++k) {
+        const int ch = c.lane + 64 * k;
+        if (ch * 8 < hidden) hv[k] = ld16<kCpPlain>(rt, ch * 16);
+      }
+      float sq = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kHidChunks; ++k) {
+        const int ch = c.lane + 64 * k;
+        if (ch * 8 < hidden) {
+          *reinterpret_cast<uint4*>(&L.h[ch * 8]) = hv[k];
+          const uint32_t w[4] = {hv[k].x, hv[k].y, hv[k].z, hv[k].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xFFFF0000u);
+            sq += lo * lo;
+            sq += hi * hi;
+          }
+        }
+      }
+      sq = dsum(sq);
+      if (c.lane == 0) L.ss = sq;
+    } else {
       const int tt = static_cast<int>(token / 16), cc = static_cast<int>(token % 16);
       const uint32_t* wt = reinterpret_cast<const uint32_t*>(M.head_w);
       constexpr int K = (kMaxHidden / kGroup * 16 + 63) / 64;

@@ -117,6 +117,26 @@ __global__ void embed_int4_kernel(const int64_t* __restrict__ tokens, const int6
   }
 }
 
+// One 16-byte chunk of the row per thread.
+__global__ void embed_bf16_kernel(const int64_t* __restrict__ tokens, const int64_t* __restrict__ prompt,
+                                  int prompt_len, const int* __restrict__ position,
+                                  const uint4* __restrict__ table, int hidden, int vocab, uint4* __restrict__ out) {
+  const int b = blockIdx.y;
+  const int chunk = blockIdx.x * blockDim.x + threadIdx.x;
+  const int chunks = hidden / 8;
+  if (chunk >= chunks) return;
+  int64_t tok;
+  if (prompt) {
+    const int pos = *position;
+    if (pos < 0 || pos >= prompt_len) return;
+    tok = prompt[(size_t)b * prompt_len + pos];
+  } else {
+    tok = tokens[b];
+  }
+  if (tok < 0 || tok >= vocab) return;
+  out[(size_t)b * chunks + chunk] = table[(size_t)tok * chunks + chunk];
+}
+
 // argmax with torch's tie rule (first index of the maximum). Each workgroup reduces a
 // chunk of one row to (value, index); the last workgroup reduces the chunks in order.
 constexpr int kArgmaxChunk = 1024;
@@ -260,6 +280,18 @@ int df_embed_int4(const int64_t* tokens, const int64_t* prompt, int prompt_len, 
   const int work = hidden / 128 * 16;
   hipLaunchKernelGGL(embed_int4_kernel, dim3((work + 255) / 256, batch), dim3(256), 0, stream, tokens, prompt,
                      prompt_len, position, reinterpret_cast<const uint32_t*>(w_tiled), s_tiled, hidden, vocab, out);
+  DF_RETURN_LAUNCH_STATUS();
+}
+
+int df_embed_bf16(const int64_t* tokens, const int64_t* prompt, int prompt_len, const int* position, int batch,
+                  const uint16_t* table, int hidden, int vocab, uint16_t* out, hipStream_t stream) {
+  if ((!tokens && !prompt) || (prompt && (!position || prompt_len < 1)) || !table || !out || batch < 1 ||
+      hidden % 8 || vocab < 1)
+    return DF_BAD_ARGUMENT;
+  const int chunks = hidden / 8;
+  hipLaunchKernelGGL(embed_bf16_kernel, dim3((chunks + 255) / 256, batch), dim3(256), 0, stream, tokens, prompt,
+                     prompt_len, position, reinterpret_cast<const uint4*>(table), hidden, vocab,
+                     reinterpret_cast<uint4*>(out));
   DF_RETURN_LAUNCH_STATUS();
 }
 

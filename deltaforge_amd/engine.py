@@ -114,6 +114,12 @@ class DecodeEngine:
         self.head = gemv(lin["lm_head"].packed, lin["lm_head"].scale)
         self.final_norm = p["norm.weight"]
         self.inv_freq = inv_freq(c).to(dev)
+        # a checkpoint's own bf16 embedding table (``checkpoint.load_checkpoint``); without one the
+        # token rows come from the tied int4 head, which is the synthetic model's table
+        table = p.get("embed_tokens.weight")
+        if table is not None and tuple(table.shape) != (c.vocab_size, c.hidden_size):
+            raise ValueError(f"embed_tokens.weight must be [{c.vocab_size}, {c.hidden_size}], got {tuple(table.shape)}")
+        self.embed_table = table.to(torch.bfloat16).contiguous() if table is not None else None
         self.splits = ops.attention_splits(batch, c.num_key_value_heads, max_seq_len)
         attn_ws = int(N.lib().df_attention_decode_workspace_bytes(batch, c.num_attention_heads, c.num_key_value_heads,
                                                                   c.head_dim, self.splits))
@@ -145,8 +151,12 @@ class DecodeEngine:
     def enqueue_step(self, *, from_prompt: bool = False, log_token: bool = True) -> None:
         """Launch one decode step on the current stream (no host sync, no allocation)."""
         c = self.config
-        ops.embed_int4(self.tokens, self.head.weight, self.h,
-                       prompt=self.prompt if from_prompt else None, position=self.position if from_prompt else None)
+        if self.embed_table is not None:
+            ops.embed_bf16(self.tokens, self.embed_table, self.h, prompt=self.prompt if from_prompt else None,
+                           position=self.position if from_prompt else None)
+        else:
+            ops.embed_int4(self.tokens, self.head.weight, self.h, prompt=self.prompt if from_prompt else None,
+                           position=self.position if from_prompt else None)
         conv_c, vd, hv = c.linear_conv_dim, c.linear_value_dim, c.linear_num_value_heads
         qd, kd = 2 * c.num_attention_heads * c.head_dim, c.num_key_value_heads * c.head_dim
         for layer in self.layers:

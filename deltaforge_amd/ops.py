@@ -33,6 +33,7 @@ __all__ = [
     "attention_splits",
     "causal_conv_step",
     "delta_rule_step",
+    "embed_bf16",
     "embed_int4",
     "gated_delta_step",
     "int4_dequant",
@@ -571,6 +572,31 @@ def embed_int4(tokens: Tensor, head: Int4Weight, out: Tensor | None = None, *,
     N.check(N.lib().df_embed_int4(tokens.data_ptr(), N.ptr(prompt), plen, N.ptr(position), tokens.numel(),
                                   head.w.data_ptr(), head.s.data_ptr(), head.K, head.N, out.data_ptr(),
                                   _stream(tokens)), "embed_int4")
+    return out
+
+
+def embed_bf16(tokens: Tensor, table: Tensor, out: Tensor | None = None, *,
+               prompt: Tensor | None = None, position: Tensor | None = None) -> Tensor:
+    """Embedding rows of a bf16 ``[vocab, hidden]`` table (reference.py:804), selected as in
+    ``embed_int4``: for checkpoints whose table is not the dequantised int4 head."""
+    if tokens.dtype != torch.int64 or tokens.dim() != 1:
+        raise ValueError("tokens must be int64 [B]")
+    if table.dim() != 2 or table.dtype != BF16 or not table.is_contiguous() or table.shape[1] % 8:
+        raise ValueError(f"table must be a contiguous bf16 [vocab, hidden % 8 == 0], got {table.dtype} "
+                         f"{tuple(table.shape)}")
+    if prompt is not None and (prompt.dtype != torch.int64 or prompt.dim() != 2 or position is None
+                               or not prompt.is_contiguous() or prompt.shape[0] != tokens.numel()):
+        raise ValueError("prompt must be contiguous int64 [B, P] with a device position")
+    vocab, hidden = table.shape
+    if out is not None and (out.dtype != BF16 or tuple(out.shape) != (tokens.numel(), hidden)
+                            or not out.is_contiguous()):
+        raise ValueError(f"out must be a contiguous bf16 [{tokens.numel()}, {hidden}]")
+    require_gpus("embed_bf16", tokens, table, prompt, position, out)
+    if out is None:
+        out = torch.empty((tokens.numel(), hidden), dtype=BF16, device=tokens.device)
+    plen = prompt.shape[1] if prompt is not None else 0
+    N.check(N.lib().df_embed_bf16(tokens.data_ptr(), N.ptr(prompt), plen, N.ptr(position), tokens.numel(),
+                                  table.data_ptr(), hidden, vocab, out.data_ptr(), _stream(tokens)), "embed_bf16")
     return out
 
 

@@ -166,6 +166,12 @@ class PersistentDecoder:
         self.head = repack(lin["lm_head"].packed, lin["lm_head"].scale)
         self.final_norm = p["norm.weight"]
         self.inv_freq = inv_freq(c).to(dev)
+        # a checkpoint's own bf16 embedding table (``checkpoint.load_checkpoint``); without one the
+        # token rows come from the tied int4 head, which is the synthetic model's table
+        table = p.get("embed_tokens.weight")
+        if table is not None and tuple(table.shape) != (c.vocab_size, c.hidden_size):
+            raise ValueError(f"embed_tokens.weight must be [{c.vocab_size}, {c.hidden_size}], got {tuple(table.shape)}")
+        self.embed_table = table.to(torch.bfloat16).contiguous() if table is not None else None
         raw = b"".join(bytes(s) for s in structs)
         self.layers_dev = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(dev)
 
@@ -202,6 +208,7 @@ class PersistentDecoder:
         m.token_log, m.log_capacity = self.token_log.data_ptr(), self.max_new_tokens
         m.step = self.step_index.data_ptr()
         m.logits = self.logits.data_ptr()
+        m.embed_table = self.embed_table.data_ptr() if self.embed_table is not None else None
         if self._trace is not None:
             m.trace, m.trace_step, m.trace_capacity = self._trace.data_ptr(), self._trace_step, self._trace.numel()
         return m

@@ -217,6 +217,13 @@ int df_embed_int4(const int64_t* tokens, const int64_t* prompt, int prompt_len,
                   const uint16_t* s_tiled, int hidden, int vocab, uint16_t* out,
                   hipStream_t stream);
 
+/* Embedding rows from a bf16 table (reference.py:804, `F.embedding`): out[b] =
+ * table[t], t chosen as in df_embed_int4. For checkpoints whose embedding table is not the
+ * dequantised int4 head. */
+int df_embed_bf16(const int64_t* tokens, const int64_t* prompt, int prompt_len,
+                  const int* position, int batch, const uint16_t* table, int hidden,
+                  int vocab, uint16_t* out, hipStream_t stream);
+
 size_t df_argmax_workspace_bytes(int rows, int n);
 /* Greedy next token: first index of the max of each bf16 logits row (torch's tie rule;
  * model.py:145-147 `logits[:, -1].argmax`). After all rows are reduced, the last
@@ -292,6 +299,8 @@ typedef struct DfPersistModel {
   uint64_t* trace;                 /* optional: s_memrealtime (100 MHz) stamps of one    */
   int trace_step;                  /* step's phases (start, staged, end), as seen by     */
   int trace_capacity;              /* workgroup (XCD 0, rank 0); NULL disables           */
+  const uint16_t* embed_table;     /* [vocab][hidden] bf16 embedding rows, or NULL to    */
+                                   /* embed from the int4 head (the tied table)          */
 } DfPersistModel;
 
 /* Workspace for df_decode_persistent, zero-filled once before first use and kept (it

@@ -24,10 +24,12 @@ pytestmark = pytest.mark.gpu
 
 
 def oracle_for(model: synth.SynthModel) -> OracleModel:
-    """The same int4 model as the oracle sees it: every linear int4, embedding = dequantised head."""
+    """The same int4 model as the oracle sees it: every linear int4; the embedding is the model's
+    own bf16 table when it has one (a loaded checkpoint), else the dequantised head."""
     params = dict(model.params)
     head = model.linears["lm_head"]
-    params["embed_tokens.weight"] = dequantise_int4_k_major(head.packed, head.scale, 128).to(torch.bfloat16).t().contiguous()
+    if "embed_tokens.weight" not in params:
+        params["embed_tokens.weight"] = dequantise_int4_k_major(head.packed, head.scale, 128).to(torch.bfloat16).t().contiguous()
     table = {name: (w.packed, w.scale, 128) for name, w in model.linears.items()}
     return OracleModel(model.config, params, table)
 
