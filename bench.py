@@ -47,6 +47,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--calibration-copy", action="store_true",
                     help="after the timed decode, run three plain 256 MiB device copies (for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE passes)")
+    ap.add_argument("--prefill", choices=("parallel", "steps"), default="parallel",
+                    help="parallel: the prompt through each layer at once (deltaforge_amd.prefill, persistent "
+                         "engine only); steps: teacher-forced decode steps")
     ap.add_argument("--engine", choices=("persistent", "graph"), default="persistent",
                     help="persistent: one cooperative launch per decode run (df_decode_persistent); "
                          "graph: the per-op kernels replayed as one HIP graph per step")
@@ -158,16 +161,43 @@ def cpu_baseline(model, position: int) -> dict:
             "seconds_per_token": best}
 
 
-def run_decode(engine, args, persistent: bool) -> tuple[float, list[int]]:
-    """Prefill (untimed), warm up on a snapshot, restore, then time exactly ``args.steps``
-    greedy tokens with HIP events on the stream the decode runs on. Returns (seconds, first tokens)."""
-    prompt = synth_prompt(engine.config, args.prompt_len)
-    t0 = time.perf_counter()
-    engine.prefill(prompt.cuda())
+def run_prefill(engine, model, args, persistent: bool) -> dict:
+    """Fill the engine's caches with the benchmark prompt; time it with HIP events.
+
+    Parallel mode runs ``Prefiller.fill`` twice: the first call loads the kernels, the second is
+    timed. Steps mode times the engine's own teacher-forced decode steps. The decode timing
+    below does not include this."""
+    prompt = synth_prompt(engine.config, args.prompt_len).cuda()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if args.prefill == "parallel" and persistent:
+        from deltaforge_amd.prefill import Prefiller
+
+        pre = Prefiller(model)
+        pre.fill(engine, prompt)
+        torch.cuda.synchronize()
+        start.record(stream)
+        pre.fill(engine, prompt)
+        end.record(stream)
+        mode = "parallel (deltaforge_amd.prefill: int4 GEMM, chunked delta rule, causal attention)"
+        del pre
+    else:
+        start.record(stream)
+        engine.prefill(prompt)
+        end.record(stream)
+        mode = "teacher-forced decode steps"
+    torch.cuda.synchronize()
     if persistent:
         engine.check()
-    torch.cuda.synchronize()
-    log(f"prefill of {args.prompt_len} tokens (teacher-forced decode steps) in {time.perf_counter() - t0:.1f}s")
+    ms = start.elapsed_time(end)
+    log(f"prefill of {args.prompt_len} tokens ({mode}) in {ms:.1f} ms")
+    return {"tokens": args.prompt_len, "ms": round(ms, 2), "tok_per_s": round(args.prompt_len / ms * 1e3, 1),
+            "mode": mode}
+
+
+def run_decode(engine, args, persistent: bool) -> tuple[float, list[int]]:
+    """Warm up on a snapshot of the prefilled caches, restore, then time exactly ``args.steps``
+    greedy tokens with HIP events on the stream the decode runs on. Returns (seconds, first tokens)."""
     snap = engine.snapshot()
     engine.decode(args.warmup)
     if persistent:
@@ -230,6 +260,7 @@ def main() -> int:
         copy_calibration()
         return 0
 
+    prefill = run_prefill(engine, model, args, persistent)
     seconds, tokens = run_decode(engine, args, persistent)
     if args.calibration_copy:
         copy_calibration()
@@ -306,6 +337,7 @@ def main() -> int:
         },
         "roofline": roofline,
         "cpu_baseline": baseline,
+        "prefill": prefill,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -84,6 +84,31 @@ class PersistModel(C.Structure):
     ]
 
 
+class Int4GemmArgs(C.Structure):
+    _fields_ = [("x", _vp), ("w", _vp), ("s", _vp), ("out", _vp),
+                ("M", _i), ("K", _i), ("N", _i), ("ldx", _i), ("ldo", _i), ("epilogue", _i)]
+
+
+class DeltaPrefillArgs(C.Structure):
+    _fields_ = [("mixed", _vp), ("a", _vp), ("b", _vp), ("A_log", _vp), ("dt_bias", _vp), ("state", _vp),
+                ("out", _vp), ("ld_mixed", _i), ("ld_ab", _i), ("ld_out", _i),
+                ("tokens", _i), ("num_k_heads", _i), ("num_v_heads", _i)]
+
+
+class QkPrefillArgs(C.Structure):
+    _fields_ = [("proj", _vp), ("q_norm", _vp), ("k_norm", _vp), ("inv_freq", _vp), ("q_out", _vp),
+                ("k_cache", _vp), ("v_cache", _vp), ("ld_proj", _i), ("k_col", _i), ("v_col", _i),
+                ("tokens", _i), ("pos0", _i), ("max_len", _i), ("num_q_heads", _i), ("num_kv_heads", _i),
+                ("rotary_dim", _i), ("eps", _f)]
+
+
+class AttnPrefillArgs(C.Structure):
+    _fields_ = [("q", _vp), ("k_cache", _vp), ("v_cache", _vp), ("gate", _vp), ("out", _vp),
+                ("ld_gate", _i), ("gate_head_stride", _i), ("ld_out", _i),
+                ("tokens", _i), ("pos0", _i), ("max_len", _i), ("num_q_heads", _i), ("num_kv_heads", _i),
+                ("gate_kind", _i), ("scale", _f)]
+
+
 # name -> (restype, argtypes); the exported surface of include/deltaforge_hip.h
 SIGNATURES = {
     "df_int4_gemv_plan": (_i, [_i, _i, _i, _i, _i, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i), C.POINTER(_sz)]),
@@ -106,6 +131,12 @@ SIGNATURES = {
     "df_causal_conv_step": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp]),
     "df_embed_int4": (_i, [_vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i, _vp, _vp]),
     "df_embed_bf16": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i, _i, _vp, _vp]),
+    "df_int4_gemm": (_i, [C.POINTER(Int4GemmArgs), _vp]),
+    "df_causal_conv_prefill": (_i, [_vp, _i, _i, _i, _vp, _vp, _i, _vp, _i, _vp]),
+    "df_delta_rule_prefill": (_i, [C.POINTER(DeltaPrefillArgs), _vp]),
+    "df_gated_rms_norm_rows": (_i, [_vp, _i, _vp, _i, _vp, _f, _i, _i, _vp, _i, _vp]),
+    "df_qk_norm_rope_prefill": (_i, [C.POINTER(QkPrefillArgs), _vp]),
+    "df_attention_prefill": (_i, [C.POINTER(AttnPrefillArgs), _vp]),
     "df_argmax_workspace_bytes": (_sz, [_i, _i]),
     "df_argmax": (_i, [_vp, _i, _i, _vp, _vp, _i, _vp, _i, _vp, _vp, _sz, _vp]),
     "df_decode_persistent_workspace_bytes": (_sz, [_i]),

@@ -1,0 +1,763 @@
+// Prompt prefill for gfx950: every token of the prompt in one pass per layer.
+//
+// Kernels:
+// - the int4 GEMM on MFMA, with a store or a SwiGLU epilogue;
+// - the 4-tap causal conv over a sequence;
+// - the chunked gated delta rule;
+// - GatedRMSNorm over rows;
+// - q/k RMSNorm + partial RoPE over rows, which also writes the KV cache;
+// - causal GQA attention with the reference's bf16 softmax rounding.
+//
+// Every rounding point is the reference's forward over a sequence (reference.py:496-550,
+// 610-677, 692-735). Only fp32 summation order differs.
+#include <math.h>
+
+#include "common.h"
+#include "deltaforge_hip.h"
+
+namespace df {
+namespace pf {
+
+DF_DEVICE df_f32x4 mfma(const uint4& a, const uint4& b, df_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, a), __builtin_bit_cast(df_bf16x8, b),
+                                                 c, 0, 0, 0);
+}
+
+DF_DEVICE float readlane(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// ---------------------------------------------------------------------------------------
+// int4 GEMM: out[m][n] = bf16( sum_k x[m][k] * bf16((nibble - 8) * scale) ), fp32 sums
+// ---------------------------------------------------------------------------------------
+//
+// The weight is in the library's device tiling (df_int4_repack). A 1 KB block is 16 columns x
+// one 128-group, and lane L of a 64-lane read owns its bytes [16 L, 16 L + 16): four words of
+// column L % 16. Word i holds k = 32 (L / 16) + 8 i + e, e < 8, with element e at bit
+// 4 (e / 2), plus 16 when e is odd. That is exactly the B operand of
+// v_mfma_f32_16x16x32_bf16 number i, whose A operand is then x[row][32 (L / 16) + 8 i ..+8].
+// A workgroup computes a 128 x 128 tile. Its four waves each own 64 rows x 64 columns (4 x 4
+// products). Per 128-group, the x rows and the dequantised weights are staged in LDS.
+
+constexpr int kGmBM = 128;
+constexpr int kGmTiles = 8;           // 16-column tiles per workgroup (128 columns)
+constexpr int kGmXPitch = 128 + 8;    // bf16 per staged x row (16-byte pad)
+
+// Word `w` of a tiled block with its column scale -> bf16((n - 8) * s) for its 8 values, in
+// k order (the product (n - 8) * s is exact in fp32; the bf16 rounding is the reference's).
+DF_DEVICE uint4 dequant8(uint32_t w, float s) {
+  w ^= 0x88888888u;  // each nibble n becomes n - 8 as a signed 4-bit field
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int q0 = static_cast<int>(w << (28 - 4 * j)) >> 28;  // element 2j: bits 4j ..
+    const int q1 = static_cast<int>(w << (12 - 4 * j)) >> 28;  // element 2j+1: bits 16 + 4j ..
+    o[j] = static_cast<uint32_t>(f2bf(static_cast<float>(q0) * s)) |
+           (static_cast<uint32_t>(f2bf(static_cast<float>(q1) * s)) << 16);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void int4_gemm_kernel(DfInt4GemmArgs p) {
+  __shared__ __align__(16) uint16_t xs[kGmBM * kGmXPitch];
+  __shared__ __align__(16) uint4 ws[kGmTiles * 4 * 64];  // [tile][mfma i][lane]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+  const int m0 = blockIdx.y * kGmBM, t0 = blockIdx.x * kGmTiles;
+  const int G = p.K / 128, ntiles = p.N / 16;
+  df_f32x4 acc[4][4];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[rb][j] = df_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // x: 128 rows x 16 chunks of 16 bytes
+      const int ch = tid + 256 * i, r = ch >> 4, cc = ch & 15;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (m0 + r < p.M) v = *reinterpret_cast<const uint4*>(p.x + (size_t)(m0 + r) * p.ldx + g * 128 + cc * 8);
+      *reinterpret_cast<uint4*>(&xs[r * kGmXPitch + cc * 8]) = v;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // weights: 8 blocks x 64 lanes' 16 bytes
+      const int u = tid + 256 * i, j = u >> 6, L = u & 63;
+      uint4 wv = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);  // zeros past N
+      float sc = 0.0f;
+      if (t0 + j < ntiles) {
+        const size_t blk = (size_t)(t0 + j) * G + g;
+        wv = *reinterpret_cast<const uint4*>(p.w + blk * 1024 + L * 16);
+        sc = bf2f(p.s[blk * 16 + (L & 15)]);
+      }
+      ws[(j * 4 + 0) * 64 + L] = dequant8(wv.x, sc);
+      ws[(j * 4 + 1) * 64 + L] = dequant8(wv.y, sc);
+      ws[(j * 4 + 2) * 64 + L] = dequant8(wv.z, sc);
+      ws[(j * 4 + 3) * 64 + L] = dequant8(wv.w, sc);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint4 a[4], b[4];
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb)
+        a[rb] = *reinterpret_cast<const uint4*>(
+            &xs[(wr * 64 + rb * 16 + (lane & 15)) * kGmXPitch + (lane >> 4) * 32 + i * 8]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = ws[((wc * 4 + j) * 4 + i) * 64 + lane];
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[rb][j] = mfma(a[rb], b[j], acc[rb][j]);
+    }
+    __syncthreads();
+  }
+
+  // lane holds D[4 (lane / 16) + r][lane % 16] of each 16 x 16 product
+  const int col_in = lane & 15;
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = m0 + wr * 64 + rb * 16 + (lane >> 4) * 4 + r;
+      if (row >= p.M) continue;
+      if (EPI == DF_EPI_SWIGLU) {
+        // tiles alternate gate, up: product pairs (0, 1) and (2, 3) of this wave;
+        // bf16(bf16(silu(bf16(g))) * bf16(u)) (reference.py:692-693)
+#pragma unroll
+        for (int jp = 0; jp < 2; ++jp) {
+          const int tile = t0 + wc * 4 + 2 * jp;
+          if (tile >= ntiles) continue;
+          const float gv = round_bf(acc[rb][2 * jp][r]), uv = round_bf(acc[rb][2 * jp + 1][r]);
+          p.out[(size_t)row * p.ldo + (tile / 2) * 16 + col_in] = f2bf(round_bf(silu(gv)) * uv);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int tile = t0 + wc * 4 + j;
+          if (tile >= ntiles) continue;
+          p.out[(size_t)row * p.ldo + tile * 16 + col_in] = f2bf(acc[rb][j][r]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// causal conv over the sequence (reference.py:496-510)
+// ---------------------------------------------------------------------------------------
+
+// out[t][c] = bf16(silu(bf16(sum_j w[c][j] x(p - 3 + j)))) for position p = pos0 + t, taps in
+// order with fp32 sums (the decode step's arithmetic); x(q) is row q - pos0 of the input for
+// q >= pos0, else the history ring (slot q mod 4, zero for positions before the first).
+__global__ __launch_bounds__(256) void conv_seq_kernel(const uint16_t* __restrict__ x, int ldx, int tokens,
+                                                       int channels, const uint16_t* __restrict__ w,
+                                                       const uint16_t* __restrict__ ring, int pos0,
+                                                       uint16_t* __restrict__ out, int ldo) {
+#pragma clang fp contract(off)
+  const int c = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
+  if (c >= channels) return;
+  const uint2 wt = *reinterpret_cast<const uint2*>(w + (size_t)c * 4);
+  const float wk[4] = {__uint_as_float(wt.x << 16), __uint_as_float(wt.x & 0xFFFF0000u),
+                       __uint_as_float(wt.y << 16), __uint_as_float(wt.y & 0xFFFF0000u)};
+  float h[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int tt = t - 3 + j;
+    h[j] = tt >= 0 ? bf2f(x[(size_t)tt * ldx + c]) : bf2f(ring[(size_t)c * 4 + ((pos0 + tt) & 3)]);
+  }
+  float acc = h[0] * wk[0];
+  acc = acc + h[1] * wk[1];
+  acc = acc + h[2] * wk[2];
+  acc = acc + h[3] * wk[3];
+  out[(size_t)t * ldo + c] = f2bf(silu(round_bf(acc)));
+}
+
+// The last three inputs into the ring (slot position mod 4), after conv_seq_kernel read it.
+__global__ __launch_bounds__(256) void conv_ring_update_kernel(const uint16_t* __restrict__ x, int ldx, int tokens,
+                                                               int channels, uint16_t* __restrict__ ring, int pos0) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= channels) return;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int t = tokens - 3 + j;
+    if (t >= 0) ring[(size_t)c * 4 + ((pos0 + t) & 3)] = x[(size_t)t * ldx + c];
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// chunked gated delta rule (reference.py:403-461 over a sequence)
+// ---------------------------------------------------------------------------------------
+//
+// Within a chunk of C = 64 tokens, with cumulative log-decay gamma_t = g_1 + ... + g_t and
+// the chunk's initial state S0 (Dk x Dv), the token-by-token rule
+//   S <- exp(g_t) S;  delta_t = beta_t (v_t - S^T k_t);  S <- S + k_t delta_t^T;  o_t = S^T q_t
+// is, exactly:
+//   A[t][j]  = exp(gamma_t - gamma_j) (k_t . k_j), j < t           (strictly lower)
+//   delta    = solve (I + diag(beta) A) delta = diag(beta) (V - diag(exp gamma) K S0)
+//   O        = diag(exp gamma) Q S0 + (exp(gamma_t - gamma_j) (q_t . k_j))_{j <= t} delta
+//   S_C      = exp(gamma_C) S0 + sum_j exp(gamma_C - gamma_j) k_j delta_j^T
+// with q, k the L2-normalised rows (q also / sqrt(Dk)). The triangular solve is forward
+// substitution, one value column per register and one token per lane. A workgroup owns one
+// value head and 32 value columns, and walks the chunks in order with its state slice in LDS.
+// The S0-independent products (A, QK) are recomputed by the head's four workgroups.
+
+constexpr int kCk = 64;         // tokens per chunk
+constexpr int kDk = 128;        // key (and value) head dim
+constexpr int kVs = 32;         // value columns per workgroup
+constexpr int kKPitch = kDk + 4;
+
+struct DeltaLds {
+  float S[kDk][kVs];
+  float K[kCk][kKPitch];
+  float Q[kCk][kKPitch];
+  float A[kCk][kCk];
+  float QK[kCk][kCk];
+  float U[kCk][kVs + 1];   // V, then V - e^gamma K S0
+  float D[kCk][kVs + 1];   // delta
+  float gam[kCk], beta[kCk], eg[kCk], dec[kCk];
+};
+
+__global__ __launch_bounds__(256) void delta_chunked_kernel(DfDeltaPrefillArgs p) {
+  __shared__ __align__(16) DeltaLds L;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.x, vs = blockIdx.y;
+  const int kh = h / (p.num_v_heads / p.num_k_heads);
+  const int key_dim = p.num_k_heads * kDk;
+  const int qoff = kh * kDk, koff = key_dim + kh * kDk, voff = 2 * key_dim + h * kDk + vs * kVs;
+  float* gstate = p.state + (size_t)h * kDk * kDk;
+  for (int e = tid; e < kDk * kVs; e += 256) L.S[e / kVs][e % kVs] = gstate[(size_t)(e / kVs) * kDk + vs * kVs + e % kVs];
+  const float alog = bf2f(p.A_log[h]), dtb = bf2f(p.dt_bias[h]);
+  const float qscale = sqrtf(static_cast<float>(kDk));
+
+  for (int c0 = 0; c0 < p.tokens; c0 += kCk) {
+    // ---- 1: normalised q, k rows; v slice; gates -----------------------------------
+    for (int t = wave * 16; t < wave * 16 + 16; ++t) {
+      const int T = c0 + t;
+      float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f;
+      if (T < p.tokens) {
+        const uint16_t* row = p.mixed + (size_t)T * p.ld_mixed;
+        const uint32_t qw = *reinterpret_cast<const uint32_t*>(row + qoff + 2 * lane);
+        const uint32_t kw = *reinterpret_cast<const uint32_t*>(row + koff + 2 * lane);
+        q0 = __uint_as_float(qw << 16);
+        q1 = __uint_as_float(qw & 0xFFFF0000u);
+        k0 = __uint_as_float(kw << 16);
+        k1 = __uint_as_float(kw & 0xFFFF0000u);
+        if (lane < kVs) L.U[t][lane] = bf2f(row[voff + lane]);
+      } else if (lane < kVs) {
+        L.U[t][lane] = 0.0f;
+      }
+      const float rq = 1.0f / sqrtf(wave_sum(q0 * q0 + q1 * q1) + 1e-6f);
+      const float rk = 1.0f / sqrtf(wave_sum(k0 * k0 + k1 * k1) + 1e-6f);
+      L.Q[t][2 * lane] = (q0 * rq) / qscale;
+      L.Q[t][2 * lane + 1] = (q1 * rq) / qscale;
+      L.K[t][2 * lane] = k0 * rk;
+      L.K[t][2 * lane + 1] = k1 * rk;
+    }
+    if (wave == 0) {
+      const int T = c0 + lane;
+      float g = 0.0f, beta = 0.0f;
+      if (T < p.tokens) {
+        const float av = bf2f(p.a[(size_t)T * p.ld_ab + h]), bv = bf2f(p.b[(size_t)T * p.ld_ab + h]);
+        beta = round_bf(sigmoid(bv));                       // sigmoid of the bf16 projection, bf16
+        g = -expf(alog) * softplus(av + dtb);               // fp32 (reference.py:528-532)
+      }
+      float gam = g;  // inclusive prefix sum over the chunk's tokens
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float o = __shfl_up(gam, off, 64);
+        if (lane >= off) gam += o;
+      }
+      const float last = readlane(gam, 63);
+      L.gam[lane] = gam;
+      L.beta[lane] = beta;
+      L.eg[lane] = expf(gam);
+      L.dec[lane] = expf(last - gam);
+    }
+    __syncthreads();
+
+    // ---- 2: A (strictly lower) and QK (lower), decayed --------------------------------
+    {
+      const int tb = tid >> 4, jb = tid & 15;
+      float aa[4][4], qq[4][4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) aa[r][c] = qq[r][c] = 0.0f;
+      if (jb <= tb) {
+        for (int k = 0; k < kDk; k += 4) {
+          float4 kt[4], kj[4], qt[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            kt[r] = *reinterpret_cast<const float4*>(&L.K[tb * 4 + r][k]);
+            qt[r] = *reinterpret_cast<const float4*>(&L.Q[tb * 4 + r][k]);
+            kj[r] = *reinterpret_cast<const float4*>(&L.K[jb * 4 + r][k]);
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              aa[r][c] += kt[r].x * kj[c].x + kt[r].y * kj[c].y + kt[r].z * kj[c].z + kt[r].w * kj[c].w;
+              qq[r][c] += qt[r].x * kj[c].x + qt[r].y * kj[c].y + qt[r].z * kj[c].z + qt[r].w * kj[c].w;
+            }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int t = tb * 4 + r, j = jb * 4 + c;
+          const float d = j <= t ? expf(L.gam[t] - L.gam[j]) : 0.0f;
+          L.A[t][j] = j < t ? aa[r][c] * d : 0.0f;
+          L.QK[t][j] = j <= t ? qq[r][c] * d : 0.0f;
+        }
+    }
+    // ---- 3: U = V - e^gamma K S0 (reads K, S; writes U rows this thread owns) ----------
+    {
+      const int t = tid >> 2, c0s = (tid & 3) * 8;
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int k = 0; k < kDk; k += 4) {
+        const float4 kv = *reinterpret_cast<const float4*>(&L.K[t][k]);
+        const float kk[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float4 s0 = *reinterpret_cast<const float4*>(&L.S[k + e][c0s]);
+          const float4 s1 = *reinterpret_cast<const float4*>(&L.S[k + e][c0s + 4]);
+          acc[0] += kk[e] * s0.x; acc[1] += kk[e] * s0.y; acc[2] += kk[e] * s0.z; acc[3] += kk[e] * s0.w;
+          acc[4] += kk[e] * s1.x; acc[5] += kk[e] * s1.y; acc[6] += kk[e] * s1.z; acc[7] += kk[e] * s1.w;
+        }
+      }
+      const float egt = L.eg[t];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) L.U[t][c0s + c] = L.U[t][c0s + c] - egt * acc[c];
+    }
+    __syncthreads();
+
+    // ---- 4: forward substitution; wave w solves value columns 8w .. 8w + 7 ------------
+    {
+      float arow[kCk];
+#pragma unroll
+      for (int j = 0; j < kCk; j += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(&L.A[lane][j]);
+        arow[j] = v.x; arow[j + 1] = v.y; arow[j + 2] = v.z; arow[j + 3] = v.w;
+      }
+      float acc[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc[c] = L.U[lane][wave * 8 + c];
+      const float bl = L.beta[lane];
+#pragma unroll
+      for (int j = 0; j < kCk; ++j) {
+        const float bj = readlane(bl, j);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float dj = readlane(acc[c], j) * bj;  // delta_j: every term of j's sum is in
+          acc[c] = fmaf(-arow[j], dj, acc[c]);        // A[t][j] = 0 for j >= t
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 8; ++c) L.D[lane][wave * 8 + c] = bl * acc[c];
+    }
+    __syncthreads();
+
+    // ---- 5: O = e^gamma Q S0 + QK delta ----------------------------------------------
+    {
+      const int t = tid >> 2, c0s = (tid & 3) * 8;
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int k = 0; k < kDk; k += 4) {
+        const float4 qv = *reinterpret_cast<const float4*>(&L.Q[t][k]);
+        const float qk[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float4 s0 = *reinterpret_cast<const float4*>(&L.S[k + e][c0s]);
+          const float4 s1 = *reinterpret_cast<const float4*>(&L.S[k + e][c0s + 4]);
+          acc[0] += qk[e] * s0.x; acc[1] += qk[e] * s0.y; acc[2] += qk[e] * s0.z; acc[3] += qk[e] * s0.w;
+          acc[4] += qk[e] * s1.x; acc[5] += qk[e] * s1.y; acc[6] += qk[e] * s1.z; acc[7] += qk[e] * s1.w;
+        }
+      }
+      const float egt = L.eg[t];
+      float o[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) o[c] = egt * acc[c];
+      for (int j = 0; j <= t; ++j) {
+        const float w = L.QK[t][j];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) o[c] += w * L.D[j][c0s + c];
+      }
+      if (c0 + t < p.tokens) {
+        uint32_t packed[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          packed[c] = static_cast<uint32_t>(f2bf(o[2 * c])) | (static_cast<uint32_t>(f2bf(o[2 * c + 1])) << 16);
+        *reinterpret_cast<uint4*>(p.out + (size_t)(c0 + t) * p.ld_out + h * kDk + vs * kVs + c0s) =
+            make_uint4(packed[0], packed[1], packed[2], packed[3]);
+      }
+    }
+    __syncthreads();
+
+    // ---- 6: S <- e^gamma_C S0 + sum_j e^(gamma_C - gamma_j) k_j delta_j^T ------------
+    {
+      const int k = tid >> 1, cs = (tid & 1) * 16;
+      float acc[16];
+#pragma unroll
+      for (int c = 0; c < 16; ++c) acc[c] = 0.0f;
+      for (int j = 0; j < kCk; ++j) {
+        const float kd = L.K[j][k] * L.dec[j];
+#pragma unroll
+        for (int c = 0; c < 16; ++c) acc[c] += kd * L.D[j][cs + c];
+      }
+      const float egl = L.eg[kCk - 1];
+#pragma unroll
+      for (int c = 0; c < 16; ++c) L.S[k][cs + c] = egl * L.S[k][cs + c] + acc[c];
+    }
+    __syncthreads();
+  }
+  for (int e = tid; e < kDk * kVs; e += 256) gstate[(size_t)(e / kVs) * kDk + vs * kVs + e % kVs] = L.S[e / kVs][e % kVs];
+}
+
+// ---------------------------------------------------------------------------------------
+// GatedRMSNorm over rows (reference.py:115-121): one wave per (token, value head)
+// ---------------------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void gated_norm_rows_kernel(const uint16_t* __restrict__ x, int ldx,
+                                                              const uint16_t* __restrict__ z, int ldz,
+                                                              const uint16_t* __restrict__ w, float eps, int tokens,
+                                                              int heads, uint16_t* __restrict__ out, int ldo) {
+  const int lane = threadIdx.x & 63;
+  const int unit = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (unit >= tokens * heads) return;
+  const int t = unit / heads, hh = unit % heads;
+  const int d = hh * 128 + 2 * lane;
+  const uint32_t xv = *reinterpret_cast<const uint32_t*>(x + (size_t)t * ldx + d);
+  const uint32_t zv = *reinterpret_cast<const uint32_t*>(z + (size_t)t * ldz + d);
+  const uint32_t wv = *reinterpret_cast<const uint32_t*>(w + 2 * lane);
+  const float x0 = __uint_as_float(xv << 16), x1 = __uint_as_float(xv & 0xFFFF0000u);
+  const float r = 1.0f / sqrtf(wave_sum(x0 * x0 + x1 * x1) / 128.0f + eps);
+  const float n0 = round_bf(x0 * r), n1 = round_bf(x1 * r);
+  const float y0 = round_bf(__uint_as_float(wv << 16) * n0), y1 = round_bf(__uint_as_float(wv & 0xFFFF0000u) * n1);
+  const float g0 = silu(__uint_as_float(zv << 16)), g1 = silu(__uint_as_float(zv & 0xFFFF0000u));
+  *reinterpret_cast<uint32_t*>(out + (size_t)t * ldo + d) =
+      static_cast<uint32_t>(f2bf(y0 * g0)) | (static_cast<uint32_t>(f2bf(y1 * g1)) << 16);
+}
+
+// ---------------------------------------------------------------------------------------
+// q/k RMSNorm (1 + w) + partial RoPE over rows; K/V cache rows written
+// ---------------------------------------------------------------------------------------
+
+constexpr int kHd = 256;
+
+// The decode kernel's norm_rope4 arithmetic (attention.hip), from global rows: lane holds
+// dims 4 lane .. 4 lane + 3.
+DF_DEVICE void norm_rope_row(float x[4], const uint16_t* nw, float eps, const float* inv_freq, int rot, float posf,
+                             int lane) {
+  float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(kHd) + eps);
+  float n[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) n[i] = round_bf((x[i] * r) * (1.0f + bf2f(nw[lane * 4 + i])));
+  const int half = rot / 2;
+  float partner[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) partner[i] = __shfl_xor(n[i], half / 4, 64);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int dim = lane * 4 + i;
+    if (dim < rot) {
+      const float ang = posf * inv_freq[dim % half];
+      const float c = round_bf(cosf(ang)), s = round_bf(sinf(ang));
+      const float rotated = dim < half ? -partner[i] : partner[i];
+      x[i] = round_bf(round_bf(n[i] * c) + round_bf(rotated * s));
+    } else {
+      x[i] = n[i];
+    }
+  }
+}
+
+DF_DEVICE void load4(const uint16_t* src, float x[4]) {
+  const uint2 v = *reinterpret_cast<const uint2*>(src);
+  x[0] = __uint_as_float(v.x << 16);
+  x[1] = __uint_as_float(v.x & 0xFFFF0000u);
+  x[2] = __uint_as_float(v.y << 16);
+  x[3] = __uint_as_float(v.y & 0xFFFF0000u);
+}
+DF_DEVICE void store4(uint16_t* dst, const float x[4]) {
+  *reinterpret_cast<uint2*>(dst) =
+      make_uint2(static_cast<uint32_t>(f2bf(x[0])) | (static_cast<uint32_t>(f2bf(x[1])) << 16),
+                 static_cast<uint32_t>(f2bf(x[2])) | (static_cast<uint32_t>(f2bf(x[3])) << 16));
+}
+
+// One wave per (token, slot): slots < Hq are query heads (normed, roped -> q_out), the next Hkv
+// are KV heads (key normed and roped, value copied, both into the cache at pos0 + t).
+__global__ __launch_bounds__(256) void qk_rows_kernel(DfQkPrefillArgs p) {
+  const int lane = threadIdx.x & 63;
+  const int slots = p.num_q_heads + p.num_kv_heads;
+  const int unit = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (unit >= p.tokens * slots) return;
+  const int t = unit / slots, sl = unit % slots;
+  const float posf = static_cast<float>(p.pos0 + t);
+  const uint16_t* row = p.proj + (size_t)t * p.ld_proj;
+  float x[4];
+  if (sl < p.num_q_heads) {
+    load4(row + sl * 2 * kHd + lane * 4, x);  // head sl's [query | gate]: the query half
+    norm_rope_row(x, p.q_norm, p.eps, p.inv_freq, p.rotary_dim, posf, lane);
+    store4(p.q_out + ((size_t)t * p.num_q_heads + sl) * kHd + lane * 4, x);
+  } else {
+    const int g = sl - p.num_q_heads;
+    load4(row + p.k_col + g * kHd + lane * 4, x);
+    norm_rope_row(x, p.k_norm, p.eps, p.inv_freq, p.rotary_dim, posf, lane);
+    const size_t dst = ((size_t)g * p.max_len + p.pos0 + t) * kHd + lane * 4;
+    store4(p.k_cache + dst, x);
+    *reinterpret_cast<uint2*>(p.v_cache + dst) = *reinterpret_cast<const uint2*>(row + p.v_col + g * kHd + lane * 4);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// causal GQA attention over the prompt (reference.py:645-677)
+// ---------------------------------------------------------------------------------------
+//
+// scores = bf16(bf16(q . k) * scale), masked above the diagonal; p = bf16(softmax_fp32);
+// o = bf16(p @ V); out = bf16(o * bf16(gate_fn(gate))). The bf16 rounding of p needs the
+// row's final max and sum, so the keys are visited twice: pass 1 finds (max, sum), pass 2
+// forms p and accumulates p V. A workgroup owns 16 query positions of one KV head; wave w is
+// query head 4 g + w. Products run on v_mfma_f32_16x16x32_bf16 (query rows x keys, then
+// query rows x head dims); keys are staged 64 at a time, V transposed for its B operand.
+
+constexpr int kAtKeys = 64;
+constexpr int kKsPitch = kHd + 8;
+constexpr int kVtPitch = kAtKeys + 8;
+constexpr int kPtPitch = kAtKeys + 8;
+
+__global__ __launch_bounds__(256, 2) void attn_prefill_kernel(DfAttnPrefillArgs p) {
+  __shared__ __align__(16) uint16_t Ks[kAtKeys * kKsPitch];
+  __shared__ __align__(16) uint16_t Vt[kHd * kVtPitch];
+  __shared__ __align__(16) uint16_t Pt[4][16 * kPtPitch];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.y, h = g * 4 + wave;
+  const int t0 = blockIdx.x * 16;
+  const int rq = lane & 15, kq = lane >> 4;
+  // A operands of q . k: row rq, dims 32 ds + 8 kq .. + 8
+  uint4 qa[8];
+  {
+    const int t = t0 + rq;
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds)
+      qa[ds] = t < p.tokens
+                   ? *reinterpret_cast<const uint4*>(p.q + ((size_t)t * p.num_q_heads + h) * kHd + ds * 32 + kq * 8)
+                   : make_uint4(0u, 0u, 0u, 0u);
+  }
+  const int last_t = min(t0 + 16, p.tokens) - 1;
+  const int nkeys = p.pos0 + last_t + 1;  // keys any row of the block attends
+  const int nkb = (nkeys + kAtKeys - 1) / kAtKeys;
+  const uint16_t* kbase = p.k_cache + (size_t)g * p.max_len * kHd;
+  const uint16_t* vbase = p.v_cache + (size_t)g * p.max_len * kHd;
+  // this lane's rows of the 16 x 16 products: 4 kq + r, at positions pos0 + t0 + 4 kq + r
+  float m[4], l[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.0f;
+  }
+
+  auto stage_k = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // 64 keys x 32 chunks of 16 bytes
+      const int ch = tid + 256 * i, key = ch >> 5, cc = ch & 31;
+      const int kg = kb * kAtKeys + key;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (kg < nkeys) v = *reinterpret_cast<const uint4*>(kbase + (size_t)kg * kHd + cc * 8);
+      *reinterpret_cast<uint4*>(&Ks[key * kKsPitch + cc * 8]) = v;
+    }
+  };
+  // scores of key block kb for this lane: s[sb][r] (key kb*64 + 16 sb + lane % 16)
+  auto scores = [&](int kb, float (&s)[4][4]) {
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      df_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ds = 0; ds < 8; ++ds) {
+        const uint4 b = *reinterpret_cast<const uint4*>(&Ks[(sb * 16 + rq) * kKsPitch + ds * 32 + kq * 8]);
+        acc = mfma(qa[ds], b, acc);
+      }
+      const int key = kb * kAtKeys + sb * 16 + rq;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int pos = p.pos0 + t0 + kq * 4 + r;
+        s[sb][r] = key <= pos ? round_bf(round_bf(acc[r]) * p.scale) : -INFINITY;
+      }
+    }
+  };
+
+  // ---- pass 1: row max and sum --------------------------------------------------------
+  for (int kb = 0; kb < nkb; ++kb) {
+    stage_k(kb);
+    __syncthreads();
+    float s[4][4];
+    scores(kb, s);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float mx = fmaxf(fmaxf(s[0][r], s[1][r]), fmaxf(s[2][r], s[3][r]));
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      const float mn = fmaxf(m[r], mx);
+      float sum = 0.0f;
+#pragma unroll
+      for (int sb = 0; sb < 4; ++sb) sum += s[sb][r] == -INFINITY ? 0.0f : expf(s[sb][r] - mn);
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
+      l[r] = (m[r] == -INFINITY ? 0.0f : l[r] * expf(m[r] - mn)) + sum;
+      m[r] = mn;
+    }
+    __syncthreads();
+  }
+
+  // ---- pass 2: p = bf16(exp(s - max) / sum), o += p V ----------------------------------
+  df_f32x4 o[16];
+#pragma unroll
+  for (int db = 0; db < 16; ++db) o[db] = df_f32x4{0.f, 0.f, 0.f, 0.f};
+  uint16_t* pt = Pt[wave];
+  for (int kb = 0; kb < nkb; ++kb) {
+    stage_k(kb);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // V transposed: Vt[d][key]
+      const int ch = tid + 256 * i, key = ch >> 5, cc = ch & 31;
+      const int kg = kb * kAtKeys + key;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (kg < nkeys) v = *reinterpret_cast<const uint4*>(vbase + (size_t)kg * kHd + cc * 8);
+      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        Vt[(cc * 8 + e) * kVtPitch + key] = static_cast<uint16_t>(vw[e >> 1] >> (16 * (e & 1)));
+    }
+    __syncthreads();
+    float s[4][4];
+    scores(kb, s);
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pr = s[sb][r] == -INFINITY ? 0.0f : expf(s[sb][r] - m[r]) / l[r];
+        pt[(kq * 4 + r) * kPtPitch + sb * 16 + rq] = f2bf(pr);
+      }
+    __syncthreads();  // p rows are read back by other lanes of the wave in the A layout
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const uint4 pa = *reinterpret_cast<const uint4*>(&pt[rq * kPtPitch + ks * 32 + kq * 8]);
+#pragma unroll
+      for (int db = 0; db < 16; ++db) {
+        const uint4 b = *reinterpret_cast<const uint4*>(&Vt[(db * 16 + rq) * kVtPitch + ks * 32 + kq * 8]);
+        o[db] = mfma(pa, b, o[db]);
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: bf16(o) * bf16(gate_fn(gate)) ----------------------------------------
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = t0 + kq * 4 + r;
+    if (t >= p.tokens) continue;
+    const uint16_t* gr = p.gate + (size_t)t * p.ld_gate + h * p.gate_head_stride;
+    uint16_t* orow = p.out + (size_t)t * p.ld_out + h * kHd;
+#pragma unroll
+    for (int db = 0; db < 16; ++db) {
+      const int d = db * 16 + rq;
+      const float gx = bf2f(gr[d]);
+      const float gv = round_bf(p.gate_kind == 0 ? sigmoid(gx) : silu(gx));
+      orow[d] = f2bf(round_bf(o[db][r]) * gv);
+    }
+  }
+}
+
+}  // namespace pf
+}  // namespace df
+
+using namespace df;
+using namespace df::pf;
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+extern "C" {
+
+int df_int4_gemm(const DfInt4GemmArgs* a, hipStream_t stream) {
+  if (!a || !a->x || !a->w || !a->s || !a->out || a->M < 1 || a->K < 256 || a->K % 256 || a->N < 16 || a->N % 16)
+    return DF_BAD_ARGUMENT;
+  if (a->epilogue != DF_EPI_STORE && a->epilogue != DF_EPI_SWIGLU) return DF_BAD_ARGUMENT;
+  if (a->epilogue == DF_EPI_SWIGLU && a->N % 32) return DF_BAD_ARGUMENT;
+  const int out_cols = a->epilogue == DF_EPI_SWIGLU ? a->N / 2 : a->N;
+  if (a->ldx < a->K || a->ldx % 8 || a->ldo < out_cols || !aligned16(a->x) || !aligned16(a->w))
+    return DF_BAD_ARGUMENT;
+  const dim3 grid((a->N / 16 + kGmTiles - 1) / kGmTiles, (a->M + kGmBM - 1) / kGmBM);
+  if (grid.y > 65535) return DF_BAD_ARGUMENT;
+  if (a->epilogue == DF_EPI_SWIGLU)
+    hipLaunchKernelGGL(int4_gemm_kernel<DF_EPI_SWIGLU>, grid, dim3(256), 0, stream, *a);
+  else
+    hipLaunchKernelGGL(int4_gemm_kernel<DF_EPI_STORE>, grid, dim3(256), 0, stream, *a);
+  DF_RETURN_LAUNCH_STATUS();
+}
+
+int df_causal_conv_prefill(const uint16_t* x, int ldx, int tokens, int channels, const uint16_t* weight,
+                           uint16_t* ring, int pos0, uint16_t* out, int ldo, hipStream_t stream) {
+  if (!x || !weight || !ring || !out || tokens < 1 || channels < 1 || ldx < channels || ldo < channels || pos0 < 0 ||
+      (reinterpret_cast<uintptr_t>(weight) & 7) || tokens > 65535)
+    return DF_BAD_ARGUMENT;
+  const int cb = (channels + 255) / 256;
+  hipLaunchKernelGGL(conv_seq_kernel, dim3(cb, tokens), dim3(256), 0, stream, x, ldx, tokens, channels, weight, ring,
+                     pos0, out, ldo);
+  hipLaunchKernelGGL(conv_ring_update_kernel, dim3(cb), dim3(256), 0, stream, x, ldx, tokens, channels, ring, pos0);
+  DF_RETURN_LAUNCH_STATUS();
+}
+
+int df_delta_rule_prefill(const DfDeltaPrefillArgs* a, hipStream_t stream) {
+  if (!a || !a->mixed || !a->a || !a->b || !a->A_log || !a->dt_bias || !a->state || !a->out || a->tokens < 1)
+    return DF_BAD_ARGUMENT;
+  if (a->num_k_heads < 1 || a->num_v_heads < 1 || a->num_v_heads % a->num_k_heads) return DF_BAD_ARGUMENT;
+  const int channels = 2 * a->num_k_heads * kDk + a->num_v_heads * kDk;
+  if (a->ld_mixed < channels || a->ld_mixed % 2 || a->ld_out < a->num_v_heads * kDk || a->ld_out % 8 ||
+      a->ld_ab < a->num_v_heads || (reinterpret_cast<uintptr_t>(a->mixed) & 3) || !aligned16(a->out))
+    return DF_BAD_ARGUMENT;
+  hipLaunchKernelGGL(delta_chunked_kernel, dim3(a->num_v_heads, kDk / kVs), dim3(256), 0, stream, *a);
+  DF_RETURN_LAUNCH_STATUS();
+}
+
+int df_gated_rms_norm_rows(const uint16_t* x, int ldx, const uint16_t* z, int ldz, const uint16_t* weight, float eps,
+                           int tokens, int heads, uint16_t* out, int ldo, hipStream_t stream) {
+  if (!x || !z || !weight || !out || tokens < 1 || heads < 1 || ldx < heads * 128 || ldz < heads * 128 ||
+      ldo < heads * 128 || ldx % 2 || ldz % 2 || ldo % 2 || (reinterpret_cast<uintptr_t>(x) & 3) ||
+      (reinterpret_cast<uintptr_t>(z) & 3) || (reinterpret_cast<uintptr_t>(out) & 3) ||
+      (reinterpret_cast<uintptr_t>(weight) & 3))
+    return DF_BAD_ARGUMENT;
+  const long units = (long)tokens * heads;
+  hipLaunchKernelGGL(gated_norm_rows_kernel, dim3((units + 3) / 4), dim3(256), 0, stream, x, ldx, z, ldz, weight, eps,
+                     tokens, heads, out, ldo);
+  DF_RETURN_LAUNCH_STATUS();
+}
+
+int df_qk_norm_rope_prefill(const DfQkPrefillArgs* a, hipStream_t stream) {
+  if (!a || !a->proj || !a->q_norm || !a->k_norm || !a->inv_freq || !a->q_out || !a->k_cache || !a->v_cache ||
+      a->tokens < 1 || a->num_q_heads < 1 || a->num_kv_heads < 1 || a->pos0 < 0 ||
+      a->pos0 + a->tokens > a->max_len)
+    return DF_BAD_ARGUMENT;
+  const int half = a->rotary_dim / 2;
+  if (a->rotary_dim > kHd || half < 4 || (half & (half - 1))) return DF_BAD_ARGUMENT;
+  if (a->ld_proj % 4 || a->k_col % 4 || a->v_col % 4 || (reinterpret_cast<uintptr_t>(a->proj) & 7) ||
+      a->ld_proj < a->num_q_heads * 2 * kHd || a->k_col + a->num_kv_heads * kHd > a->ld_proj ||
+      a->v_col + a->num_kv_heads * kHd > a->ld_proj)
+    return DF_BAD_ARGUMENT;
+  const long units = (long)a->tokens * (a->num_q_heads + a->num_kv_heads);
+  hipLaunchKernelGGL(qk_rows_kernel, dim3((units + 3) / 4), dim3(256), 0, stream, *a);
+  DF_RETURN_LAUNCH_STATUS();
+}
+
+int df_attention_prefill(const DfAttnPrefillArgs* a, hipStream_t stream) {
+  if (!a || !a->q || !a->k_cache || !a->v_cache || !a->gate || !a->out || a->tokens < 1 || a->pos0 < 0 ||
+      a->pos0 + a->tokens > a->max_len || a->num_kv_heads < 1 || a->num_q_heads != 4 * a->num_kv_heads)
+    return DF_BAD_ARGUMENT;
+  if (!aligned16(a->q) || !aligned16(a->k_cache) || !aligned16(a->v_cache) || a->ld_out < a->num_q_heads * kHd ||
+      a->gate_kind < 0 || a->gate_kind > 1)
+    return DF_BAD_ARGUMENT;
+  const int qb = (a->tokens + 15) / 16;
+  hipLaunchKernelGGL(attn_prefill_kernel, dim3(qb, a->num_kv_heads), dim3(256), 0, stream, *a);
+  DF_RETURN_LAUNCH_STATUS();
+}
+
+}  // extern "C"

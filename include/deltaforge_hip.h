@@ -235,6 +235,93 @@ int df_argmax(const uint16_t* logits, int rows, int n, int64_t* tokens, int64_t*
               int log_stride, int* position, int advance, int* step, void* workspace,
               size_t workspace_bytes, hipStream_t stream);
 
+/* ---- prompt prefill (every token of the prompt per launch) ----------------------
+ * The reference runs a prompt through ReferenceModel.forward with seq_len = P
+ * (reference.py:779-817): the projections as [P, K] x [K, N] products, the conv over the
+ * sequence, the sequential delta-rule scan (reference.py:450-458) and causal attention. These
+ * entry points are that forward's pieces. Rounding points are the reference's; only fp32
+ * summation order differs. */
+
+/* out = bf16(x @ bf16(dequant(W))), fp32 sums, W in the device tiling of df_int4_repack
+ * (reference kernels/quantised_linear.py GEMV_MAX_ROWS dense fallback, which dequantises and
+ * calls F.linear for more than 64 rows). epilogue DF_EPI_STORE: out [M][N]. DF_EPI_SWIGLU:
+ * W's 16-column tiles alternate gate, up; out [M][N/2] = bf16(bf16(silu(gate)) * up).
+ * K % 256 == 0, N % 16 == 0 (32 for SwiGLU), ldx % 8 == 0, x and w 16-byte aligned. */
+typedef struct DfInt4GemmArgs {
+  const uint16_t* x;
+  const uint8_t* w;
+  const uint16_t* s;
+  uint16_t* out;
+  int M, K, N, ldx, ldo, epilogue;
+} DfInt4GemmArgs;
+int df_int4_gemm(const DfInt4GemmArgs* args, hipStream_t stream);
+
+/* Causal 4-tap conv + SiLU over `tokens` rows at positions pos0 .. pos0 + tokens - 1
+ * (reference.py:496-510 with the decode step's fp32 tap order): x [tokens][ldx] (channels
+ * 0 .. channels-1), weight [channels][4]; history from ring [channels][4] (slot = position
+ * mod 4, as the decode step keeps it); afterwards the ring holds the last three inputs. */
+int df_causal_conv_prefill(const uint16_t* x, int ldx, int tokens, int channels, const uint16_t* weight,
+                           uint16_t* ring, int pos0, uint16_t* out, int ldo, hipStream_t stream);
+
+/* Gated delta rule over a sequence, chunked (64 tokens) and exact in real arithmetic to the
+ * token-by-token scan (reference.py:403-461): q, k L2-normalised (q / sqrt(128)), GQA value
+ * head h on key head h / (Hv / Hk), beta = bf16(sigmoid(b)), g = -exp(A_log) softplus(a +
+ * dt_bias). mixed: the conv output [tokens][ld_mixed] = q | k | v channels; a, b: the raw
+ * bf16 gate projections [tokens][ld_ab]; state [Hv][128][128] fp32 read and updated;
+ * out [tokens][ld_out] bf16 (head h at column 128 h). */
+typedef struct DfDeltaPrefillArgs {
+  const uint16_t* mixed;
+  const uint16_t* a;
+  const uint16_t* b;
+  const uint16_t* A_log;
+  const uint16_t* dt_bias;
+  float* state;
+  uint16_t* out;
+  int ld_mixed, ld_ab, ld_out;
+  int tokens, num_k_heads, num_v_heads;
+} DfDeltaPrefillArgs;
+int df_delta_rule_prefill(const DfDeltaPrefillArgs* args, hipStream_t stream);
+
+/* GatedRMSNorm over rows (reference.py:115-121): per 128-wide head of x,
+ * out = bf16(bf16(w * bf16(x rsqrt(mean x^2 + eps))) * silu(z)). */
+int df_gated_rms_norm_rows(const uint16_t* x, int ldx, const uint16_t* z, int ldz, const uint16_t* weight, float eps,
+                           int tokens, int heads, uint16_t* out, int ldo, hipStream_t stream);
+
+/* The attention projection's rows (reference.py:617-639): proj [tokens][ld_proj] holds per
+ * query head [query 256 | gate 256], then keys at k_col, values at v_col (head_dim 256).
+ * Queries and keys get RMSNorm (1 + w) and partial RoPE at position pos0 + t; queries go to
+ * q_out [tokens][Hq][256], keys and values into the caches [Hkv][max_len][256] at row pos0 + t. */
+typedef struct DfQkPrefillArgs {
+  const uint16_t* proj;
+  const uint16_t* q_norm;
+  const uint16_t* k_norm;
+  const float* inv_freq;
+  uint16_t* q_out;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int ld_proj, k_col, v_col;
+  int tokens, pos0, max_len, num_q_heads, num_kv_heads, rotary_dim;
+  float eps;
+} DfQkPrefillArgs;
+int df_qk_norm_rope_prefill(const DfQkPrefillArgs* args, hipStream_t stream);
+
+/* Causal GQA attention of `tokens` queries at positions pos0 .. over cache rows 0 .. pos
+ * (reference.py:645-677): scores = bf16(bf16(q.k) * scale), p = bf16(softmax_fp32),
+ * o = bf16(p V), out = bf16(o * bf16(gate_fn(gate))) with gate_fn sigmoid (gate_kind 0) or
+ * silu (1). Hq = 4 Hkv, head_dim 256. gate of head h, token t: gate[t * ld_gate + h *
+ * gate_head_stride + d]. */
+typedef struct DfAttnPrefillArgs {
+  const uint16_t* q;
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  const uint16_t* gate;
+  uint16_t* out;
+  int ld_gate, gate_head_stride, ld_out;
+  int tokens, pos0, max_len, num_q_heads, num_kv_heads, gate_kind;
+  float scale;
+} DfAttnPrefillArgs;
+int df_attention_prefill(const DfAttnPrefillArgs* args, hipStream_t stream);
+
 /* ---- persistent decode: many bs=1 tokens in one cooperative launch ------------------
  *
  * The whole decode step of greedy_decode (model.py:108-148 driving ReferenceModel.forward,
