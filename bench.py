@@ -66,10 +66,12 @@ GATE_UP_KERNEL = "w4_gemv_kernel<RMSNORM, SWIGLU> (post-attention norm + gate/up
 # the counter reads for a plain 256 MiB device copy (x 2.000 for FETCH_SIZE, x 1.000 for
 # WRITE_SIZE). Re-measure when the kernel changes.
 GATE_UP_TRAFFIC_BYTES = 12049 * 1024 * 2 + 18 * 1024
-# HBM bytes per decode token of the persistent kernel from the same calibrated PMC passes over
-# the timed 256-token launch (332,680,602 KiB fetched x 1.9998, 17,664,056 KiB written, / 256).
-# Re-measure when the kernel changes.
+# HBM bytes per decode token of the persistent kernel from the calibrated PMC passes over the
+# timed 256-token launch (332,680,602 KiB fetched x 1.9998, 17,664,056 KiB written, / 256),
+# recorded with their commands in PERSISTENT_TRAFFIC_SOURCE. Re-measure when the kernel changes.
 PERSISTENT_TRAFFIC_BYTES_PER_TOKEN = 2731843864
+PERSISTENT_TRAFFIC_SOURCE = ("profiles/decode_persistent_config5.md: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
+                             "over bench.py --steps 256, scaled by a 256 MiB copy in the same process")
 
 
 def gate_up_bytes(cfg) -> int:
@@ -231,7 +233,7 @@ def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path has no "
-              "multi-GPU mode: see DESIGN.md on how it would shard).", file=sys.stderr)
+              "multi-GPU mode; it would shard by value head, KV split and vocabulary rows).", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -281,6 +283,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(launch_bytes / seconds / 8e12, 4),
             "traffic": PERSISTENT_TRAFFIC_BYTES_PER_TOKEN * args.steps if PERSISTENT_TRAFFIC_BYTES_PER_TOKEN else None,
+            "traffic_source": PERSISTENT_TRAFFIC_SOURCE,
             "us_per_launch": round(seconds * 1e6, 1),
             "bytes_per_launch": launch_bytes,
             "tokens_per_launch": args.steps,
