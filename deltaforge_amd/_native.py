@@ -133,7 +133,8 @@ SIGNATURES = {
     "df_embed_bf16": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i, _i, _vp, _vp]),
     "df_int4_gemm": (_i, [C.POINTER(Int4GemmArgs), _vp]),
     "df_causal_conv_prefill": (_i, [_vp, _i, _i, _i, _vp, _vp, _i, _vp, _i, _vp]),
-    "df_delta_rule_prefill": (_i, [C.POINTER(DeltaPrefillArgs), _vp]),
+    "df_delta_rule_prefill_workspace_bytes": (_sz, [_i, _i]),
+    "df_delta_rule_prefill": (_i, [C.POINTER(DeltaPrefillArgs), _vp, _sz, _vp]),
     "df_gated_rms_norm_rows": (_i, [_vp, _i, _vp, _i, _vp, _f, _i, _i, _vp, _i, _vp]),
     "df_qk_norm_rope_prefill": (_i, [C.POINTER(QkPrefillArgs), _vp]),
     "df_attention_prefill": (_i, [C.POINTER(AttnPrefillArgs), _vp]),

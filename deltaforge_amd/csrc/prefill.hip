@@ -192,226 +192,282 @@ __global__ __launch_bounds__(256) void conv_ring_update_kernel(const uint16_t* _
 // Within a chunk of C = 64 tokens, with cumulative log-decay gamma_t = g_1 + ... + g_t and
 // the chunk's initial state S0 (Dk x Dv), the token-by-token rule
 //   S <- exp(g_t) S;  delta_t = beta_t (v_t - S^T k_t);  S <- S + k_t delta_t^T;  o_t = S^T q_t
-// is, exactly:
-//   A[t][j]  = exp(gamma_t - gamma_j) (k_t . k_j), j < t           (strictly lower)
-//   delta    = solve (I + diag(beta) A) delta = diag(beta) (V - diag(exp gamma) K S0)
-//   O        = diag(exp gamma) Q S0 + (exp(gamma_t - gamma_j) (q_t . k_j))_{j <= t} delta
-//   S_C      = exp(gamma_C) S0 + sum_j exp(gamma_C - gamma_j) k_j delta_j^T
-// with q, k the L2-normalised rows (q also / sqrt(Dk)). The triangular solve is forward
-// substitution, one value column per register and one token per lane. A workgroup owns one
-// value head and 32 value columns, and walks the chunks in order with its state slice in LDS.
-// The S0-independent products (A, QK) are recomputed by the head's four workgroups.
+// is, exactly in real arithmetic:
+//   A'[t][j] = beta_t exp(gamma_t - gamma_j) (k_t . k_j), j < t      (strictly lower)
+//   [Wv | Wk] = (I + A')^-1 [diag(beta) V | diag(beta e^gamma) K]      (forward substitution)
+//   delta    = Wv - Wk S0
+//   QK[t][j] = exp(gamma_t - gamma_j) (q_t . k_j), j <= t
+//   O        = O_loc + Qx S0,   O_loc = QK Wv,   Qx = diag(e^gamma) Q - QK Wk
+//   S_C      = e^gamma_C S0 + Kd^T delta,   Kd = diag(exp(gamma_C - gamma)) K
+// with q, k the L2-normalised rows (q also / sqrt(Dk)). Everything but the three products
+// with S0 is independent of the state, so it runs for every (chunk, head) at once
+// (delta_prep_kernel, 2048 workgroups at 4096 tokens). The scan kernel then walks the chunks
+// in order with the state slice in LDS and does only O, delta and the state update.
+// Padding tokens past the prompt get g = beta = 0 and q = k = v = 0, which changes nothing.
 
-constexpr int kCk = 64;         // tokens per chunk
-constexpr int kDk = 128;        // key (and value) head dim
-constexpr int kVs = 32;         // value columns per workgroup
-constexpr int kKPitch = kDk + 4;
+constexpr int kCk = 64;          // tokens per chunk
+constexpr int kDk = 128;         // key (and value) head dim
+constexpr int kPitch = kDk + 4;  // fp32 row pitch in LDS
+constexpr int kMat = kCk * kDk;  // floats of one chunk matrix in the scratch
+constexpr int kPrepMats = 5;     // O_loc, Qx, Wv, Wk, Kd
 
-struct DeltaLds {
-  float S[kDk][kVs];
-  float K[kCk][kKPitch];
-  float Q[kCk][kKPitch];
-  float A[kCk][kCk];
-  float QK[kCk][kCk];
-  float U[kCk][kVs + 1];   // V, then V - e^gamma K S0
-  float D[kCk][kVs + 1];   // delta
+DF_DEVICE size_t prep_base(int chunk, int h, int hv) { return ((size_t)chunk * hv + h) * kPrepMats * kMat; }
+
+struct PrepLds {
+  float Q[kCk][kPitch];
+  float K[kCk][kPitch];
+  float V[kCk][kPitch];
+  float A[kCk][kCk];    // beta_t-scaled, decayed, strictly lower
+  float QK[kCk][kCk];   // decayed, lower with the diagonal
   float gam[kCk], beta[kCk], eg[kCk], dec[kCk];
 };
 
-__global__ __launch_bounds__(256) void delta_chunked_kernel(DfDeltaPrefillArgs p) {
-  __shared__ __align__(16) DeltaLds L;
+__global__ __launch_bounds__(256) void delta_prep_kernel(DfDeltaPrefillArgs p, float* __restrict__ scratch) {
+  __shared__ __align__(16) PrepLds L;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int h = blockIdx.x, vs = blockIdx.y;
+  const int chunk = blockIdx.x, h = blockIdx.y;
+  const int c0 = chunk * kCk;
   const int kh = h / (p.num_v_heads / p.num_k_heads);
   const int key_dim = p.num_k_heads * kDk;
-  const int qoff = kh * kDk, koff = key_dim + kh * kDk, voff = 2 * key_dim + h * kDk + vs * kVs;
-  float* gstate = p.state + (size_t)h * kDk * kDk;
-  for (int e = tid; e < kDk * kVs; e += 256) L.S[e / kVs][e % kVs] = gstate[(size_t)(e / kVs) * kDk + vs * kVs + e % kVs];
-  const float alog = bf2f(p.A_log[h]), dtb = bf2f(p.dt_bias[h]);
+  const int qoff = kh * kDk, koff = key_dim + kh * kDk, voff = 2 * key_dim + h * kDk;
   const float qscale = sqrtf(static_cast<float>(kDk));
 
-  for (int c0 = 0; c0 < p.tokens; c0 += kCk) {
-    // ---- 1: normalised q, k rows; v slice; gates -----------------------------------
-    for (int t = wave * 16; t < wave * 16 + 16; ++t) {
-      const int T = c0 + t;
-      float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f;
-      if (T < p.tokens) {
-        const uint16_t* row = p.mixed + (size_t)T * p.ld_mixed;
-        const uint32_t qw = *reinterpret_cast<const uint32_t*>(row + qoff + 2 * lane);
-        const uint32_t kw = *reinterpret_cast<const uint32_t*>(row + koff + 2 * lane);
-        q0 = __uint_as_float(qw << 16);
-        q1 = __uint_as_float(qw & 0xFFFF0000u);
-        k0 = __uint_as_float(kw << 16);
-        k1 = __uint_as_float(kw & 0xFFFF0000u);
-        if (lane < kVs) L.U[t][lane] = bf2f(row[voff + lane]);
-      } else if (lane < kVs) {
-        L.U[t][lane] = 0.0f;
-      }
-      const float rq = 1.0f / sqrtf(wave_sum(q0 * q0 + q1 * q1) + 1e-6f);
-      const float rk = 1.0f / sqrtf(wave_sum(k0 * k0 + k1 * k1) + 1e-6f);
-      L.Q[t][2 * lane] = (q0 * rq) / qscale;
-      L.Q[t][2 * lane + 1] = (q1 * rq) / qscale;
-      L.K[t][2 * lane] = k0 * rk;
-      L.K[t][2 * lane + 1] = k1 * rk;
+  // ---- normalised q, k rows; v rows; gates --------------------------------------------
+  for (int t = wave * 16; t < wave * 16 + 16; ++t) {
+    const int T = c0 + t;
+    float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
+    if (T < p.tokens) {
+      const uint16_t* row = p.mixed + (size_t)T * p.ld_mixed;
+      const uint32_t qw = *reinterpret_cast<const uint32_t*>(row + qoff + 2 * lane);
+      const uint32_t kw = *reinterpret_cast<const uint32_t*>(row + koff + 2 * lane);
+      const uint32_t vw = *reinterpret_cast<const uint32_t*>(row + voff + 2 * lane);
+      q0 = __uint_as_float(qw << 16);
+      q1 = __uint_as_float(qw & 0xFFFF0000u);
+      k0 = __uint_as_float(kw << 16);
+      k1 = __uint_as_float(kw & 0xFFFF0000u);
+      v0 = __uint_as_float(vw << 16);
+      v1 = __uint_as_float(vw & 0xFFFF0000u);
     }
-    if (wave == 0) {
-      const int T = c0 + lane;
-      float g = 0.0f, beta = 0.0f;
-      if (T < p.tokens) {
-        const float av = bf2f(p.a[(size_t)T * p.ld_ab + h]), bv = bf2f(p.b[(size_t)T * p.ld_ab + h]);
-        beta = round_bf(sigmoid(bv));                       // sigmoid of the bf16 projection, bf16
-        g = -expf(alog) * softplus(av + dtb);               // fp32 (reference.py:528-532)
-      }
-      float gam = g;  // inclusive prefix sum over the chunk's tokens
+    const float rq = 1.0f / sqrtf(wave_sum(q0 * q0 + q1 * q1) + 1e-6f);
+    const float rk = 1.0f / sqrtf(wave_sum(k0 * k0 + k1 * k1) + 1e-6f);
+    L.Q[t][2 * lane] = (q0 * rq) / qscale;
+    L.Q[t][2 * lane + 1] = (q1 * rq) / qscale;
+    L.K[t][2 * lane] = k0 * rk;
+    L.K[t][2 * lane + 1] = k1 * rk;
+    L.V[t][2 * lane] = v0;
+    L.V[t][2 * lane + 1] = v1;
+  }
+  if (wave == 0) {
+    const int T = c0 + lane;
+    float g = 0.0f, beta = 0.0f;
+    if (T < p.tokens) {
+      const float av = bf2f(p.a[(size_t)T * p.ld_ab + h]), bv = bf2f(p.b[(size_t)T * p.ld_ab + h]);
+      beta = round_bf(sigmoid(bv));                                          // bf16 sigmoid
+      g = -expf(bf2f(p.A_log[h])) * softplus(av + bf2f(p.dt_bias[h]));      // fp32 (reference.py:528-532)
+    }
+    float gam = g;  // inclusive prefix sum over the chunk
 #pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float o = __shfl_up(gam, off, 64);
-        if (lane >= off) gam += o;
-      }
-      const float last = readlane(gam, 63);
-      L.gam[lane] = gam;
-      L.beta[lane] = beta;
-      L.eg[lane] = expf(gam);
-      L.dec[lane] = expf(last - gam);
+    for (int off = 1; off < 64; off <<= 1) {
+      const float o = __shfl_up(gam, off, 64);
+      if (lane >= off) gam += o;
     }
-    __syncthreads();
+    const float last = readlane(gam, 63);
+    L.gam[lane] = gam;
+    L.beta[lane] = beta;
+    L.eg[lane] = expf(gam);
+    L.dec[lane] = expf(last - gam);
+    if (lane == 0) scratch[(size_t)gridDim.x * p.num_v_heads * kPrepMats * kMat + (size_t)chunk * p.num_v_heads + h] =
+        expf(last);
+  }
+  __syncthreads();
 
-    // ---- 2: A (strictly lower) and QK (lower), decayed --------------------------------
-    {
-      const int tb = tid >> 4, jb = tid & 15;
-      float aa[4][4], qq[4][4];
+  // ---- A' and QK (4 x 4 register tiles of the lower triangle) ---------------------------
+  {
+    const int tb = tid >> 4, jb = tid & 15;
+    float aa[4][4], qq[4][4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) aa[r][c] = qq[r][c] = 0.0f;
-      if (jb <= tb) {
-        for (int k = 0; k < kDk; k += 4) {
-          float4 kt[4], kj[4], qt[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            kt[r] = *reinterpret_cast<const float4*>(&L.K[tb * 4 + r][k]);
-            qt[r] = *reinterpret_cast<const float4*>(&L.Q[tb * 4 + r][k]);
-            kj[r] = *reinterpret_cast<const float4*>(&L.K[jb * 4 + r][k]);
-          }
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              aa[r][c] += kt[r].x * kj[c].x + kt[r].y * kj[c].y + kt[r].z * kj[c].z + kt[r].w * kj[c].w;
-              qq[r][c] += qt[r].x * kj[c].x + qt[r].y * kj[c].y + qt[r].z * kj[c].z + qt[r].w * kj[c].w;
-            }
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int t = tb * 4 + r, j = jb * 4 + c;
-          const float d = j <= t ? expf(L.gam[t] - L.gam[j]) : 0.0f;
-          L.A[t][j] = j < t ? aa[r][c] * d : 0.0f;
-          L.QK[t][j] = j <= t ? qq[r][c] * d : 0.0f;
-        }
-    }
-    // ---- 3: U = V - e^gamma K S0 (reads K, S; writes U rows this thread owns) ----------
-    {
-      const int t = tid >> 2, c0s = (tid & 3) * 8;
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < 4; ++c) aa[r][c] = qq[r][c] = 0.0f;
+    if (jb <= tb) {
       for (int k = 0; k < kDk; k += 4) {
-        const float4 kv = *reinterpret_cast<const float4*>(&L.K[t][k]);
-        const float kk[4] = {kv.x, kv.y, kv.z, kv.w};
+        float4 kt[4], kj[4], qt[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float4 s0 = *reinterpret_cast<const float4*>(&L.S[k + e][c0s]);
-          const float4 s1 = *reinterpret_cast<const float4*>(&L.S[k + e][c0s + 4]);
-          acc[0] += kk[e] * s0.x; acc[1] += kk[e] * s0.y; acc[2] += kk[e] * s0.z; acc[3] += kk[e] * s0.w;
-          acc[4] += kk[e] * s1.x; acc[5] += kk[e] * s1.y; acc[6] += kk[e] * s1.z; acc[7] += kk[e] * s1.w;
+        for (int r = 0; r < 4; ++r) {
+          kt[r] = *reinterpret_cast<const float4*>(&L.K[tb * 4 + r][k]);
+          qt[r] = *reinterpret_cast<const float4*>(&L.Q[tb * 4 + r][k]);
+          kj[r] = *reinterpret_cast<const float4*>(&L.K[jb * 4 + r][k]);
         }
-      }
-      const float egt = L.eg[t];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) L.U[t][c0s + c] = L.U[t][c0s + c] - egt * acc[c];
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            aa[r][c] += kt[r].x * kj[c].x + kt[r].y * kj[c].y + kt[r].z * kj[c].z + kt[r].w * kj[c].w;
+            qq[r][c] += qt[r].x * kj[c].x + qt[r].y * kj[c].y + qt[r].z * kj[c].z + qt[r].w * kj[c].w;
+          }
+      }
     }
-    __syncthreads();
-
-    // ---- 4: forward substitution; wave w solves value columns 8w .. 8w + 7 ------------
-    {
-      float arow[kCk];
 #pragma unroll
-      for (int j = 0; j < kCk; j += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(&L.A[lane][j]);
-        arow[j] = v.x; arow[j + 1] = v.y; arow[j + 2] = v.z; arow[j + 3] = v.w;
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int t = tb * 4 + r, j = jb * 4 + c;
+        const float d = j <= t ? expf(L.gam[t] - L.gam[j]) : 0.0f;
+        L.A[t][j] = j < t ? L.beta[t] * (aa[r][c] * d) : 0.0f;
+        L.QK[t][j] = j <= t ? qq[r][c] * d : 0.0f;
       }
+  }
+  float* base = scratch + prep_base(chunk, h, p.num_v_heads);
+  // Kd = diag(exp(gamma_C - gamma)) K, before K becomes a right-hand side
+  for (int e = tid; e < kMat; e += 256) base[4 * kMat + e] = L.dec[e / kDk] * L.K[e / kDk][e % kDk];
+  __syncthreads();
+  for (int e = tid; e < kMat; e += 256) {
+    const int t = e / kDk, k = e % kDk;
+    L.V[t][k] *= L.beta[t];
+    L.K[t][k] *= L.beta[t] * L.eg[t];
+  }
+  __syncthreads();
+
+  // ---- forward substitution: X_t = R_t - sum_{j<t} A'[t][j] X_j, in place --------------
+  // wave w solves columns 64 w .. 64 w + 63 of [V | K], eight at a time; lane = token.
+  {
+    float arow[kCk];
+#pragma unroll
+    for (int j = 0; j < kCk; j += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(&L.A[lane][j]);
+      arow[j] = v.x; arow[j + 1] = v.y; arow[j + 2] = v.z; arow[j + 3] = v.w;
+    }
+    float (*M)[kPitch] = wave < 2 ? L.V : L.K;
+    const int cbase = (wave & 1) * 64;
+#pragma unroll 1
+    for (int pass = 0; pass < 8; ++pass) {
+      const int col = cbase + pass * 8;
       float acc[8];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) acc[c] = L.U[lane][wave * 8 + c];
-      const float bl = L.beta[lane];
+      for (int c = 0; c < 8; ++c) acc[c] = M[lane][col + c];
 #pragma unroll
       for (int j = 0; j < kCk; ++j) {
-        const float bj = readlane(bl, j);
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const float dj = readlane(acc[c], j) * bj;  // delta_j: every term of j's sum is in
-          acc[c] = fmaf(-arow[j], dj, acc[c]);        // A[t][j] = 0 for j >= t
-        }
+        for (int c = 0; c < 8; ++c) acc[c] = fmaf(-arow[j], readlane(acc[c], j), acc[c]);
       }
 #pragma unroll
-      for (int c = 0; c < 8; ++c) L.D[lane][wave * 8 + c] = bl * acc[c];
+      for (int c = 0; c < 8; ++c) M[lane][col + c] = acc[c];
+    }
+  }
+  __syncthreads();
+
+  // ---- O_loc = QK Wv and Qx = diag(e^gamma) Q - QK Wk; Wv, Wk out ----------------------
+  {
+    const int t = tid >> 2, cs = (tid & 3) * 32;
+    float o[32], qx[32];
+#pragma unroll
+    for (int c = 0; c < 32; ++c) {
+      o[c] = 0.0f;
+      qx[c] = 0.0f;
+    }
+    for (int j = 0; j <= t; ++j) {
+      const float w = L.QK[t][j];
+#pragma unroll
+      for (int c = 0; c < 32; c += 4) {
+        const float4 wv = *reinterpret_cast<const float4*>(&L.V[j][cs + c]);
+        const float4 wk = *reinterpret_cast<const float4*>(&L.K[j][cs + c]);
+        o[c] += w * wv.x; o[c + 1] += w * wv.y; o[c + 2] += w * wv.z; o[c + 3] += w * wv.w;
+        qx[c] += w * wk.x; qx[c + 1] += w * wk.y; qx[c + 2] += w * wk.z; qx[c + 3] += w * wk.w;
+      }
+    }
+    const float egt = L.eg[t];
+    float* orow = base + (size_t)t * kDk + cs;
+    float* qrow = base + kMat + (size_t)t * kDk + cs;
+#pragma unroll
+    for (int c = 0; c < 32; c += 4) {
+      *reinterpret_cast<float4*>(orow + c) = make_float4(o[c], o[c + 1], o[c + 2], o[c + 3]);
+      *reinterpret_cast<float4*>(qrow + c) =
+          make_float4(egt * L.Q[t][cs + c] - qx[c], egt * L.Q[t][cs + c + 1] - qx[c + 1],
+                      egt * L.Q[t][cs + c + 2] - qx[c + 2], egt * L.Q[t][cs + c + 3] - qx[c + 3]);
+    }
+  }
+  for (int e = tid; e < kMat; e += 256) {
+    base[2 * kMat + e] = L.V[e / kDk][e % kDk];
+    base[3 * kMat + e] = L.K[e / kDk][e % kDk];
+  }
+}
+
+// The scan: one workgroup per (value head, 16 value columns), the state slice in LDS, the
+// chunks in order. Per chunk: O = O_loc + Qx S0 (tokens out as bf16), delta = Wv - Wk S0,
+// S = e^gamma_C S0 + Kd^T delta.
+constexpr int kScanVs = 16;
+
+struct ScanLds {
+  float S[kDk][kScanVs];
+  float Qx[kCk][kPitch];
+  float Wk[kCk][kPitch];
+  float Kd[kCk][kPitch];
+  float D[kCk][kScanVs + 1];
+};
+
+__global__ __launch_bounds__(256) void delta_scan_kernel(DfDeltaPrefillArgs p, const float* __restrict__ scratch) {
+  __shared__ __align__(16) ScanLds L;
+  const int tid = threadIdx.x;
+  const int h = blockIdx.x, vs = blockIdx.y;
+  const int col0 = vs * kScanVs;
+  const int nchunks = (p.tokens + kCk - 1) / kCk;
+  float* gstate = p.state + (size_t)h * kDk * kDk;
+  for (int e = tid; e < kDk * kScanVs; e += 256)
+    L.S[e / kScanVs][e % kScanVs] = gstate[(size_t)(e / kScanVs) * kDk + col0 + e % kScanVs];
+  const float* ecs = scratch + (size_t)nchunks * p.num_v_heads * kPrepMats * kMat;
+  for (int chunk = 0; chunk < nchunks; ++chunk) {
+    const float* base = scratch + prep_base(chunk, h, p.num_v_heads);
+    for (int e = tid; e < kMat / 4; e += 256) {  // Qx, Wk, Kd rows into LDS
+      const int t = (e * 4) / kDk, k = (e * 4) % kDk;
+      *reinterpret_cast<float4*>(&L.Qx[t][k]) = *reinterpret_cast<const float4*>(base + kMat + e * 4);
+      *reinterpret_cast<float4*>(&L.Wk[t][k]) = *reinterpret_cast<const float4*>(base + 3 * kMat + e * 4);
+      *reinterpret_cast<float4*>(&L.Kd[t][k]) = *reinterpret_cast<const float4*>(base + 4 * kMat + e * 4);
     }
     __syncthreads();
-
-    // ---- 5: O = e^gamma Q S0 + QK delta ----------------------------------------------
-    {
-      const int t = tid >> 2, c0s = (tid & 3) * 8;
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    {  // O and delta: token t, columns cq .. cq + 3 of the slice
+      const int t = tid >> 2, cq = (tid & 3) * 4;
+      const float4 ol = *reinterpret_cast<const float4*>(base + (size_t)t * kDk + col0 + cq);
+      const float4 wv = *reinterpret_cast<const float4*>(base + 2 * kMat + (size_t)t * kDk + col0 + cq);
+      float o[4] = {ol.x, ol.y, ol.z, ol.w}, d[4] = {wv.x, wv.y, wv.z, wv.w};
       for (int k = 0; k < kDk; k += 4) {
-        const float4 qv = *reinterpret_cast<const float4*>(&L.Q[t][k]);
-        const float qk[4] = {qv.x, qv.y, qv.z, qv.w};
+        const float4 qv = *reinterpret_cast<const float4*>(&L.Qx[t][k]);
+        const float4 kv = *reinterpret_cast<const float4*>(&L.Wk[t][k]);
+        const float qq[4] = {qv.x, qv.y, qv.z, qv.w}, ww[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float4 s0 = *reinterpret_cast<const float4*>(&L.S[k + e][c0s]);
-          const float4 s1 = *reinterpret_cast<const float4*>(&L.S[k + e][c0s + 4]);
-          acc[0] += qk[e] * s0.x; acc[1] += qk[e] * s0.y; acc[2] += qk[e] * s0.z; acc[3] += qk[e] * s0.w;
-          acc[4] += qk[e] * s1.x; acc[5] += qk[e] * s1.y; acc[6] += qk[e] * s1.z; acc[7] += qk[e] * s1.w;
+          const float4 sv = *reinterpret_cast<const float4*>(&L.S[k + e][cq]);
+          o[0] += qq[e] * sv.x; o[1] += qq[e] * sv.y; o[2] += qq[e] * sv.z; o[3] += qq[e] * sv.w;
+          d[0] -= ww[e] * sv.x; d[1] -= ww[e] * sv.y; d[2] -= ww[e] * sv.z; d[3] -= ww[e] * sv.w;
         }
       }
-      const float egt = L.eg[t];
-      float o[8];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) o[c] = egt * acc[c];
-      for (int j = 0; j <= t; ++j) {
-        const float w = L.QK[t][j];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) o[c] += w * L.D[j][c0s + c];
-      }
-      if (c0 + t < p.tokens) {
-        uint32_t packed[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          packed[c] = static_cast<uint32_t>(f2bf(o[2 * c])) | (static_cast<uint32_t>(f2bf(o[2 * c + 1])) << 16);
-        *reinterpret_cast<uint4*>(p.out + (size_t)(c0 + t) * p.ld_out + h * kDk + vs * kVs + c0s) =
-            make_uint4(packed[0], packed[1], packed[2], packed[3]);
+      for (int c = 0; c < 4; ++c) L.D[t][cq + c] = d[c];
+      const int T = chunk * kCk + t;
+      if (T < p.tokens) {
+        *reinterpret_cast<uint2*>(p.out + (size_t)T * p.ld_out + h * kDk + col0 + cq) =
+            make_uint2(static_cast<uint32_t>(f2bf(o[0])) | (static_cast<uint32_t>(f2bf(o[1])) << 16),
+                       static_cast<uint32_t>(f2bf(o[2])) | (static_cast<uint32_t>(f2bf(o[3])) << 16));
       }
     }
     __syncthreads();
-
-    // ---- 6: S <- e^gamma_C S0 + sum_j e^(gamma_C - gamma_j) k_j delta_j^T ------------
-    {
-      const int k = tid >> 1, cs = (tid & 1) * 16;
-      float acc[16];
+    {  // S <- e^gamma_C S0 + Kd^T delta: row k, columns c8 .. c8 + 7
+      const int k = tid >> 1, c8 = (tid & 1) * 8;
+      const float ec = ecs[(size_t)chunk * p.num_v_heads + h];
+      float acc[8];
 #pragma unroll
-      for (int c = 0; c < 16; ++c) acc[c] = 0.0f;
+      for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
       for (int j = 0; j < kCk; ++j) {
-        const float kd = L.K[j][k] * L.dec[j];
+        const float kd = L.Kd[j][k];
 #pragma unroll
-        for (int c = 0; c < 16; ++c) acc[c] += kd * L.D[j][cs + c];
+        for (int c = 0; c < 8; ++c) acc[c] += kd * L.D[j][c8 + c];
       }
-      const float egl = L.eg[kCk - 1];
 #pragma unroll
-      for (int c = 0; c < 16; ++c) L.S[k][cs + c] = egl * L.S[k][cs + c] + acc[c];
+      for (int c = 0; c < 8; ++c) L.S[k][c8 + c] = ec * L.S[k][c8 + c] + acc[c];
     }
     __syncthreads();
   }
-  for (int e = tid; e < kDk * kVs; e += 256) gstate[(size_t)(e / kVs) * kDk + vs * kVs + e % kVs] = L.S[e / kVs][e % kVs];
+  for (int e = tid; e < kDk * kScanVs; e += 256)
+    gstate[(size_t)(e / kScanVs) * kDk + col0 + e % kScanVs] = L.S[e / kScanVs][e % kScanVs];
 }
 
 // ---------------------------------------------------------------------------------------
@@ -707,15 +763,29 @@ int df_causal_conv_prefill(const uint16_t* x, int ldx, int tokens, int channels,
   DF_RETURN_LAUNCH_STATUS();
 }
 
-int df_delta_rule_prefill(const DfDeltaPrefillArgs* a, hipStream_t stream) {
+size_t df_delta_rule_prefill_workspace_bytes(int tokens, int num_v_heads) {
+  if (tokens < 1 || num_v_heads < 1) return 0;
+  const size_t chunks = (size_t)(tokens + kCk - 1) / kCk;
+  return (chunks * num_v_heads * (kPrepMats * (size_t)kMat + 1)) * sizeof(float);
+}
+
+int df_delta_rule_prefill(const DfDeltaPrefillArgs* a, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (!a || !a->mixed || !a->a || !a->b || !a->A_log || !a->dt_bias || !a->state || !a->out || a->tokens < 1)
     return DF_BAD_ARGUMENT;
   if (a->num_k_heads < 1 || a->num_v_heads < 1 || a->num_v_heads % a->num_k_heads) return DF_BAD_ARGUMENT;
   const int channels = 2 * a->num_k_heads * kDk + a->num_v_heads * kDk;
-  if (a->ld_mixed < channels || a->ld_mixed % 2 || a->ld_out < a->num_v_heads * kDk || a->ld_out % 8 ||
-      a->ld_ab < a->num_v_heads || (reinterpret_cast<uintptr_t>(a->mixed) & 3) || !aligned16(a->out))
+  if (a->ld_mixed < channels || a->ld_mixed % 2 || a->ld_out < a->num_v_heads * kDk || a->ld_out % 4 ||
+      a->ld_ab < a->num_v_heads || (reinterpret_cast<uintptr_t>(a->mixed) & 3) ||
+      (reinterpret_cast<uintptr_t>(a->out) & 7) || (reinterpret_cast<uintptr_t>(a->state) & 15))
     return DF_BAD_ARGUMENT;
-  hipLaunchKernelGGL(delta_chunked_kernel, dim3(a->num_v_heads, kDk / kVs), dim3(256), 0, stream, *a);
+  if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 15) ||
+      workspace_bytes < df_delta_rule_prefill_workspace_bytes(a->tokens, a->num_v_heads))
+    return DF_WORKSPACE_TOO_SMALL;
+  const int chunks = (a->tokens + kCk - 1) / kCk;
+  float* scratch = reinterpret_cast<float*>(workspace);
+  hipLaunchKernelGGL(delta_prep_kernel, dim3(chunks, a->num_v_heads), dim3(256), 0, stream, *a, scratch);
+  hipLaunchKernelGGL(delta_scan_kernel, dim3(a->num_v_heads, kDk / kScanVs), dim3(256), 0, stream, *a,
+                     static_cast<const float*>(scratch));
   DF_RETURN_LAUNCH_STATUS();
 }
 

@@ -119,11 +119,13 @@ def delta_rule_prefill(mixed: Tensor, a: Tensor, b: Tensor, A_log: Tensor, dt_bi
     if out is None:
         out = torch.empty((tokens, hv * 128), dtype=BF16, device=mixed.device)
     ops.require_gpus(op, mixed, a, b, A_log, dt_bias, state, out)
+    nbytes = int(N.lib().df_delta_rule_prefill_workspace_bytes(tokens, hv))
+    ws = ops.workspace(mixed.device, nbytes, "delta_prefill")
     args = N.DeltaPrefillArgs(mixed=mixed.data_ptr(), a=a.data_ptr(), b=b.data_ptr(), A_log=A_log.data_ptr(),
                               dt_bias=dt_bias.data_ptr(), state=state.data_ptr(), out=out.data_ptr(),
                               ld_mixed=_row_view(mixed, "mixed"), ld_ab=ld_ab, ld_out=_row_view(out, "out"),
                               tokens=tokens, num_k_heads=num_k_heads, num_v_heads=hv)
-    N.check(N.lib().df_delta_rule_prefill(C.byref(args), ops._stream(mixed)), op)
+    N.check(N.lib().df_delta_rule_prefill(C.byref(args), ws.data_ptr(), ws.numel(), ops._stream(mixed)), op)
     return out
 
 

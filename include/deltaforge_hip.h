@@ -280,7 +280,11 @@ typedef struct DfDeltaPrefillArgs {
   int ld_mixed, ld_ab, ld_out;
   int tokens, num_k_heads, num_v_heads;
 } DfDeltaPrefillArgs;
-int df_delta_rule_prefill(const DfDeltaPrefillArgs* args, hipStream_t stream);
+/* Workspace (bytes) for `tokens` tokens and Hv value heads: per (64-token chunk, head), the
+ * five 64 x 128 fp32 state-independent products of the chunk and its total decay. */
+size_t df_delta_rule_prefill_workspace_bytes(int tokens, int num_v_heads);
+int df_delta_rule_prefill(const DfDeltaPrefillArgs* args, void* workspace, size_t workspace_bytes,
+                          hipStream_t stream);
 
 /* GatedRMSNorm over rows (reference.py:115-121): per 128-wide head of x,
  * out = bf16(bf16(w * bf16(x rsqrt(mean x^2 + eps))) * silu(z)). */
