@@ -14,6 +14,7 @@
 
 #include "common.h"
 #include "deltaforge_hip.h"
+#include "int4_block.h"
 
 namespace df {
 namespace pf {
@@ -37,26 +38,12 @@ DF_DEVICE float readlane(float v, int lane) {
 // 4 (e / 2), plus 16 when e is odd. That is exactly the B operand of
 // v_mfma_f32_16x16x32_bf16 number i, whose A operand is then x[row][32 (L / 16) + 8 i ..+8].
 // A workgroup computes a 128 x 128 tile. Its four waves each own 64 rows x 64 columns (4 x 4
-// products). Per 128-group, the x rows and the dequantised weights are staged in LDS.
+// products). Per 128-group, the x rows and the dequantised weights are staged in LDS; the
+// dequant is int4_block.h's exact one (19 VALU per 8 weights).
 
 constexpr int kGmBM = 128;
 constexpr int kGmTiles = 8;           // 16-column tiles per workgroup (128 columns)
 constexpr int kGmXPitch = 128 + 8;    // bf16 per staged x row (16-byte pad)
-
-// Word `w` of a tiled block with its column scale -> bf16((n - 8) * s) for its 8 values, in
-// k order (the product (n - 8) * s is exact in fp32; the bf16 rounding is the reference's).
-DF_DEVICE uint4 dequant8(uint32_t w, float s) {
-  w ^= 0x88888888u;  // each nibble n becomes n - 8 as a signed 4-bit field
-  uint32_t o[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int q0 = static_cast<int>(w << (28 - 4 * j)) >> 28;  // element 2j: bits 4j ..
-    const int q1 = static_cast<int>(w << (12 - 4 * j)) >> 28;  // element 2j+1: bits 16 + 4j ..
-    o[j] = static_cast<uint32_t>(f2bf(static_cast<float>(q0) * s)) |
-           (static_cast<uint32_t>(f2bf(static_cast<float>(q1) * s)) << 16);
-  }
-  return make_uint4(o[0], o[1], o[2], o[3]);
-}
 
 template <int EPI>
 __global__ __launch_bounds__(256, 2) void int4_gemm_kernel(DfInt4GemmArgs p) {
@@ -72,30 +59,48 @@ __global__ __launch_bounds__(256, 2) void int4_gemm_kernel(DfInt4GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[rb][j] = df_f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int g = 0; g < G; ++g) {
+  // Group g + 1's x chunks and weight words are loaded into registers while group g's
+  // products run; the stores into LDS (and the dequant) follow the barrier that ends them.
+  uint4 xr[8], wr8[2];
+  uint16_t sr[2];
+  auto load_group = [&](int g) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {  // x: 128 rows x 16 chunks of 16 bytes
       const int ch = tid + 256 * i, r = ch >> 4, cc = ch & 15;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (m0 + r < p.M) v = *reinterpret_cast<const uint4*>(p.x + (size_t)(m0 + r) * p.ldx + g * 128 + cc * 8);
-      *reinterpret_cast<uint4*>(&xs[r * kGmXPitch + cc * 8]) = v;
+      xr[i] = m0 + r < p.M ? *reinterpret_cast<const uint4*>(p.x + (size_t)(m0 + r) * p.ldx + g * 128 + cc * 8)
+                           : make_uint4(0u, 0u, 0u, 0u);
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {  // weights: 8 blocks x 64 lanes' 16 bytes
+    for (int i = 0; i < 2; ++i) {  // weights: 8 blocks x 64 lanes' 16 bytes (zeros past N)
       const int u = tid + 256 * i, j = u >> 6, L = u & 63;
-      uint4 wv = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);  // zeros past N
-      float sc = 0.0f;
+      wr8[i] = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
+      sr[i] = 0;
       if (t0 + j < ntiles) {
         const size_t blk = (size_t)(t0 + j) * G + g;
-        wv = *reinterpret_cast<const uint4*>(p.w + blk * 1024 + L * 16);
-        sc = bf2f(p.s[blk * 16 + (L & 15)]);
+        wr8[i] = *reinterpret_cast<const uint4*>(p.w + blk * 1024 + L * 16);
+        sr[i] = p.s[blk * 16 + (L & 15)];
       }
-      ws[(j * 4 + 0) * 64 + L] = dequant8(wv.x, sc);
-      ws[(j * 4 + 1) * 64 + L] = dequant8(wv.y, sc);
-      ws[(j * 4 + 2) * 64 + L] = dequant8(wv.z, sc);
-      ws[(j * 4 + 3) * 64 + L] = dequant8(wv.w, sc);
+    }
+  };
+  load_group(0);
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int ch = tid + 256 * i, r = ch >> 4, cc = ch & 15;
+      *reinterpret_cast<uint4*>(&xs[r * kGmXPitch + cc * 8]) = xr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int u = tid + 256 * i, j = u >> 6, L = u & 63;
+      // the exact bf16((n - 8) * scale) of the per-op GEMV (int4_block.h)
+      const GroupScale gs = group_scale(sr[i]);
+      ws[(j * 4 + 0) * 64 + L] = dequant8(wr8[i].x, gs);
+      ws[(j * 4 + 1) * 64 + L] = dequant8(wr8[i].y, gs);
+      ws[(j * 4 + 2) * 64 + L] = dequant8(wr8[i].z, gs);
+      ws[(j * 4 + 3) * 64 + L] = dequant8(wr8[i].w, gs);
     }
     __syncthreads();
+    if (g + 1 < G) load_group(g + 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint4 a[4], b[4];
