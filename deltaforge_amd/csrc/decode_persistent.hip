@@ -1804,6 +1804,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
 }
 
 // The control wave's whole launch.
+template <bool TABLE>
 DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int steps, int teacher_forced, Lds& L) {
   const int hidden = M.hidden;
   const int G = q.Gh;
@@ -1829,7 +1830,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       if (c.lane == 0 && c.xcd == 0 && c.r == 0) raise_abort(c, kErrToken);
       return fail(1);
     }
-    if (M.embed_table) {
+    if constexpr (TABLE) {
       // the checkpoint's bf16 row, 16 bytes per lane per chunk, and its sum of squares (the
       // same order in every workgroup)
       const auto rt = rsrc(M.embed_table + (size_t)token * hidden);
@@ -2141,6 +2142,10 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
   }
 }
 
+// TABLE: embed from the checkpoint's bf16 table (M.embed_table) instead of the tied int4
+// head. Two instances, so the tied build carries no code for the other path (the decode is
+// sensitive to the kernel's code layout).
+template <bool TABLE>
 __global__ __launch_bounds__(kThreads) void decode_kernel(DfPersistModel M, Ws w, int steps, int teacher_forced) {
   __shared__ Lds L;
   Ctx c;
@@ -2203,7 +2208,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DfPersistModel M, Ws w
   q.t_hi = c.xcd * vocab_tiles + ((c.r + 1) * vocab_tiles) / kPerXcd;
   __syncthreads();  // everyone has read the registration before L.token is reused
 
-  if (c.control) control_main(M, q, c, steps, teacher_forced, L);
+  if (c.control) control_main<TABLE>(M, q, c, steps, teacher_forced, L);
   else compute_main(M, q, c, steps, L);
 }
 
@@ -2260,6 +2265,8 @@ extern "C" int df_decode_persistent(const DfPersistModel* model, int steps, int 
   ws_layout(m.hidden, &w, reinterpret_cast<char*>(workspace));
   hipLaunchKernelGGL(register_reset_kernel, dim3(1), dim3(64), 0, stream, w.ctl);
   if (hipGetLastError() != hipSuccess) return DF_LAUNCH_FAILED;
+  const void* kernel =
+      m.embed_table ? reinterpret_cast<const void*>(decode_kernel<true>) : reinterpret_cast<const void*>(decode_kernel<false>);
   if (plain_launch()) {
     // an ordinary dispatch of the same grid: co-residency is checked here instead of by the
     // cooperative launch (one workgroup per CU, every CU of the device), and a workgroup that
@@ -2267,15 +2274,16 @@ extern "C" int df_decode_persistent(const DfPersistModel* model, int steps, int 
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(decode_kernel), kThreads,
-                                                     0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0) != hipSuccess ||
         cus * per_cu < kNwg)
       return DF_LAUNCH_FAILED;
-    hipLaunchKernelGGL(decode_kernel, dim3(kNwg), dim3(kThreads), 0, stream, m, w, steps, teacher_forced);
+    if (m.embed_table)
+      hipLaunchKernelGGL(decode_kernel<true>, dim3(kNwg), dim3(kThreads), 0, stream, m, w, steps, teacher_forced);
+    else
+      hipLaunchKernelGGL(decode_kernel<false>, dim3(kNwg), dim3(kThreads), 0, stream, m, w, steps, teacher_forced);
     return hipGetLastError() == hipSuccess ? DF_OK : DF_LAUNCH_FAILED;
   }
   void* args[] = {&m, &w, &steps, &teacher_forced};
-  const hipError_t e =
-      hipLaunchCooperativeKernel(reinterpret_cast<const void*>(decode_kernel), dim3(kNwg), dim3(kThreads), args, 0, stream);
+  const hipError_t e = hipLaunchCooperativeKernel(kernel, dim3(kNwg), dim3(kThreads), args, 0, stream);
   return e == hipSuccess ? DF_OK : DF_LAUNCH_FAILED;
 }
