@@ -44,6 +44,7 @@
 #include "deltaforge_hip.h"
 #include "int4_block.h"
 
+#include <algorithm>
 #include <cstdlib>
 
 namespace df {
@@ -77,6 +78,9 @@ constexpr int kAttnCols = 1536;
 constexpr int kAttnK = 1024;
 constexpr int kApHead = kHd + 2;                    // acc[256], m, l
 constexpr int kTileKeys = kCompute * 16;            // 128 keys per attention tile
+constexpr int kSplits = 2 * kPerXcd;                // key splits of a KV head over its XCD pair
+constexpr int kPairHeads = 4;                       // query heads of a KV head (2 per XCD of the pair);
+                                                    // an XCD's own two are its slots 0, 1
 // factored int4 dot product: B = bf16(128 + n), n - 8 = B - 136
 constexpr uint32_t kBiasPair = 0x43004300u;         // bf16 128.0 in both halves
 constexpr float kBias = 136.0f;
@@ -93,7 +97,8 @@ struct Ws {
   float* cpgu;       // [8][2][kColparMax] gate|up partial outputs, 2 slots (flag hand-off)
   uint16_t* hloc;    // [8][hidden] the hidden vector, one copy per XCD (flag hand-off)
   uint32_t* core;    // [8][512] DeltaNet core / merged attention output of the XCD, (bf16 | epoch << 16)
-  float* apart;      // [8][32 splits][2 heads][kApHead]
+  float* apart;      // split partials: [8][32 splits][2 heads][kApHead] fp32, or in the PAIR
+                     // instance [4 XCD pairs][64 records][4 head slots][kApHead] (fp32, u32 epoch)
   uint64_t* rowpar;  // [2][8][hidden] (fp32 value, u32 epoch) row-parallel partials
   uint64_t* cand;    // [256] argmax candidates (value, index, epoch bits)
 };
@@ -113,7 +118,8 @@ __host__ __device__ inline size_t ws_layout(int hidden, Ws* w, char* base) {
   char* cpgu = take((size_t)kXcd * 2 * kColparMax * sizeof(float));
   char* hloc = take((size_t)kXcd * hidden * sizeof(uint16_t));
   char* core = take((size_t)kXcd * 512 * sizeof(uint32_t));
-  char* apart = take((size_t)kXcd * kPerXcd * 2 * kApHead * sizeof(float));
+  char* apart = take(std::max((size_t)kXcd * kPerXcd * 2 * kApHead * sizeof(float),
+                               (size_t)(kXcd / 2) * kSplits * kPairHeads * kApHead * sizeof(uint64_t)));
   char* rowpar = take((size_t)2 * kXcd * hidden * sizeof(uint64_t));
   char* cand = take((size_t)kNwg * sizeof(uint64_t));
   if (w) {
@@ -280,6 +286,29 @@ struct Lds {
       float acc[kPerXcd][16];
       float gate[16];
     } mg;
+    struct {                                     // attention split, keys split over the XCD
+                                                 // pair: the KV head's 4 query heads (the
+                                                 // decode_kernel<., true> instance)
+      __align__(16) uint16_t q[kPairHeads][kHd];
+      __align__(16) uint16_t knew[kHd];
+      __align__(16) uint16_t vnew[kHd];
+      float qraw[kPairHeads][kHd];
+      float kraw[kHd];                           // kraw and vraw adjacent: one staged segment
+      float vraw[kHd];
+      __align__(16) uint16_t qn_w[kHd];
+      __align__(16) uint16_t kn_w[kHd];
+      float inv[kRot / 2];
+      float sc[kPairHeads][kTileKeys];
+      float alpha[kPairHeads];
+      float ml[kPairHeads][2];
+      __align__(16) float red[kPairHeads][kHd];  // the split's PV sums (the per-wave partials
+                                                 // are summed from the drained weight ring)
+    } at4;
+    struct {                                     // its split merge (control wave)
+      float wgt[kSplits];
+      __align__(16) float acc[kSplits][16];
+      float gate[16];
+    } mg4;
     struct {                                     // down: the XCD's gate|up column sums
       __align__(16) float gu[kColparMax];
     } ac;
@@ -542,12 +571,19 @@ DF_DEVICE int head_tiles_of_wave(const Geo& q, int wave) {
 // built once per launch in LDS. The same list serves every token of the launch.
 //
 // Run descriptor: w = weights of the first block | (blocks << 48), s = its scales | hold << 63
-// (hold: the first run of an attention layer's o_proj; the stream stops there until the
-// layer's KV-cache loads are consumed, because they share the wave's in-order vmcnt).
+// (hold: the stream stops before this run until the attention layer's KV-cache loads are
+// consumed, because they share the wave's in-order vmcnt). With the keys split per XCD the
+// hold is the first run after an attention layer's input projection (o_proj's). With the keys
+// split over the XCD pair it is a zero-block marker run of its own right after the input
+// projection: the split's PV partials then borrow the ring, which must be drained there for
+// every wave, and a flag carried by the next real run would leave a wave with no blocks
+// between two attention layers' input projections with its ring full at the second.
 struct RunDesc {
   uint64_t w, s;
 };
-constexpr int kMaxRuns = 200;  // per wave and token: 6 per layer (<= 2 per row-parallel phase) + the head's tiles
+// per wave and token: 6 per layer (<= 2 per row-parallel phase), a marker per attention layer
+// and the head's tiles
+constexpr int kMaxRuns = 232;
 constexpr uint64_t kPtrMask = (1ull << 48) - 1;
 __shared__ __align__(16) RunDesc g_runs[kCompute][kMaxRuns];
 
@@ -558,7 +594,7 @@ struct Stream {
   int ri, nruns;         // next run to open, runs per token
   int issued, consumed;  // blocks, since the launch began
   int wslot, rslot;      // ring slots of the next issue / the next consume
-  int state;             // 0 streaming, 1 held before an attention layer's o_proj,
+  int state;             // 0 streaming, 1 held after an attention layer's input projection,
                          // 2 released, 3 past the launch's last block
   int istep;             // token of the cursor
 };
@@ -567,6 +603,7 @@ enum StreamState : int { kStreaming = 0, kHeld = 1, kReleased = 2, kDone = 3 };
 
 // Compute waves, once per launch: this wave's run list (lane 0 writes it; the wave's LDS
 // accesses complete in order, so its own later reads see it). Returns the runs per token.
+template <bool PAIR>
 DF_DEVICE int build_runs(const DfPersistModel& M, const Geo& q, const Ctx& c) {
   int n = 0;
   auto put = [&](const uint8_t* w, const uint16_t* sc, int blocks, bool hold) {
@@ -582,7 +619,7 @@ DF_DEVICE int build_runs(const DfPersistModel& M, const Geo& q, const Ctx& c) {
       const Gemv g = gemv_of(&g_layers[li], q, k, c.xcd, c.r);
       int lo, cnt;
       wave_range(g, c.wave, lo, cnt);
-      hold = hold || (kind == 1 && k == 1);
+      if constexpr (!PAIR) hold = hold || (kind == 1 && k == 1);
       // blocks lo .. lo + cnt of the slice (tile-major, ng groups per tile): a tile's run is
       // contiguous, and so are consecutive tiles when the slice spans every group
       while (cnt > 0) {
@@ -593,6 +630,9 @@ DF_DEVICE int build_runs(const DfPersistModel& M, const Geo& q, const Ctx& c) {
         hold = false;
         lo += len;
         cnt -= len;
+      }
+      if constexpr (PAIR) {
+        if (kind == 1 && k == 0) put(nullptr, nullptr, 0, true);
       }
     }
   }
@@ -605,7 +645,9 @@ DF_DEVICE int build_runs(const DfPersistModel& M, const Geo& q, const Ctx& c) {
   // Every geometry the launcher accepts fits: per layer at most 1 run each for the
   // column-parallel phases and 2 for each row-parallel one (a wave's share of out_proj /
   // o_proj is at most 3 blocks of 4-group runs, of down at most 5/8 of a run of ngx blocks),
-  // and at most 8 head tiles per wave (64 per workgroup), so 6 x 32 + 8 = kMaxRuns.
+  // a marker per attention layer, and at most 8 head tiles per wave (64 per workgroup), so
+  // 7 x 32 + 8 = kMaxRuns.
+  static_assert(kMaxRuns == 7 * kMaxLayers + 8, "run list capacity");
   return min(n, kMaxRuns);
 }
 
@@ -928,6 +970,11 @@ template <int CP>
 DF_DEVICE uint64_t ld8(__amdgpu_buffer_rsrc_t r, int byte_off) {
   return __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, CP));
 }
+// 16-byte store; with kCpSystem it writes through (sc0 sc1), like st_sys.
+template <int CP>
+DF_DEVICE void st16(__amdgpu_buffer_rsrc_t r, int byte_off, uint4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(df_i4, v), r, byte_off, 0, CP);
+}
 
 // n bf16 (n % 8 == 0, n <= 512 K) from global memory into LDS.
 template <int K, int CP>
@@ -1017,6 +1064,57 @@ DF_DEVICE bool gather_colpar(const Ctx& c, const Seg (&seg)[NS], uint32_t want) 
   return true;
 }
 
+// Control wave: an attention layer's inputs, polled together, as bf16-rounded slot sums: this
+// XCD's two query heads (columns 0 and 512) into slots 0, 1, its k | v columns (1024 ..1535)
+// and, when the keys are split over the pair, the other XCD's two query heads into slots 2, 3
+// (that XCD wrote them through to memory; read at system scope).
+DF_DEVICE bool gather_attn(const Ctx& c, float (*qraw)[kHd], float* kvraw, uint32_t want, bool pair) {
+  const auto rl = rsrc(c.w.colpar + (size_t)c.xcd * 2 * kColparMax);
+  const auto rp = rsrc(c.w.colpar + (size_t)(c.xcd ^ 1) * 2 * kColparMax);
+  // chunk k of a lane: 2 columns at col(k); partner chunks 0..3, own chunks 0..7
+  auto pcol = [&](int k) { return (k < 2 ? 0 : 512) + 2 * (c.lane + 64 * (k & 1)); };
+  auto lcol = [&](int k) { return (k < 2 ? 0 : k < 4 ? 512 : 1024) + 2 * (c.lane + 64 * (k < 4 ? (k & 1) : k - 4)); };
+  uint4 pa[4], pb[4], la[8], lb[8];
+  const bool ok = poll_tagged(c, [&]() {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (pair) {
+        pa[k] = ld16<kCpSystem>(rp, pcol(k) * 8);
+        pb[k] = ld16<kCpSystem>(rp, (kColparMax + pcol(k)) * 8);
+      } else {  // not used
+        pa[k] = pb[k] = make_uint4(0u, want, 0u, want);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      la[k] = ld16<kCpAgent>(rl, lcol(k) * 8);
+      lb[k] = ld16<kCpAgent>(rl, (kColparMax + lcol(k)) * 8);
+    }
+    bool t = true;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) t = t && pairs_ok(pa[k], want) && pairs_ok(pb[k], want);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) t = t && pairs_ok(la[k], want) && pairs_ok(lb[k], want);
+    return t;
+  });
+  if (!ok) return false;
+  if (pair) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float* d = qraw[2 + (k >> 1)] + 2 * (c.lane + 64 * (k & 1));
+      d[0] = round_bf(__uint_as_float(pa[k].x) + __uint_as_float(pb[k].x));
+      d[1] = round_bf(__uint_as_float(pa[k].z) + __uint_as_float(pb[k].z));
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    float* d = k < 4 ? qraw[k >> 1] + 2 * (c.lane + 64 * (k & 1)) : kvraw + 2 * (c.lane + 64 * (k - 4));
+    d[0] = round_bf(__uint_as_float(la[k].x) + __uint_as_float(lb[k].x));
+    d[1] = round_bf(__uint_as_float(la[k].z) + __uint_as_float(lb[k].z));
+  }
+  return true;
+}
+
 // Control wave, after the flag hand-off: the XCD's 2 inter_x gate|up columns as (unrounded)
 // sums of the two column-parallel slots, into gu. This hand-off keeps flags and untagged
 // fp32: polling its data tagged would mean twice the bytes (37 KB per workgroup), more than
@@ -1100,7 +1198,7 @@ DF_DEVICE bool stage_core(Lds& L, const Ctx& c, uint32_t want, bool sums) {
 // into its slot (r & 1); tiles wholly inside its range also zero the other slot.
 // TAGGED: the input projection's (fp32, epoch) pairs; else gate|up's plain fp32.
 template <bool TAGGED>
-DF_DEVICE void colpar_epilogue(const Gemv& g, const Ctx& c, const Lds& L) {
+DF_DEVICE void colpar_epilogue(const Gemv& g, const Ctx& c, const Lds& L, bool through = false) {
   const int t_first = g.b_lo / g.ng, t_last = (g.b_hi - 1) / g.ng;
   const int nt = t_last - t_first + 1;
   uint64_t* cp = c.w.colpar + (size_t)c.xcd * 2 * kColparMax;
@@ -1112,7 +1210,10 @@ DF_DEVICE void colpar_epilogue(const Gemv& g, const Ctx& c, const Lds& L) {
     const float v = part_sum(L, tr, col);
     const int j = t * 16 + col;
     const bool whole = t * g.ng >= g.b_lo && (t + 1) * g.ng <= g.b_hi;
-    if (TAGGED) {
+    if (TAGGED && through && ((j >> 8) & 1) == 0 && j < kAttnK) {  // query columns: read by the pair's other XCD too
+      st_sys(&cp[mine * kColparMax + j], pack_epoch(v, c.epoch));
+      if (whole) st_sys(&cp[(mine ^ 1) * kColparMax + j], pack_epoch(0.0f, c.epoch));
+    } else if (TAGGED) {
       cp[mine * kColparMax + j] = pack_epoch(v, c.epoch);
       if (whole) cp[(mine ^ 1) * kColparMax + j] = pack_epoch(0.0f, c.epoch);
     } else {
@@ -1551,6 +1652,130 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, floa
   sync(c);
 }
 
+// Two ways to split the keys of KV head x / 2, chosen per step from the context length:
+// - per XCD: each XCD of the pair splits all keys over its 32 workgroups for its own two
+//   query heads (both XCDs stream every key);
+// - over the pair: the 64 workgroups of XCDs x & ~1 and x | 1 split the keys once, each
+//   split serving all four query heads, so every key and value row leaves HBM once per layer.
+//   It costs two cross-XCD hand-offs (the partner's queries, the merge over 64 splits), about
+//   one 128-key tile of time, so it is used when it saves at least two tiles per workgroup.
+__host__ __device__ inline bool at_pair(int nkeys) {
+  const int t32 = (nkeys + kPerXcd * kTileKeys - 1) / (kPerXcd * kTileKeys);
+  const int t64 = (nkeys + kSplits * kTileKeys - 1) / (kSplits * kTileKeys);
+  return t32 - t64 >= 2;
+}
+// Split of this workgroup: keys [j0, j1). Its record index in the pair's partials is
+// (x & 1) * 32 + r in both modes.
+DF_DEVICE void at_keys4(const Ctx& c, int& j0, int& j1) {
+  const int nkeys = c.pos + 1;
+  const bool pair = at_pair(nkeys);
+  const int nsplit = pair ? kSplits : kPerXcd;
+  const int per = (nkeys + nsplit - 1) / nsplit;
+  const int split = pair ? (c.xcd & 1) * kPerXcd + c.r : c.r;
+  j0 = min(split * per, nkeys);
+  j1 = min(j0 + per, nkeys);
+}
+
+// Compute waves (kTileBars barriers): one 128-key tile for nh query heads (2: this XCD's, 4:
+// the KV head's, split over the pair): QK (MFMA, row h = head slot h), then the V rows are
+// loaded while the online softmax runs (wave h for head h), then PV.
+DF_DEVICE void at_tile4(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, float acc[kPairHeads][4], int nh,
+                        Lds& L) {
+  auto& A = L.u.at4;
+  const int col = c.lane & 15, slot = c.lane >> 4;
+  const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
+  // the tile's K loads are the only vector loads in flight (the weight stream is held):
+  // waiting for all of them here also tells the compiler that none is pending afterwards
+  wait_vm<0>();
+  {
+    const int key = t0 + c.wave * 16 + col;
+    const bool live = key < j1;
+    df_f32x4 d4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      uint4 kn = *reinterpret_cast<const uint4*>(A.knew + d * 32 + slot * 8);
+      asm volatile("" : "+v"(kn.x), "+v"(kn.y), "+v"(kn.z), "+v"(kn.w));  // a value, not a pointer select into P
+      uint4 bw = make_uint4(0u, 0u, 0u, 0u);
+      if (live) bw = key == c.pos ? kn : P.kb[d];
+      uint4 aw = make_uint4(0u, 0u, 0u, 0u);
+      if (col < nh) aw = *reinterpret_cast<const uint4*>(&A.q[col][d * 32 + slot * 8]);
+      d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, aw), __builtin_bit_cast(df_bf16x8, bw),
+                                                   d4, 0, 0, 0);
+    }
+    if (slot == 0) {
+#pragma unroll
+      for (int h = 0; h < kPairHeads; ++h)
+        if (h < nh) A.sc[h][c.wave * 16 + col] = live ? d4[h] * scale : -INFINITY;
+    }
+  }
+  // V rows: keys t0 + 16 wave + j, dims 4 lane ..+3
+  uint2 vb[16];
+  {
+    const size_t base = (size_t)(c.xcd >> 1) * c.max_len;
+    GlobalBf16 vc = (GlobalBf16)LF(Lp, v_cache);
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+      const int kk = t0 + c.wave * 16 + jj;
+      vb[jj] = make_uint2(0u, 0u);
+      if (kk < j1 && kk != c.pos) vb[jj] = gload8(vc + (base + kk) * kHd + c.lane * 4);
+    }
+  }
+  sync(c);
+  if (c.wave < nh) {
+    const int h = c.wave;
+    const float s0 = A.sc[h][c.lane], s1 = A.sc[h][c.lane + 64];
+    const float tmax = dmax(fmaxf(s0, s1));
+    const float mo = A.ml[h][0];
+    const float m_new = fmaxf(mo, tmax);
+    float p0 = 0.f, p1 = 0.f, alpha = 1.0f;
+    if (m_new != -INFINITY) {
+      p0 = s0 == -INFINITY ? 0.0f : expf(s0 - m_new);
+      p1 = s1 == -INFINITY ? 0.0f : expf(s1 - m_new);
+      alpha = mo == -INFINITY ? 0.0f : expf(mo - m_new);
+    }
+    const float lsum = dsum(p0 + p1);
+    A.sc[h][c.lane] = p0;
+    A.sc[h][c.lane + 64] = p1;
+    if (c.lane == 0) {
+      A.ml[h][0] = m_new;
+      A.ml[h][1] = A.ml[h][1] * alpha + lsum;
+      A.alpha[h] = alpha;
+    }
+  }
+  sync(c);
+  wait_vm<0>();  // the V rows (nothing else is in flight)
+  {
+#pragma unroll
+    for (int h = 0; h < kPairHeads; ++h) {
+      if (h >= nh) break;
+      const float a = A.alpha[h];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[h][i] *= a;
+    }
+    uint2 vn = *reinterpret_cast<const uint2*>(A.vnew + c.lane * 4);
+    asm volatile("" : "+v"(vn.x), "+v"(vn.y));
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+      const int kk = t0 + c.wave * 16 + jj;
+      if (kk < j1) {
+        const uint2 raw = kk == c.pos ? vn : vb[jj];
+        const float v0 = __uint_as_float(raw.x << 16), v1 = __uint_as_float(raw.x & 0xFFFF0000u);
+        const float v2 = __uint_as_float(raw.y << 16), v3 = __uint_as_float(raw.y & 0xFFFF0000u);
+#pragma unroll
+        for (int h = 0; h < kPairHeads; ++h) {
+          if (h >= nh) break;
+          const float pr = A.sc[h][c.wave * 16 + jj];
+          acc[h][0] += pr * v0;
+          acc[h][1] += pr * v1;
+          acc[h][2] += pr * v2;
+          acc[h][3] += pr * v3;
+        }
+      }
+    }
+  }
+  sync(c);
+}
+
 // ---------------------------------------------------------------------------------------
 // the two roles
 //
@@ -1585,6 +1810,7 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, floa
 // ---------------------------------------------------------------------------------------
 
 // The compute waves' whole launch.
+template <bool PAIR>
 DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int steps, Lds& L) {
   const int hidden = M.hidden;
   const int G = q.Gh;
@@ -1598,7 +1824,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
   st.issued = st.consumed = st.wslot = st.rslot = 0;
   st.ri = st.istep = 0;
   st.state = kStreaming;
-  st.nruns = build_runs(M, q, c);
+  st.nruns = build_runs<PAIR>(M, q, c);
   fill(st, steps, c);
   auto stop = [&]() { __builtin_amdgcn_s_waitcnt(0); };
 
@@ -1649,85 +1875,182 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         }
       } else {
         // attention split
-        fence(c);
-        int j0, j1;
-        at_keys(c, j0, j1);
-        auto& A = L.u.at;
-        sync(c);  // q/k/v staged
-        if (!L.ok) return stop();
-        const float posf = static_cast<float>(c.pos);
-        if (c.wave < 3) {
-          float x[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) x[i] = c.wave < 2 ? A.qraw[c.wave][c.lane * 4 + i] : A.kraw[c.lane * 4 + i];
-          norm_rope4_lds(x, c.wave < 2 ? A.qn_w : A.kn_w, M.eps, A.inv, posf, c.lane);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            if (c.wave < 2) A.q[c.wave][c.lane * 4 + i] = f2bf(x[i]);
-            else A.knew[c.lane * 4 + i] = f2bf(x[i]);
-          }
-        } else if (c.wave == 3) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) A.vnew[c.lane * 4 + i] = f2bf(A.vraw[c.lane * 4 + i]);
-        }
-        sync(c);
-        // the even XCD of the pair writes the new key/value (write-through: the odd XCD
-        // reads this row in later steps)
-        if ((c.xcd & 1) == 0 && c.pos >= j0 && c.pos < j1 && c.tid < kHd / 2) {
-          const size_t row = ((size_t)(c.xcd >> 1) * M.max_len + c.pos) * kHd;
-          const uint32_t kw = static_cast<uint32_t>(A.knew[2 * c.tid]) | (static_cast<uint32_t>(A.knew[2 * c.tid + 1]) << 16);
-          const uint32_t vw = static_cast<uint32_t>(A.vnew[2 * c.tid]) | (static_cast<uint32_t>(A.vnew[2 * c.tid + 1]) << 16);
-          st_sys(reinterpret_cast<uint32_t*>(LF(Lp, k_cache) + row) + c.tid, kw);
-          st_sys(reinterpret_cast<uint32_t*>(LF(Lp, v_cache) + row) + c.tid, vw);
-        }
-        float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        for (int t0 = j0; t0 < j1; t0 += kTileKeys) {
-          // K rows are loaded here, in straight-line code with their use (a prefetch across
-          // the staging barrier leaves the compiler unsure they completed, and it then makes
-          // the weight-stream loops wait for them)
-          AtPre P;
-          at_issue_k(c, Lp, t0, j1, P);
-          at_tile(c, Lp, t0, j1, P, acc, L);
-        }
-        // the split's KV loads are consumed (wait unconditionally: the compiler cannot pair
-        // the first tile's prefetch with the loop, and the held stream has nothing in flight)
-        wait_vm<0>();
-        // combine the waves' PV partials (into wave 0's row)
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) A.red[c.wave][hh][c.lane * 4 + i] = acc[hh][i];
-        sync(c);
-        {
-          const int e = c.tid;  // 512 = 2 heads x 256 dims
-          const int hh = e / kHd, d = e % kHd;
-          float sum = 0.0f;
-#pragma unroll
-          for (int wv = 0; wv < kCompute; ++wv) sum += A.red[wv][hh][d];
-          A.red[0][hh][d] = sum;
-        }
-        sync(c);
-        // the weight stream resumes with o_proj while the control wave merges the splits: two
-        // blocks per wave at a time, spaced out, so the refill (64 KB per CU) does not hold up
-        // the control wave's hand-off loads, which share the CU's memory pipeline
-        if (st.state == kHeld) {
-          st.state = kReleased;
-          open_run(st, steps);
-#pragma unroll 1
-          for (int k = 2; k <= kRing; k += 2) {
-            fill(st, steps, c, k);
-            if (k < kRing) __builtin_amdgcn_s_sleep(10);
-          }
-        }
-        {  // o_proj (the merge runs on the control wave meanwhile)
+        if constexpr (PAIR) {
           fence(c);
-          const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
-            sync(c);
+          int j0, j1;
+          at_keys4(c, j0, j1);
+          auto& A = L.u.at4;
+          sync(c);  // q/k/v staged
           if (!L.ok) return stop();
-          gemv_consume(g, c, st, M, q, steps, L);
+          const float posf = static_cast<float>(c.pos);
+          const int nh = at_pair(c.pos + 1) ? kPairHeads : 2;  // head slots in use
+          if (c.wave < nh || c.wave == kPairHeads) {  // waves 0..nh-1: the query heads, wave 4: the new key
+            const bool qw = c.wave < kPairHeads;
+            float x[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = qw ? A.qraw[c.wave][c.lane * 4 + i] : A.kraw[c.lane * 4 + i];
+            norm_rope4_lds(x, qw ? A.qn_w : A.kn_w, M.eps, A.inv, posf, c.lane);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              if (qw) A.q[c.wave][c.lane * 4 + i] = f2bf(x[i]);
+              else A.knew[c.lane * 4 + i] = f2bf(x[i]);
+            }
+          } else if (c.wave == kPairHeads + 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) A.vnew[c.lane * 4 + i] = f2bf(A.vraw[c.lane * 4 + i]);
+          }
           sync(c);
-          sync(c);  // all-reduce done
+          // the split that holds the new position writes its key/value row (write-through: any
+          // workgroup of either XCD of the pair reads the row in later steps); split per XCD,
+          // the even XCD's
+          if (c.pos >= j0 && c.pos < j1 && c.tid < kHd / 2 && (at_pair(c.pos + 1) || (c.xcd & 1) == 0)) {
+            const size_t row = ((size_t)(c.xcd >> 1) * M.max_len + c.pos) * kHd;
+            const uint32_t kw = static_cast<uint32_t>(A.knew[2 * c.tid]) | (static_cast<uint32_t>(A.knew[2 * c.tid + 1]) << 16);
+            const uint32_t vw = static_cast<uint32_t>(A.vnew[2 * c.tid]) | (static_cast<uint32_t>(A.vnew[2 * c.tid + 1]) << 16);
+            st_sys(reinterpret_cast<uint32_t*>(LF(Lp, k_cache) + row) + c.tid, kw);
+            st_sys(reinterpret_cast<uint32_t*>(LF(Lp, v_cache) + row) + c.tid, vw);
+          }
+          float acc[kPairHeads][4];
+#pragma unroll
+          for (int h = 0; h < kPairHeads; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[h][i] = 0.0f;
+          for (int t0 = j0; t0 < j1; t0 += kTileKeys) {
+            // K rows are loaded here, in straight-line code with their use (a prefetch across
+            // the staging barrier leaves the compiler unsure they completed, and it then makes
+            // the weight-stream loops wait for them)
+            AtPre P;
+            at_issue_k(c, Lp, t0, j1, P);
+            at_tile4(c, Lp, t0, j1, P, acc, nh, L);
+          }
+          // the split's KV loads are consumed (wait unconditionally: the compiler cannot pair
+          // the first tile's prefetch with the loop, and the held stream has nothing in flight)
+          wait_vm<0>();
+          // combine the waves' PV partials into A.red. The partials (32 KB) go to the weight
+          // ring, which is drained here: the stream holds at this layer's marker run, right after
+          // its input projection, so every block it issued was consumed and no DMA is in flight;
+          // the ring is refilled only after the second barrier below.
+          {
+            float(*prt)[kPairHeads][kHd] = reinterpret_cast<float(*)[kPairHeads][kHd]>(&g_ring_w[0][0][0]);
+            static_assert(sizeof(float) * kCompute * kPairHeads * kHd <= sizeof(g_ring_w), "partials fit the ring");
+#pragma unroll
+            for (int hh = 0; hh < kPairHeads; ++hh)
+              if (hh < nh)
+                *reinterpret_cast<float4*>(&prt[c.wave][hh][c.lane * 4]) = make_float4(acc[hh][0], acc[hh][1], acc[hh][2], acc[hh][3]);
+            sync(c);
+#pragma unroll
+            for (int e = c.tid; e < nh * kHd; e += kCompute * 64) {
+              const int hh = e / kHd, d = e % kHd;
+              float sum = 0.0f;
+#pragma unroll
+              for (int wv = 0; wv < kCompute; ++wv) sum += prt[wv][hh][d];
+              A.red[hh][d] = sum;
+            }
+          }
+          sync(c);
+          // the weight stream resumes with o_proj while the control wave merges the splits: two
+          // blocks per wave at a time, spaced out, so the refill (64 KB per CU) does not hold up
+          // the control wave's hand-off loads, which share the CU's memory pipeline
+          if (st.state == kHeld) {
+            st.state = kReleased;
+            open_run(st, steps);
+#pragma unroll 1
+            for (int k = 2; k <= kRing; k += 2) {
+              fill(st, steps, c, k);
+              if (k < kRing) __builtin_amdgcn_s_sleep(10);
+            }
+          }
+          {  // o_proj (the merge runs on the control wave meanwhile)
+            fence(c);
+            const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
+              sync(c);
+            if (!L.ok) return stop();
+            gemv_consume(g, c, st, M, q, steps, L);
+            sync(c);
+            sync(c);  // all-reduce done
+            if (!L.ok) return stop();
+          }
+        } else {
+          fence(c);
+          int j0, j1;
+          at_keys(c, j0, j1);
+          auto& A = L.u.at;
+          sync(c);  // q/k/v staged
           if (!L.ok) return stop();
+          const float posf = static_cast<float>(c.pos);
+          if (c.wave < 3) {
+            float x[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = c.wave < 2 ? A.qraw[c.wave][c.lane * 4 + i] : A.kraw[c.lane * 4 + i];
+            norm_rope4_lds(x, c.wave < 2 ? A.qn_w : A.kn_w, M.eps, A.inv, posf, c.lane);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              if (c.wave < 2) A.q[c.wave][c.lane * 4 + i] = f2bf(x[i]);
+              else A.knew[c.lane * 4 + i] = f2bf(x[i]);
+            }
+          } else if (c.wave == 3) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) A.vnew[c.lane * 4 + i] = f2bf(A.vraw[c.lane * 4 + i]);
+          }
+          sync(c);
+          // the even XCD of the pair writes the new key/value (write-through: the odd XCD
+          // reads this row in later steps)
+          if ((c.xcd & 1) == 0 && c.pos >= j0 && c.pos < j1 && c.tid < kHd / 2) {
+            const size_t row = ((size_t)(c.xcd >> 1) * M.max_len + c.pos) * kHd;
+            const uint32_t kw = static_cast<uint32_t>(A.knew[2 * c.tid]) | (static_cast<uint32_t>(A.knew[2 * c.tid + 1]) << 16);
+            const uint32_t vw = static_cast<uint32_t>(A.vnew[2 * c.tid]) | (static_cast<uint32_t>(A.vnew[2 * c.tid + 1]) << 16);
+            st_sys(reinterpret_cast<uint32_t*>(LF(Lp, k_cache) + row) + c.tid, kw);
+            st_sys(reinterpret_cast<uint32_t*>(LF(Lp, v_cache) + row) + c.tid, vw);
+          }
+          float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+          for (int t0 = j0; t0 < j1; t0 += kTileKeys) {
+            // K rows are loaded here, in straight-line code with their use (a prefetch across
+            // the staging barrier leaves the compiler unsure they completed, and it then makes
+            // the weight-stream loops wait for them)
+            AtPre P;
+            at_issue_k(c, Lp, t0, j1, P);
+            at_tile(c, Lp, t0, j1, P, acc, L);
+          }
+          // the split's KV loads are consumed (wait unconditionally: the compiler cannot pair
+          // the first tile's prefetch with the loop, and the held stream has nothing in flight)
+          wait_vm<0>();
+          // combine the waves' PV partials (into wave 0's row)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) A.red[c.wave][hh][c.lane * 4 + i] = acc[hh][i];
+          sync(c);
+          {
+            const int e = c.tid;  // 512 = 2 heads x 256 dims
+            const int hh = e / kHd, d = e % kHd;
+            float sum = 0.0f;
+#pragma unroll
+            for (int wv = 0; wv < kCompute; ++wv) sum += A.red[wv][hh][d];
+            A.red[0][hh][d] = sum;
+          }
+          sync(c);
+          // the weight stream resumes with o_proj while the control wave merges the splits: two
+          // blocks per wave at a time, spaced out, so the refill (64 KB per CU) does not hold up
+          // the control wave's hand-off loads, which share the CU's memory pipeline
+          if (st.state == kHeld) {
+            st.state = kReleased;
+            open_run(st, steps);
+#pragma unroll 1
+            for (int k = 2; k <= kRing; k += 2) {
+              fill(st, steps, c, k);
+              if (k < kRing) __builtin_amdgcn_s_sleep(10);
+            }
+          }
+          {  // o_proj (the merge runs on the control wave meanwhile)
+            fence(c);
+            const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
+              sync(c);
+            if (!L.ok) return stop();
+            gemv_consume(g, c, st, M, q, steps, L);
+            sync(c);
+            sync(c);  // all-reduce done
+            if (!L.ok) return stop();
+          }
         }
       }
       {  // gate|up + SwiGLU
@@ -1804,7 +2127,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
 }
 
 // The control wave's whole launch.
-template <bool TABLE>
+template <bool TABLE, bool PAIR>
 DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int steps, int teacher_forced, Lds& L) {
   const int hidden = M.hidden;
   const int G = q.Gh;
@@ -1909,15 +2232,19 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         if (kind == 0) {
           dma_row128(LF(Lp, gnorm_w), L.gnw, c.lane);
         } else {
-          dma_row128(LF(Lp, q_norm), L.u.at.qn_w, c.lane);
-          dma_row128(LF(Lp, q_norm) + 128, L.u.at.qn_w + 128, c.lane);
-          dma_row128(LF(Lp, k_norm), L.u.at.kn_w, c.lane);
-          dma_row128(LF(Lp, k_norm) + 128, L.u.at.kn_w + 128, c.lane);
+          uint16_t* qn_w = PAIR ? L.u.at4.qn_w : L.u.at.qn_w;
+          uint16_t* kn_w = PAIR ? L.u.at4.kn_w : L.u.at.kn_w;
+          dma_row128(LF(Lp, q_norm), qn_w, c.lane);
+          dma_row128(LF(Lp, q_norm) + 128, qn_w + 128, c.lane);
+          dma_row128(LF(Lp, k_norm), kn_w, c.lane);
+          dma_row128(LF(Lp, k_norm) + 128, kn_w + 128, c.lane);
           pre_inv = c.lane < kRot / 2 ? M.inv_freq[c.lane] : 0.0f;
         }
         sync(c);  // blocks consumed
         c.epoch += 1;
-        colpar_epilogue<true>(g, c, L);
+        // with the keys split over the pair, an attention layer's query columns (j < 1024,
+        // (j / 256) even) are also read by the pair's other XCD
+        colpar_epilogue<true>(g, c, L, PAIR && kind != 0 && at_pair(c.pos + 1));
       }
       if (kind == 0) {
         // ================= conv + gated delta step ===================================
@@ -1942,90 +2269,223 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         }
       } else {
         // ================= attention split ===========================================
-        fence(c, kTAttn);
-        auto& A = L.u.at;
-        {
-          const Seg seg[3] = {{0, kHd, A.qraw[0]}, {512, kHd, A.qraw[1]}, {kAttnK, 2 * kHd, A.kraw}};
-          if (!gather_colpar<3, 8>(c, seg, c.epoch)) return fail(1);  // kraw and vraw are adjacent in LDS
-          if (c.lane < kRot / 2) A.inv[c.lane] = pre_inv;
-          if (c.lane < 2) {
-            A.ml[c.lane][0] = -INFINITY;
-            A.ml[c.lane][1] = 0.0f;
+        if constexpr (PAIR) {
+          fence(c, kTAttn);
+          auto& A = L.u.at4;
+          {
+            if (!gather_attn(c, A.qraw, A.kraw, c.epoch, at_pair(c.pos + 1))) return fail(1);  // kraw, vraw adjacent
+            if (c.lane < kRot / 2) A.inv[c.lane] = pre_inv;
+            if (c.lane < kPairHeads) {
+              A.ml[c.lane][0] = -INFINITY;
+              A.ml[c.lane][1] = 0.0f;
+            }
           }
-        }
-        sync(c);
-        stamp(c, kTStaged);
-        sync(c);  // q/k normed and roped
-        int j0, j1;
-        at_keys(c, j0, j1);
-        for (int t0 = j0; t0 < j1; t0 += kTileKeys)
-          for (int i = 0; i < kTileBars; ++i) sync(c);
-        sync(c);
-        sync(c);  // PV partials summed into A.red[0]
-        c.epoch += 1;
-        {
-          float* ap = c.w.apart + ((size_t)c.xcd * kPerXcd + c.r) * 2 * kApHead;
-          for (int e = c.lane; e < 2 * kHd; e += 64) ap[(e / kHd) * kApHead + e % kHd] = A.red[0][e / kHd][e % kHd];
-          if (c.lane < 2) {
-            ap[c.lane * kApHead + kHd] = A.ml[c.lane][0];
-            ap[c.lane * kApHead + kHd + 1] = A.ml[c.lane][1];
-          }
-        }
-        signal_local(c, c.epoch);
-        // ================= merge the 32 splits: head r/16, dims 16 (r%16) ..+15 =======
-        {
-          fence(c, kTMerge);
-          auto& Mg = L.u.mg;
-          const int hl = c.r >> 4, d0 = (c.r & 15) * 16;
-          if (!wait_local(c, c.epoch)) return fail(1);
+          sync(c);
+          stamp(c, kTStaged);
+          sync(c);  // q/k normed and roped
+          int j0, j1;
+          at_keys4(c, j0, j1);
+          for (int t0 = j0; t0 < j1; t0 += kTileKeys)
+            for (int i = 0; i < kTileBars; ++i) sync(c);
+          sync(c);
+          sync(c);  // PV partials summed into A.red
           c.epoch += 1;
-          // split s: (m, l) of head hl and its accumulator dims d0 .. d0+15 (4 chunks)
-          const float* ap = c.w.apart + (size_t)c.xcd * kPerXcd * 2 * kApHead + hl * kApHead;
-          const auto r = rsrc(ap);
-          uint64_t ml = 0;
-          uint4 av[2];
-          if (c.lane < kPerXcd) ml = ld8<kCpAgent>(r, (c.lane * 2 * kApHead + kHd) * 4);
+          {
+            // the split's nh heads (acc, m, l) as (fp32, epoch) pairs into record (x & 1) * 32 + r
+            // of the pair: written through when the keys are split over the pair (each XCD merges
+            // its two heads over all 64 splits), else plain (only this XCD reads it, from L2)
+            const bool pair = at_pair(c.pos + 1);
+            const int nh = pair ? kPairHeads : 2;
+            const int split = (c.xcd & 1) * kPerXcd + c.r;
+            const auto ra = rsrc(reinterpret_cast<const uint64_t*>(c.w.apart) + ((size_t)(c.xcd >> 1) * kSplits + split) * kPairHeads * kApHead);
+            const uint32_t ep = c.epoch;
 #pragma unroll
-          for (int k = 0; k < 2; ++k) {
-            const int ch = c.lane + 64 * k;  // 128 chunks: split ch / 4, dims 4 (ch % 4)
-            av[k] = ld16<kCpAgent>(r, ((ch / 4) * 2 * kApHead + d0 + 4 * (ch % 4)) * 4);
+            for (int k = 0; k < kPairHeads * kHd / 128; ++k) {
+              const int e = 2 * (c.lane + 64 * k);  // dims e, e + 1 of head e / kHd
+              const int hh = e / kHd, d = e % kHd;
+              if (hh >= nh) break;  // (uniform: hh = k / 2)
+              const float2 v = *reinterpret_cast<const float2*>(&A.red[hh][d]);
+              const uint4 w = make_uint4(__float_as_uint(v.x), ep, __float_as_uint(v.y), ep);
+              if (pair) st16<kCpSystem>(ra, (hh * kApHead + d) * 8, w);
+              else st16<kCpPlain>(ra, (hh * kApHead + d) * 8, w);
+            }
+            if (c.lane < nh) {
+              const uint4 w = make_uint4(__float_as_uint(A.ml[c.lane][0]), ep, __float_as_uint(A.ml[c.lane][1]), ep);
+              if (pair) st16<kCpSystem>(ra, (c.lane * kApHead + kHd) * 8, w);
+              else st16<kCpPlain>(ra, (c.lane * kApHead + kHd) * 8, w);
+            }
           }
-          const Seg seg[1] = {{hl * 512 + kHd + d0, 16, Mg.gate}};
-          if (!gather_colpar<1, 1>(c, seg, c.epoch - 2)) return fail(1);  // the input projection's
+          // ================= merge the splits: head r/16, dims 16 (r%16) ..+15 ============
+          {
+            fence(c, kTMerge);
+            auto& Mg = L.u.mg4;
+            const int hl = c.r >> 4, d0 = (c.r & 15) * 16;
+            const uint32_t want = c.epoch;
+            c.epoch += 1;
+            // lane s reads a split's (m, l) of this XCD's head hl and its accumulator dims d0 ..
+            // d0+15, polling every (value, epoch) pair (the buffer descriptor is wave-uniform:
+            // the lane's record goes into the offset). Split over the pair, lane s reads record s
+            // at system scope, where the head is slot hl if this XCD wrote the record and slot
+            // 2 + hl if the other XCD did; split per XCD, lane s < 32 reads this XCD's record
+            // (x & 1) * 32 + s, slot hl, at agent scope, and lanes 32.. stand for empty splits.
+            const bool pair = at_pair(c.pos + 1);
+            const bool live = pair || c.lane < kPerXcd;
+            const auto r = rsrc(reinterpret_cast<const uint64_t*>(c.w.apart) + (size_t)(c.xcd >> 1) * kSplits * kPairHeads * kApHead);
+            const int rec = pair ? c.lane : (c.xcd & 1) * kPerXcd + (c.lane & (kPerXcd - 1));
+            const int slot = (rec / kPerXcd) == (c.xcd & 1) ? hl : 2 + hl;
+            const int so = ((rec * kPairHeads + slot) * kApHead) * 8;
+            static_assert(kSplits == 64, "one split per lane");
+            // (m, l) first: one 16-byte poll per lane while the splits finish; the accumulators
+            // are then read once (and re-polled only if some are not visible yet)
+            uint4 mlv = make_uint4(0xFF800000u, want, 0u, want), av[8];
 #pragma unroll
-          for (int k = 0; k < 2; ++k) {
-            const int ch = c.lane + 64 * k;
-            *reinterpret_cast<uint4*>(&Mg.acc[ch / 4][4 * (ch % 4)]) = av[k];
-          }
-          stamp(c, kTStaged);
-          const float m = __uint_as_float(static_cast<uint32_t>(ml));
-          const float l = __uint_as_float(static_cast<uint32_t>(ml >> 32));
-          const float mm = c.lane < kPerXcd && l > 0.0f ? m : -INFINITY;
-          const float mstar = dmax(mm);
-          const float wgt = mm == -INFINITY ? 0.0f : expf(mm - mstar);
-          const float den = dsum(c.lane < kPerXcd ? wgt * l : 0.0f);
-          if (c.lane < kPerXcd) Mg.wgt[c.lane] = wgt;
-          if (c.lane < 16) {
+            for (int k = 0; k < 8; ++k) av[k] = make_uint4(0u, want, 0u, want);
+            auto ld = [&](int off) { return pair ? ld16<kCpSystem>(r, off) : ld16<kCpAgent>(r, off); };
+            if (!poll_tagged(c, [&]() {
+                  if (live) mlv = ld(so + kHd * 8);
+                  return pairs_ok(mlv, want);
+                }))
+              return fail(1);
+            if (!poll_tagged(c, [&]() {
+                  if (live) {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) av[k] = ld(so + (d0 + 2 * k) * 8);
+                  }
+                  bool t = true;
+#pragma unroll
+                  for (int k = 0; k < 8; ++k) t = t && pairs_ok(av[k], want);
+                  return t;
+                }))
+              return fail(1);
+            const Seg seg[1] = {{hl * 512 + kHd + d0, 16, Mg.gate}};
+            if (!gather_colpar<1, 1>(c, seg, c.epoch - 2)) return fail(1);  // the input projection's
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+              *reinterpret_cast<float2*>(&Mg.acc[c.lane][2 * k]) = make_float2(__uint_as_float(av[k].x), __uint_as_float(av[k].z));
+            stamp(c, kTStaged);
+            const float m = __uint_as_float(mlv.x);
+            const float l = __uint_as_float(mlv.z);
+            const float mm = l > 0.0f ? m : -INFINITY;
+            const float mstar = dmax(mm);
+            const float wgt = mm == -INFINITY ? 0.0f : expf(mm - mstar);
+            const float den = dsum(wgt * l);
+            Mg.wgt[c.lane] = wgt;
+            // lane l sums splits 16 (l / 16) .. +15 of dim l % 16; the four quarters are added
+            // pairwise across lanes (fixed order)
             float num = 0.0f;
-            for (int sp = 0; sp < kPerXcd; ++sp) num += Mg.wgt[sp] * Mg.acc[sp][c.lane];
-            const float o = round_bf(num / den);
-            const float gx = Mg.gate[c.lane];
-            const float gate = round_bf(M.gate_kind == 0 ? sigmoid(gx) : silu(gx));
-            c.w.core[(size_t)c.xcd * 512 + hl * kHd + d0 + c.lane] = tag_bf16(f2bf(o * gate), c.epoch);
+            {
+              const int dd = c.lane & 15, s0 = (c.lane >> 4) * 16;
+#pragma unroll
+              for (int j = 0; j < 16; ++j) num += Mg.wgt[s0 + j] * Mg.acc[s0 + j][dd];
+              num += __shfl_xor(num, 16, 64);
+              num += __shfl_xor(num, 32, 64);
+            }
+            if (c.lane < 16) {
+              const float o = round_bf(num / den);
+              const float gx = Mg.gate[c.lane];
+              const float gate = round_bf(M.gate_kind == 0 ? sigmoid(gx) : silu(gx));
+              c.w.core[(size_t)c.xcd * 512 + hl * kHd + d0 + c.lane] = tag_bf16(f2bf(o * gate), c.epoch);
+            }
           }
-        }
-        // ================= o_proj (row-parallel) =====================================
-        {
-          fence(c, kTOProj);
-          const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
-          if (!stage_core(L, c, c.epoch, true)) return fail(1);
+          // ================= o_proj (row-parallel) =====================================
+          {
+            fence(c, kTOProj);
+            const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
+            if (!stage_core(L, c, c.epoch, true)) return fail(1);
+            sync(c);
+            stamp(c, kTStaged);
+            dma_row(LF(Lp, post_norm), L.nw, hidden, c.lane);
+            sync(c);  // blocks consumed
+            rowpar_epilogue(g, c, L, hidden);
+            if (!allreduce_residual(c, L, hidden)) return fail(1);
+            sync(c);
+          }
+        } else {
+          fence(c, kTAttn);
+          auto& A = L.u.at;
+          {
+            const Seg seg[3] = {{0, kHd, A.qraw[0]}, {512, kHd, A.qraw[1]}, {kAttnK, 2 * kHd, A.kraw}};
+            if (!gather_colpar<3, 8>(c, seg, c.epoch)) return fail(1);  // kraw and vraw are adjacent in LDS
+            if (c.lane < kRot / 2) A.inv[c.lane] = pre_inv;
+            if (c.lane < 2) {
+              A.ml[c.lane][0] = -INFINITY;
+              A.ml[c.lane][1] = 0.0f;
+            }
+          }
           sync(c);
           stamp(c, kTStaged);
-          dma_row(LF(Lp, post_norm), L.nw, hidden, c.lane);
-          sync(c);  // blocks consumed
-          rowpar_epilogue(g, c, L, hidden);
-          if (!allreduce_residual(c, L, hidden)) return fail(1);
+          sync(c);  // q/k normed and roped
+          int j0, j1;
+          at_keys(c, j0, j1);
+          for (int t0 = j0; t0 < j1; t0 += kTileKeys)
+            for (int i = 0; i < kTileBars; ++i) sync(c);
           sync(c);
+          sync(c);  // PV partials summed into A.red[0]
+          c.epoch += 1;
+          {
+            float* ap = c.w.apart + ((size_t)c.xcd * kPerXcd + c.r) * 2 * kApHead;
+            for (int e = c.lane; e < 2 * kHd; e += 64) ap[(e / kHd) * kApHead + e % kHd] = A.red[0][e / kHd][e % kHd];
+            if (c.lane < 2) {
+              ap[c.lane * kApHead + kHd] = A.ml[c.lane][0];
+              ap[c.lane * kApHead + kHd + 1] = A.ml[c.lane][1];
+            }
+          }
+          signal_local(c, c.epoch);
+          // ================= merge the 32 splits: head r/16, dims 16 (r%16) ..+15 =======
+          {
+            fence(c, kTMerge);
+            auto& Mg = L.u.mg;
+            const int hl = c.r >> 4, d0 = (c.r & 15) * 16;
+            if (!wait_local(c, c.epoch)) return fail(1);
+            c.epoch += 1;
+            // split s: (m, l) of head hl and its accumulator dims d0 .. d0+15 (4 chunks)
+            const float* ap = c.w.apart + (size_t)c.xcd * kPerXcd * 2 * kApHead + hl * kApHead;
+            const auto r = rsrc(ap);
+            uint64_t ml = 0;
+            uint4 av[2];
+            if (c.lane < kPerXcd) ml = ld8<kCpAgent>(r, (c.lane * 2 * kApHead + kHd) * 4);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+              const int ch = c.lane + 64 * k;  // 128 chunks: split ch / 4, dims 4 (ch % 4)
+              av[k] = ld16<kCpAgent>(r, ((ch / 4) * 2 * kApHead + d0 + 4 * (ch % 4)) * 4);
+            }
+            const Seg seg[1] = {{hl * 512 + kHd + d0, 16, Mg.gate}};
+            if (!gather_colpar<1, 1>(c, seg, c.epoch - 2)) return fail(1);  // the input projection's
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+              const int ch = c.lane + 64 * k;
+              *reinterpret_cast<uint4*>(&Mg.acc[ch / 4][4 * (ch % 4)]) = av[k];
+            }
+            stamp(c, kTStaged);
+            const float m = __uint_as_float(static_cast<uint32_t>(ml));
+            const float l = __uint_as_float(static_cast<uint32_t>(ml >> 32));
+            const float mm = c.lane < kPerXcd && l > 0.0f ? m : -INFINITY;
+            const float mstar = dmax(mm);
+            const float wgt = mm == -INFINITY ? 0.0f : expf(mm - mstar);
+            const float den = dsum(c.lane < kPerXcd ? wgt * l : 0.0f);
+            if (c.lane < kPerXcd) Mg.wgt[c.lane] = wgt;
+            if (c.lane < 16) {
+              float num = 0.0f;
+              for (int sp = 0; sp < kPerXcd; ++sp) num += Mg.wgt[sp] * Mg.acc[sp][c.lane];
+              const float o = round_bf(num / den);
+              const float gx = Mg.gate[c.lane];
+              const float gate = round_bf(M.gate_kind == 0 ? sigmoid(gx) : silu(gx));
+              c.w.core[(size_t)c.xcd * 512 + hl * kHd + d0 + c.lane] = tag_bf16(f2bf(o * gate), c.epoch);
+            }
+          }
+          // ================= o_proj (row-parallel) =====================================
+          {
+            fence(c, kTOProj);
+            const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
+            if (!stage_core(L, c, c.epoch, true)) return fail(1);
+            sync(c);
+            stamp(c, kTStaged);
+            dma_row(LF(Lp, post_norm), L.nw, hidden, c.lane);
+            sync(c);  // blocks consumed
+            rowpar_epilogue(g, c, L, hidden);
+            if (!allreduce_residual(c, L, hidden)) return fail(1);
+            sync(c);
+          }
         }
       }
       // ================= gate|up + SwiGLU (column-parallel) ============================
@@ -2145,7 +2605,10 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
 // TABLE: embed from the checkpoint's bf16 table (M.embed_table) instead of the tied int4
 // head. Two instances, so the tied build carries no code for the other path (the decode is
 // sensitive to the kernel's code layout).
-template <bool TABLE>
+// TABLE: the embedding reads a bf16 table (else it dequantises the tied head's row). PAIR: the
+// KV cache can hold enough keys for attention to split them over the XCD pair (chosen per step
+// by at_pair); the other instance keeps the per-XCD split and its code layout.
+template <bool TABLE, bool PAIR>
 __global__ __launch_bounds__(kThreads) void decode_kernel(DfPersistModel M, Ws w, int steps, int teacher_forced) {
   __shared__ Lds L;
   Ctx c;
@@ -2208,8 +2671,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DfPersistModel M, Ws w
   q.t_hi = c.xcd * vocab_tiles + ((c.r + 1) * vocab_tiles) / kPerXcd;
   __syncthreads();  // everyone has read the registration before L.token is reused
 
-  if (c.control) control_main<TABLE>(M, q, c, steps, teacher_forced, L);
-  else compute_main(M, q, c, steps, L);
+  if (c.control) control_main<TABLE, PAIR>(M, q, c, steps, teacher_forced, L);
+  else compute_main<PAIR>(M, q, c, steps, L);
 }
 
 __global__ void register_reset_kernel(int* ctl) {
@@ -2265,8 +2728,12 @@ extern "C" int df_decode_persistent(const DfPersistModel* model, int steps, int 
   ws_layout(m.hidden, &w, reinterpret_cast<char*>(workspace));
   hipLaunchKernelGGL(register_reset_kernel, dim3(1), dim3(64), 0, stream, w.ctl);
   if (hipGetLastError() != hipSuccess) return DF_LAUNCH_FAILED;
-  const void* kernel =
-      m.embed_table ? reinterpret_cast<const void*>(decode_kernel<true>) : reinterpret_cast<const void*>(decode_kernel<false>);
+  // the launch's positions are on the device; the cache length bounds them. (The table lists
+  // the tied-head, per-XCD instance first, which places its code first in the code object.)
+  static const void* const kernels[4] = {
+      reinterpret_cast<const void*>(decode_kernel<false, false>), reinterpret_cast<const void*>(decode_kernel<true, false>),
+      reinterpret_cast<const void*>(decode_kernel<false, true>), reinterpret_cast<const void*>(decode_kernel<true, true>)};
+  const void* kernel = kernels[(m.embed_table ? 1 : 0) + (at_pair(m.max_len) ? 2 : 0)];
   if (plain_launch()) {
     // an ordinary dispatch of the same grid: co-residency is checked here instead of by the
     // cooperative launch (one workgroup per CU, every CU of the device), and a workgroup that
@@ -2277,10 +2744,8 @@ extern "C" int df_decode_persistent(const DfPersistModel* model, int steps, int 
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0) != hipSuccess ||
         cus * per_cu < kNwg)
       return DF_LAUNCH_FAILED;
-    if (m.embed_table)
-      hipLaunchKernelGGL(decode_kernel<true>, dim3(kNwg), dim3(kThreads), 0, stream, m, w, steps, teacher_forced);
-    else
-      hipLaunchKernelGGL(decode_kernel<false>, dim3(kNwg), dim3(kThreads), 0, stream, m, w, steps, teacher_forced);
+    void* args[] = {&m, &w, &steps, &teacher_forced};
+    if (hipLaunchKernel(kernel, dim3(kNwg), dim3(kThreads), args, 0, stream) != hipSuccess) return DF_LAUNCH_FAILED;
     return hipGetLastError() == hipSuccess ? DF_OK : DF_LAUNCH_FAILED;
   }
   void* args[] = {&m, &w, &steps, &teacher_forced};

@@ -37,6 +37,9 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--candidate", required=True)
     ap.add_argument("--baseline", default=str(N.LIB_PATH))
     ap.add_argument("--prompt-len", type=int, default=4096)
+    ap.add_argument("--fill", choices=("steps", "parallel"), default="steps",
+                    help="prompt fill: teacher-forced steps of each build's own kernel, or the parallel "
+                         "prefill (the same caches for every column; long prompts in seconds)")
     ap.add_argument("--tokens", type=int, default=64)
     ap.add_argument("--rounds", type=int, default=9)
     ap.add_argument("--warmup-rounds", type=int, default=2)
@@ -55,11 +58,19 @@ def main(argv: list[str] | None = None) -> int:
     libs = {"baseline": N.load(args.baseline, names), "candidate": N.load(args.candidate, names)}
     libs["identity"] = libs["baseline"]
     decoders, snaps = {}, {}
+    filler = None
+    if args.fill == "parallel":
+        from ..prefill import Prefiller
+
+        filler = Prefiller(model)
     for label, lib in libs.items():
         t0 = time.time()
         dec = PersistentDecoder(model, max_seq_len=args.prompt_len + args.tokens + 8, max_new_tokens=args.tokens,
                                 lib=lib)
-        dec.prefill(prompt)
+        if filler is not None:
+            filler.fill(dec, prompt)
+        else:
+            dec.prefill(prompt)
         dec.check()
         decoders[label] = dec
         snaps[label] = dec.snapshot()
@@ -94,7 +105,7 @@ def main(argv: list[str] | None = None) -> int:
     rec = ResultRecord(
         kind="ab", outcome=outcome(ratio, iqr, correct=correct) if cal["holds"] else "error",
         config_name=args.name,
-        workload={"prompt_len": args.prompt_len, "tokens_per_call": args.tokens, "seed": args.seed,
+        workload={"prompt_len": args.prompt_len, "fill": args.fill, "tokens_per_call": args.tokens, "seed": args.seed,
                   "baseline": args.baseline, "candidate": args.candidate, "bytes_per_token": per_token},
         bench=res.to_dict(), correctness=corr, calibration=cal)
     if args.record:

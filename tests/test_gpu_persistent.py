@@ -88,16 +88,18 @@ def test_persistent_state_matches_engine(mid):
         assert int(dec.position.item()) == n
 
 
-def test_persistent_long_context_attention_matches_engine():
+@pytest.mark.parametrize("n", [4200, 12400])
+def test_persistent_long_context_attention_matches_engine(n):
     """Attention at 4 200 keys, where each workgroup's split (132 keys) spans two 128-key tiles
-    and 32 splits merge per head: an attention-only stack, persistent vs the per-op engine
+    and each XCD merges 32 splits per head, and at 12 400 keys, past the length where the keys
+    are split over the XCD pair instead (64 splits of 194 keys serving all four query heads of
+    a KV head, merged across XCDs): an attention-only stack, persistent vs the per-op engine
     (whose split-KV attention kernel is checked against the oracle up to 131 072 keys; the CPU
     oracle itself would take minutes here). K/V caches within 3 % normwise, logits after the
     prefill and after one more step (its new key written inside a two-tile split) within a
     mean KL of 1e-3 (the reference's layer-2 bar) with the same argmax."""
     cfg = dataclasses.replace(mid_config(2), layer_types=(FULL_ATTENTION, FULL_ATTENTION), name="attn-2")
     model = synth.synth_model(cfg, seed=7)
-    n = 4200
     prompt = synth.prompt_ids(cfg.vocab_size, n, seed=8)
     dec = PersistentDecoder(model, max_seq_len=n + 16, max_new_tokens=8)
     eng = DecodeEngine(model, max_seq_len=n + 16, max_new_tokens=8)
