@@ -285,11 +285,18 @@ class Prefiller:
             h, x = ops.add_rms_norm(d, h, nxt, eps)
         return ops.int4_gemv(x[-1:], self.head)
 
-    def fill(self, decoder, prompt: Tensor) -> None:
+    def fill(self, decoder, prompt: Tensor, *, chunk: int = 16384) -> None:
         """Prefill a ``PersistentDecoder`` (fresh or reset) with ``prompt`` ``[1, P]``: its caches,
-        position, last logits and first generated token, as its own ``prefill`` leaves them."""
+        position, last logits and first generated token, as its own ``prefill`` leaves them.
+
+        The prompt runs through ``forward`` ``chunk`` tokens at a time (positions continue from
+        the caches), which bounds the activations and the conv kernel's grid (at most 65 535
+        rows). ``chunk`` is a multiple of the delta rule's 64-token chunk, so the chunks are the
+        ones a single pass would form and the result is the same."""
         if prompt.dim() != 2 or prompt.shape[0] != 1:
             raise ValueError(f"prompt must be [1, P], got {tuple(prompt.shape)}")
+        if chunk < 64 or chunk % 64 or chunk > 65535:
+            raise ValueError("chunk must be a multiple of 64 below 65536")
         plen = prompt.shape[1]
         if plen + decoder.max_new_tokens > decoder.max_seq_len:
             raise ValueError("prompt + max_new_tokens exceeds the cache")
@@ -297,7 +304,8 @@ class Prefiller:
         ids = prompt[0].to(self.device, torch.int64).contiguous()
         decoder.prompt[:plen].copy_(ids)
         decoder.prompt_len = plen
-        logits = self.forward(ids, decoder.layer_state, pos0=0)
+        for s in range(0, plen, chunk):
+            logits = self.forward(ids[s:s + chunk], decoder.layer_state, pos0=s)
         decoder.logits.copy_(logits)
         ops.argmax_tokens(decoder.logits, decoder.tokens)
         decoder.position.fill_(plen)

@@ -286,3 +286,25 @@ def test_filled_persistent_decoder_continues_like_the_oracle(mid):
           f"filled: agreement {float(agree.float().mean()):.4f}, KL {float(kl.mean()):.3e}", flush=True)
     assert float(kl.mean()) < max(1e-3, 2 * float(kl_own.mean()))
     assert float(agree.float().mean()) >= min(7 / 8, float(agree_own.float().mean()))
+
+
+def test_fill_in_chunks_equals_one_pass(mid):
+    """``Prefiller.fill`` runs a long prompt in chunks (positions continuing from the caches).
+    With chunk boundaries on the delta rule's 64-token chunks the arithmetic is the single
+    pass's, so 200 tokens filled 64 at a time must leave bit-identical caches, logits and first
+    token; chunk sizes off that grid are refused."""
+    cfg, model, oracle, pre = mid
+    prompt = synth.prompt_ids(cfg.vocab_size, 200, seed=60).to(DEV)
+    one = PersistentDecoder(model, max_seq_len=256, max_new_tokens=16)
+    pre.fill(one, prompt)
+    parts = PersistentDecoder(model, max_seq_len=256, max_new_tokens=16)
+    pre.fill(parts, prompt, chunk=64)
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(one.layer_state, parts.layer_state)):
+        for name in a:
+            assert torch.equal(a[name], b[name]), f"layer {i} {name}"
+    assert torch.equal(one.logits, parts.logits) and torch.equal(one.tokens, parts.tokens)
+    assert int(parts.position.item()) == 200
+    for bad in (32, 100, 65536):
+        with pytest.raises(ValueError):
+            pre.fill(parts, prompt, chunk=bad)
