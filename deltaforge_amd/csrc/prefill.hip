@@ -37,9 +37,14 @@ DF_DEVICE float readlane(float v, int lane) {
 // column L % 16. Word i holds k = 32 (L / 16) + 8 i + e, e < 8, with element e at bit
 // 4 (e / 2), plus 16 when e is odd. That is exactly the B operand of
 // v_mfma_f32_16x16x32_bf16 number i, whose A operand is then x[row][32 (L / 16) + 8 i ..+8].
-// A workgroup computes a 128 x 128 tile. Its four waves each own 64 rows x 64 columns (4 x 4
-// products). Per 128-group, the x rows and the dequantised weights are staged in LDS; the
-// dequant is int4_block.h's exact one (19 VALU per 8 weights).
+// A workgroup computes a 128 x 128 tile; wave w owns all 128 rows and column tiles 2w, 2w + 1
+// (8 x 2 products). Per 128-group:
+// - only the x rows go through LDS, double-buffered (one barrier per group): the next
+//   group's rows are stored from registers while this group's products run;
+// - each wave loads its two weight blocks straight into registers a group ahead, in the
+//   MFMA B layout, and dequantises them there with int4_block.h's exact dequant (19 VALU per
+//   8 weights), so every weight is dequantised once and never staged.
+// The products, and each output's order of summation, are those of a staged-B design.
 
 constexpr int kGmBM = 128;
 constexpr int kGmTiles = 8;           // 16-column tiles per workgroup (128 columns)
@@ -47,101 +52,99 @@ constexpr int kGmXPitch = 128 + 8;    // bf16 per staged x row (16-byte pad)
 
 template <int EPI>
 __global__ __launch_bounds__(256, 2) void int4_gemm_kernel(DfInt4GemmArgs p) {
-  __shared__ __align__(16) uint16_t xs[kGmBM * kGmXPitch];
-  __shared__ __align__(16) uint4 ws[kGmTiles * 4 * 64];  // [tile][mfma i][lane]
+  __shared__ __align__(16) uint16_t xs[2][kGmBM * kGmXPitch];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wr = wave >> 1, wc = wave & 1;
-  const int m0 = blockIdx.y * kGmBM, t0 = blockIdx.x * kGmTiles;
+  const int m0 = blockIdx.y * kGmBM, t0 = blockIdx.x * kGmTiles + 2 * wave;
   const int G = p.K / 128, ntiles = p.N / 16;
-  df_f32x4 acc[4][4];
+  df_f32x4 acc[8][2];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
+  for (int rb = 0; rb < 8; ++rb)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[rb][j] = df_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 2; ++j) acc[rb][j] = df_f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Group g + 1's x chunks and weight words are loaded into registers while group g's
-  // products run; the stores into LDS (and the dequant) follow the barrier that ends them.
-  uint4 xr[8], wr8[2];
+  uint4 xr[8], wr[2];
   uint16_t sr[2];
-  auto load_group = [&](int g) {
+  auto load_x = [&](int g) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {  // x: 128 rows x 16 chunks of 16 bytes
+    for (int i = 0; i < 8; ++i) {  // 128 rows x 16 chunks of 16 bytes
       const int ch = tid + 256 * i, r = ch >> 4, cc = ch & 15;
       xr[i] = m0 + r < p.M ? *reinterpret_cast<const uint4*>(p.x + (size_t)(m0 + r) * p.ldx + g * 128 + cc * 8)
                            : make_uint4(0u, 0u, 0u, 0u);
     }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {  // weights: 8 blocks x 64 lanes' 16 bytes (zeros past N)
-      const int u = tid + 256 * i, j = u >> 6, L = u & 63;
-      wr8[i] = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
-      sr[i] = 0;
-      if (t0 + j < ntiles) {
-        const size_t blk = (size_t)(t0 + j) * G + g;
-        wr8[i] = *reinterpret_cast<const uint4*>(p.w + blk * 1024 + L * 16);
-        sr[i] = p.s[blk * 16 + (L & 15)];
-      }
-    }
   };
-  load_group(0);
-  for (int g = 0; g < G; ++g) {
+  auto store_x = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int ch = tid + 256 * i, r = ch >> 4, cc = ch & 15;
-      *reinterpret_cast<uint4*>(&xs[r * kGmXPitch + cc * 8]) = xr[i];
+      *reinterpret_cast<uint4*>(&xs[buf][r * kGmXPitch + cc * 8]) = xr[i];
     }
+  };
+  auto load_w = [&](int g) {  // this wave's two blocks of group g (zeros past N)
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int u = tid + 256 * i, j = u >> 6, L = u & 63;
-      // the exact bf16((n - 8) * scale) of the per-op GEMV (int4_block.h)
-      const GroupScale gs = group_scale(sr[i]);
-      ws[(j * 4 + 0) * 64 + L] = dequant8(wr8[i].x, gs);
-      ws[(j * 4 + 1) * 64 + L] = dequant8(wr8[i].y, gs);
-      ws[(j * 4 + 2) * 64 + L] = dequant8(wr8[i].z, gs);
-      ws[(j * 4 + 3) * 64 + L] = dequant8(wr8[i].w, gs);
+    for (int j = 0; j < 2; ++j) {
+      wr[j] = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
+      sr[j] = 0;
+      if (t0 + j < ntiles) {
+        const size_t blk = (size_t)(t0 + j) * G + g;
+        wr[j] = *reinterpret_cast<const uint4*>(p.w + blk * 1024 + lane * 16);
+        sr[j] = p.s[blk * 16 + (lane & 15)];
+      }
     }
+  };
+  load_x(0);
+  load_w(0);
+  store_x(0);
+  if (G > 1) load_x(1);
+  for (int g = 0; g < G; ++g) {
+    // xs[g & 1] is complete, and every wave is done with xs[(g + 1) & 1] (group g - 1)
     __syncthreads();
-    if (g + 1 < G) load_group(g + 1);
+    uint4 b[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const GroupScale gs = group_scale(sr[j]);  // the exact bf16((n - 8) * scale) of the per-op GEMV
+      b[j][0] = dequant8(wr[j].x, gs);
+      b[j][1] = dequant8(wr[j].y, gs);
+      b[j][2] = dequant8(wr[j].z, gs);
+      b[j][3] = dequant8(wr[j].w, gs);
+    }
+    if (g + 1 < G) {
+      store_x((g + 1) & 1);
+      load_w(g + 1);
+    }
+    if (g + 2 < G) load_x(g + 2);
+    const uint16_t* xb = xs[g & 1];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint4 a[4], b[4];
+      uint4 a[8];
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb)
-        a[rb] = *reinterpret_cast<const uint4*>(
-            &xs[(wr * 64 + rb * 16 + (lane & 15)) * kGmXPitch + (lane >> 4) * 32 + i * 8]);
+      for (int rb = 0; rb < 8; ++rb)
+        a[rb] = *reinterpret_cast<const uint4*>(&xb[(rb * 16 + (lane & 15)) * kGmXPitch + (lane >> 4) * 32 + i * 8]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = ws[((wc * 4 + j) * 4 + i) * 64 + lane];
+      for (int rb = 0; rb < 8; ++rb)
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[rb][j] = mfma(a[rb], b[j], acc[rb][j]);
+        for (int j = 0; j < 2; ++j) acc[rb][j] = mfma(a[rb], b[j][i], acc[rb][j]);
     }
-    __syncthreads();
   }
 
   // lane holds D[4 (lane / 16) + r][lane % 16] of each 16 x 16 product
   const int col_in = lane & 15;
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
+  for (int rb = 0; rb < 8; ++rb) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = m0 + wr * 64 + rb * 16 + (lane >> 4) * 4 + r;
+      const int row = m0 + rb * 16 + (lane >> 4) * 4 + r;
       if (row >= p.M) continue;
       if (EPI == DF_EPI_SWIGLU) {
-        // tiles alternate gate, up: product pairs (0, 1) and (2, 3) of this wave;
+        // tiles alternate gate, up: this wave's pair (2w, 2w + 1);
         // bf16(bf16(silu(bf16(g))) * bf16(u)) (reference.py:692-693)
-#pragma unroll
-        for (int jp = 0; jp < 2; ++jp) {
-          const int tile = t0 + wc * 4 + 2 * jp;
-          if (tile >= ntiles) continue;
-          const float gv = round_bf(acc[rb][2 * jp][r]), uv = round_bf(acc[rb][2 * jp + 1][r]);
-          p.out[(size_t)row * p.ldo + (tile / 2) * 16 + col_in] = f2bf(round_bf(silu(gv)) * uv);
-        }
+        if (t0 >= ntiles) continue;
+        const float gv = round_bf(acc[rb][0][r]), uv = round_bf(acc[rb][1][r]);
+        p.out[(size_t)row * p.ldo + (t0 / 2) * 16 + col_in] = f2bf(round_bf(silu(gv)) * uv);
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int tile = t0 + wc * 4 + j;
-          if (tile >= ntiles) continue;
-          p.out[(size_t)row * p.ldo + tile * 16 + col_in] = f2bf(acc[rb][j][r]);
+        for (int j = 0; j < 2; ++j) {
+          if (t0 + j >= ntiles) continue;
+          p.out[(size_t)row * p.ldo + (t0 + j) * 16 + col_in] = f2bf(acc[rb][j][r]);
         }
       }
     }
