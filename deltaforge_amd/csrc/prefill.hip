@@ -225,7 +225,7 @@ struct PrepLds {
   float Q[kCk][kPitch];
   float K[kCk][kPitch];
   float V[kCk][kPitch];
-  float A[kCk][kCk];    // beta_t-scaled, decayed, strictly lower
+  float At[kCk][kCk];   // A' transposed: At[j][t] = A'[t][j] (beta_t-scaled, decayed, strictly lower)
   float QK[kCk][kCk];   // decayed, lower with the diagonal
   float gam[kCk], beta[kCk], eg[kCk], dec[kCk];
 };
@@ -241,14 +241,25 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(DfDeltaPrefillArgs p, f
   const float qscale = sqrtf(static_cast<float>(kDk));
 
   // ---- normalised q, k rows; v rows; gates --------------------------------------------
-  for (int t = wave * 16; t < wave * 16 + 16; ++t) {
-    const int T = c0 + t;
-    float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
+  // wave w: tokens 16 w ..; all 16 tokens' loads are issued before any is used
+  uint32_t qkv[16][3];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int T = c0 + wave * 16 + i;
+    qkv[i][0] = qkv[i][1] = qkv[i][2] = 0u;
     if (T < p.tokens) {
       const uint16_t* row = p.mixed + (size_t)T * p.ld_mixed;
-      const uint32_t qw = *reinterpret_cast<const uint32_t*>(row + qoff + 2 * lane);
-      const uint32_t kw = *reinterpret_cast<const uint32_t*>(row + koff + 2 * lane);
-      const uint32_t vw = *reinterpret_cast<const uint32_t*>(row + voff + 2 * lane);
+      qkv[i][0] = *reinterpret_cast<const uint32_t*>(row + qoff + 2 * lane);
+      qkv[i][1] = *reinterpret_cast<const uint32_t*>(row + koff + 2 * lane);
+      qkv[i][2] = *reinterpret_cast<const uint32_t*>(row + voff + 2 * lane);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int t = wave * 16 + i;
+    float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
+    {
+      const uint32_t qw = qkv[i][0], kw = qkv[i][1], vw = qkv[i][2];
       q0 = __uint_as_float(qw << 16);
       q1 = __uint_as_float(qw & 0xFFFF0000u);
       k0 = __uint_as_float(kw << 16);
@@ -290,8 +301,21 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(DfDeltaPrefillArgs p, f
   __syncthreads();
 
   // ---- A' and QK (4 x 4 register tiles of the lower triangle) ---------------------------
+  // The 136 tiles (tb, jb <= tb) go to threads p = 4 lane + wave < 136, spread evenly over
+  // the waves; the other threads write the zero tiles above the diagonal.
   {
-    const int tb = tid >> 4, jb = tid & 15;
+    const int pidx = 4 * lane + wave;
+    int tb, jb;
+    if (pidx < 136) {
+      tb = 0;
+      while ((tb + 1) * (tb + 2) / 2 <= pidx) ++tb;
+      jb = pidx - tb * (tb + 1) / 2;
+    } else {  // upper tiles: 120 of them, for the 120 threads 136 .. 255
+      const int q = pidx - 136;  // (jb, tb) with tb < jb
+      jb = 1;
+      while (jb * (jb + 1) / 2 <= q) ++jb;
+      tb = q - jb * (jb - 1) / 2;
+    }
     float aa[4][4], qq[4][4];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -321,7 +345,7 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(DfDeltaPrefillArgs p, f
       for (int c = 0; c < 4; ++c) {
         const int t = tb * 4 + r, j = jb * 4 + c;
         const float d = j <= t ? expf(L.gam[t] - L.gam[j]) : 0.0f;
-        L.A[t][j] = j < t ? L.beta[t] * (aa[r][c] * d) : 0.0f;
+        L.At[j][t] = j < t ? L.beta[t] * (aa[r][c] * d) : 0.0f;
         L.QK[t][j] = j <= t ? qq[r][c] * d : 0.0f;
       }
   }
@@ -337,36 +361,38 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(DfDeltaPrefillArgs p, f
   __syncthreads();
 
   // ---- forward substitution: X_t = R_t - sum_{j<t} A'[t][j] X_j, in place --------------
-  // wave w solves columns 64 w .. 64 w + 63 of [V | K], eight at a time; lane = token.
+  // Lane = one of the 256 columns of [V | K] (wave w: columns 64 w ..), its 64 tokens in
+  // registers. Once token t is final, t's multiple is taken off every later token u, with
+  // A'[u][t] read from row t of At as uniform LDS broadcasts. Each token receives its terms in
+  // the order j = 0, 1, .. with the same fmaf as a token-by-token solve, but every step's
+  // updates are independent of each other.
   {
-    float arow[kCk];
-#pragma unroll
-    for (int j = 0; j < kCk; j += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(&L.A[lane][j]);
-      arow[j] = v.x; arow[j + 1] = v.y; arow[j + 2] = v.z; arow[j + 3] = v.w;
-    }
     float (*M)[kPitch] = wave < 2 ? L.V : L.K;
-    const int cbase = (wave & 1) * 64;
-#pragma unroll 1
-    for (int pass = 0; pass < 8; ++pass) {
-      const int col = cbase + pass * 8;
-      float acc[8];
+    const int col = (wave & 1) * 64 + lane;
+    float x[kCk];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) acc[c] = M[lane][col + c];
+    for (int t = 0; t < kCk; ++t) x[t] = M[t][col];
 #pragma unroll
-      for (int j = 0; j < kCk; ++j) {
+    for (int t = 0; t < kCk - 1; ++t) {
 #pragma unroll
-        for (int c = 0; c < 8; ++c) acc[c] = fmaf(-arow[j], readlane(acc[c], j), acc[c]);
+      for (int u4 = (t + 1) & ~3; u4 < kCk; u4 += 4) {
+        const float4 a = *reinterpret_cast<const float4*>(&L.At[t][u4]);
+        const float av[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (u4 + e > t) x[u4 + e] = fmaf(-av[e], x[t], x[u4 + e]);
       }
-#pragma unroll
-      for (int c = 0; c < 8; ++c) M[lane][col + c] = acc[c];
     }
+#pragma unroll
+    for (int t = 0; t < kCk; ++t) M[t][col] = x[t];
   }
   __syncthreads();
 
   // ---- O_loc = QK Wv and Qx = diag(e^gamma) Q - QK Wk; Wv, Wk out ----------------------
   {
-    const int t = tid >> 2, cs = (tid & 3) * 32;
+    // token t = 4 (li % 16) + wave for li = tid / 4: each wave gets every fourth token, so the
+    // triangular work (t + 1 terms) is spread evenly
+    const int li = tid >> 2, t = 4 * (li & 15) + wave, cs = (tid & 3) * 32;
     float o[32], qx[32];
 #pragma unroll
     for (int c = 0; c < 32; ++c) {
