@@ -426,82 +426,132 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(DfDeltaPrefillArgs p, f
   }
 }
 
-// The scan: one workgroup per (value head, 16 value columns), the state slice in LDS, the
-// chunks in order. Per chunk: O = O_loc + Qx S0 (tokens out as bf16), delta = Wv - Wk S0,
-// S = e^gamma_C S0 + Kd^T delta.
+// The scan: one workgroup per (value head, 16 value columns), the chunks in order. Per chunk:
+// O = O_loc + Qx S0 (tokens out as bf16), delta = Wv - Wk S0, S = e^gamma_C S0 + Kd^T delta,
+// all on the fp32 MFMA (v_mfma_f32_16x16x4_f32):
+// - O and delta: wave w owns tokens 16 w ..+15 (16 x 16 results over k = 128). Its A operands
+//   (rows of Qx and Wk) come straight from the pre-pass scratch; B is S, shared through LDS
+//   transposed (St[c][k]);
+// - the update: wave w owns state rows k = 32 w ..+31 (two 16 x 16 tiles over the 64 tokens),
+//   kept in registers in the MFMA result layout. A is Kd^T, read from the scratch; B is
+//   delta, shared through LDS transposed (Dt[c][t]).
+// Each lane takes k (or t) in runs of 4 (k = 16 s + 4 (lane / 16) + j for the MFMA j of
+// group s), so its operands are 16-byte loads. Every global operand of the next chunk is
+// loaded a chunk ahead (two register sets).
 constexpr int kScanVs = 16;
 
 struct ScanLds {
-  float S[kDk][kScanVs];
-  float Qx[kCk][kPitch];
-  float Wk[kCk][kPitch];
-  float Kd[kCk][kPitch];
-  float D[kCk][kScanVs + 1];
+  float St[kScanVs][kDk + 4];   // S0 transposed
+  float Dt[kScanVs][kCk + 4];   // delta transposed
 };
+
+struct ScanPre {                // one chunk's operands for one lane
+  float4 qa[8], wa[8];          // Qx, Wk: row 16 w + lane % 16, k = 16 s + 4 (lane / 16) ..+3
+  float kd[2][4][4];            // Kd[t = 16 s + 4 (lane / 16) + j][k = 32 w + 16 tile + lane % 16]
+  float ol[4], wv[4];           // O_loc, Wv at (16 w + 4 (lane / 16) + r, column lane % 16)
+};
+
+DF_DEVICE df_f32x4 mfma4(float a, float b, df_f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 
 __global__ __launch_bounds__(256) void delta_scan_kernel(DfDeltaPrefillArgs p, const float* __restrict__ scratch) {
   __shared__ __align__(16) ScanLds L;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = blockIdx.x, vs = blockIdx.y;
   const int col0 = vs * kScanVs;
   const int nchunks = (p.tokens + kCk - 1) / kCk;
+  const int n16 = lane & 15, q4 = lane >> 4;
   float* gstate = p.state + (size_t)h * kDk * kDk;
-  for (int e = tid; e < kDk * kScanVs; e += 256)
-    L.S[e / kScanVs][e % kScanVs] = gstate[(size_t)(e / kScanVs) * kDk + col0 + e % kScanVs];
   const float* ecs = scratch + (size_t)nchunks * p.num_v_heads * kPrepMats * kMat;
-  for (int chunk = 0; chunk < nchunks; ++chunk) {
+
+  // this wave's state rows in the MFMA result layout: S[32 w + 16 tile + 4 q4 + r][n16]
+  df_f32x4 S[2];
+#pragma unroll
+  for (int tl = 0; tl < 2; ++tl)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) S[tl][r] = gstate[(size_t)(32 * wave + 16 * tl + 4 * q4 + r) * kDk + col0 + n16];
+  auto put_state = [&]() {
+#pragma unroll
+    for (int tl = 0; tl < 2; ++tl)
+      *reinterpret_cast<float4*>(&L.St[n16][32 * wave + 16 * tl + 4 * q4]) = make_float4(S[tl][0], S[tl][1], S[tl][2], S[tl][3]);
+  };
+  auto fetch = [&](ScanPre& P, int chunk) {
     const float* base = scratch + prep_base(chunk, h, p.num_v_heads);
-    for (int e = tid; e < kMat / 4; e += 256) {  // Qx, Wk, Kd rows into LDS
-      const int t = (e * 4) / kDk, k = (e * 4) % kDk;
-      *reinterpret_cast<float4*>(&L.Qx[t][k]) = *reinterpret_cast<const float4*>(base + kMat + e * 4);
-      *reinterpret_cast<float4*>(&L.Wk[t][k]) = *reinterpret_cast<const float4*>(base + 3 * kMat + e * 4);
-      *reinterpret_cast<float4*>(&L.Kd[t][k]) = *reinterpret_cast<const float4*>(base + 4 * kMat + e * 4);
-    }
-    __syncthreads();
-    {  // O and delta: token t, columns cq .. cq + 3 of the slice
-      const int t = tid >> 2, cq = (tid & 3) * 4;
-      const float4 ol = *reinterpret_cast<const float4*>(base + (size_t)t * kDk + col0 + cq);
-      const float4 wv = *reinterpret_cast<const float4*>(base + 2 * kMat + (size_t)t * kDk + col0 + cq);
-      float o[4] = {ol.x, ol.y, ol.z, ol.w}, d[4] = {wv.x, wv.y, wv.z, wv.w};
-      for (int k = 0; k < kDk; k += 4) {
-        const float4 qv = *reinterpret_cast<const float4*>(&L.Qx[t][k]);
-        const float4 kv = *reinterpret_cast<const float4*>(&L.Wk[t][k]);
-        const float qq[4] = {qv.x, qv.y, qv.z, qv.w}, ww[4] = {kv.x, kv.y, kv.z, kv.w};
+    const int row = 16 * wave + n16;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float4 sv = *reinterpret_cast<const float4*>(&L.S[k + e][cq]);
-          o[0] += qq[e] * sv.x; o[1] += qq[e] * sv.y; o[2] += qq[e] * sv.z; o[3] += qq[e] * sv.w;
-          d[0] -= ww[e] * sv.x; d[1] -= ww[e] * sv.y; d[2] -= ww[e] * sv.z; d[3] -= ww[e] * sv.w;
-        }
+    for (int sg = 0; sg < 8; ++sg) {
+      P.qa[sg] = *reinterpret_cast<const float4*>(base + kMat + (size_t)row * kDk + 16 * sg + 4 * q4);
+      P.wa[sg] = *reinterpret_cast<const float4*>(base + 3 * kMat + (size_t)row * kDk + 16 * sg + 4 * q4);
+    }
+#pragma unroll
+    for (int tl = 0; tl < 2; ++tl)
+#pragma unroll
+      for (int sg = 0; sg < 4; ++sg)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          P.kd[tl][sg][j] = base[4 * kMat + (size_t)(16 * sg + 4 * q4 + j) * kDk + 32 * wave + 16 * tl + n16];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const size_t e = (size_t)(16 * wave + 4 * q4 + r) * kDk + col0 + n16;
+      P.ol[r] = base[e];
+      P.wv[r] = base[2 * kMat + e];
+    }
+  };
+  auto step = [&](const ScanPre& P, ScanPre& N, int chunk) {
+    __syncthreads();  // St holds this chunk's S0
+    if (chunk + 1 < nchunks) fetch(N, chunk + 1);
+    // O and delta for tokens 16 w + 4 q4 + r, column n16
+    df_f32x4 o = {P.ol[0], P.ol[1], P.ol[2], P.ol[3]}, d = {P.wv[0], P.wv[1], P.wv[2], P.wv[3]};
+    df_f32x4 qs = {0.f, 0.f, 0.f, 0.f}, ws = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sg = 0; sg < 8; ++sg) {
+      const float4 b = *reinterpret_cast<const float4*>(&L.St[n16][16 * sg + 4 * q4]);
+      qs = mfma4(P.qa[sg].x, b.x, qs);
+      qs = mfma4(P.qa[sg].y, b.y, qs);
+      qs = mfma4(P.qa[sg].z, b.z, qs);
+      qs = mfma4(P.qa[sg].w, b.w, qs);
+      ws = mfma4(P.wa[sg].x, b.x, ws);
+      ws = mfma4(P.wa[sg].y, b.y, ws);
+      ws = mfma4(P.wa[sg].z, b.z, ws);
+      ws = mfma4(P.wa[sg].w, b.w, ws);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      o[r] += qs[r];
+      d[r] -= ws[r];
+      const int T = chunk * kCk + 16 * wave + 4 * q4 + r;
+      if (T < p.tokens) p.out[(size_t)T * p.ld_out + h * kDk + col0 + n16] = f2bf(o[r]);
+    }
+    *reinterpret_cast<float4*>(&L.Dt[n16][16 * wave + 4 * q4]) = make_float4(d[0], d[1], d[2], d[3]);
+    __syncthreads();  // Dt complete; every wave is done reading St
+    // S <- e^gamma_C S0 + Kd^T delta
+    const float ec = ecs[(size_t)chunk * p.num_v_heads + h];
+#pragma unroll
+    for (int tl = 0; tl < 2; ++tl) {
+      df_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int sg = 0; sg < 4; ++sg) {
+        const float4 b = *reinterpret_cast<const float4*>(&L.Dt[n16][16 * sg + 4 * q4]);
+        acc = mfma4(P.kd[tl][sg][0], b.x, acc);
+        acc = mfma4(P.kd[tl][sg][1], b.y, acc);
+        acc = mfma4(P.kd[tl][sg][2], b.z, acc);
+        acc = mfma4(P.kd[tl][sg][3], b.w, acc);
       }
 #pragma unroll
-      for (int c = 0; c < 4; ++c) L.D[t][cq + c] = d[c];
-      const int T = chunk * kCk + t;
-      if (T < p.tokens) {
-        *reinterpret_cast<uint2*>(p.out + (size_t)T * p.ld_out + h * kDk + col0 + cq) =
-            make_uint2(static_cast<uint32_t>(f2bf(o[0])) | (static_cast<uint32_t>(f2bf(o[1])) << 16),
-                       static_cast<uint32_t>(f2bf(o[2])) | (static_cast<uint32_t>(f2bf(o[3])) << 16));
-      }
+      for (int r = 0; r < 4; ++r) S[tl][r] = ec * S[tl][r] + acc[r];
     }
-    __syncthreads();
-    {  // S <- e^gamma_C S0 + Kd^T delta: row k, columns c8 .. c8 + 7
-      const int k = tid >> 1, c8 = (tid & 1) * 8;
-      const float ec = ecs[(size_t)chunk * p.num_v_heads + h];
-      float acc[8];
-#pragma unroll
-      for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
-      for (int j = 0; j < kCk; ++j) {
-        const float kd = L.Kd[j][k];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) acc[c] += kd * L.D[j][c8 + c];
-      }
-#pragma unroll
-      for (int c = 0; c < 8; ++c) L.S[k][c8 + c] = ec * L.S[k][c8 + c] + acc[c];
-    }
-    __syncthreads();
+    put_state();
+  };
+  put_state();
+  ScanPre A, B;
+  fetch(A, 0);
+  for (int chunk = 0; chunk < nchunks; chunk += 2) {
+    step(A, B, chunk);
+    if (chunk + 1 < nchunks) step(B, A, chunk + 1);
   }
-  for (int e = tid; e < kDk * kScanVs; e += 256)
-    gstate[(size_t)(e / kScanVs) * kDk + col0 + e % kScanVs] = L.S[e / kScanVs][e % kScanVs];
+#pragma unroll
+  for (int tl = 0; tl < 2; ++tl)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) gstate[(size_t)(32 * wave + 16 * tl + 4 * q4 + r) * kDk + col0 + n16] = S[tl][r];
 }
 
 // ---------------------------------------------------------------------------------------
