@@ -698,14 +698,48 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(DfAttnPrefillArgs 
     l[r] = 0.0f;
   }
 
-  auto stage_k = [&](int kb) {
+  // Key block kb's K (and V) rows: loaded into registers one block ahead, stored into LDS
+  // once the previous block's products are done with it. V is stored transposed (Vt[d][key],
+  // the B operand of p V): thread (dim pair dp = tid % 128, half kh = tid / 128) loads dims
+  // 2 dp, 2 dp + 1 of keys 32 kh + 8 q + j (4-byte loads, coalesced across the lanes) and
+  // writes each dim's 8 keys with one 16-byte store.
+  uint4 kr[8];
+  uint32_t vr[32];
+  auto load_rows = [&](uint4 (&rr)[8], const uint16_t* src, int kb) {  // K rows
 #pragma unroll
     for (int i = 0; i < 8; ++i) {  // 64 keys x 32 chunks of 16 bytes
       const int ch = tid + 256 * i, key = ch >> 5, cc = ch & 31;
       const int kg = kb * kAtKeys + key;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (kg < nkeys) v = *reinterpret_cast<const uint4*>(kbase + (size_t)kg * kHd + cc * 8);
-      *reinterpret_cast<uint4*>(&Ks[key * kKsPitch + cc * 8]) = v;
+      rr[i] = make_uint4(0u, 0u, 0u, 0u);
+      if (kg < nkeys) rr[i] = *reinterpret_cast<const uint4*>(src + (size_t)kg * kHd + cc * 8);
+    }
+  };
+  auto put_k = [&]() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int ch = tid + 256 * i, key = ch >> 5, cc = ch & 31;
+      *reinterpret_cast<uint4*>(&Ks[key * kKsPitch + cc * 8]) = kr[i];
+    }
+  };
+  const int vdp = tid & 127, vkh = tid >> 7;
+  auto load_v = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const int kg = kb * kAtKeys + 32 * vkh + i;
+      vr[i] = kg < nkeys ? *reinterpret_cast<const uint32_t*>(vbase + (size_t)kg * kHd + 2 * vdp) : 0u;
+    }
+  };
+  auto put_v = [&]() {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t* w = vr + 8 * q;
+      const uint4 lo = make_uint4((w[0] & 0xFFFFu) | (w[1] << 16), (w[2] & 0xFFFFu) | (w[3] << 16),
+                                  (w[4] & 0xFFFFu) | (w[5] << 16), (w[6] & 0xFFFFu) | (w[7] << 16));
+      const uint4 hi = make_uint4((w[0] >> 16) | (w[1] & 0xFFFF0000u), (w[2] >> 16) | (w[3] & 0xFFFF0000u),
+                                  (w[4] >> 16) | (w[5] & 0xFFFF0000u), (w[6] >> 16) | (w[7] & 0xFFFF0000u));
+      const int key0 = 32 * vkh + 8 * q;
+      *reinterpret_cast<uint4*>(&Vt[(2 * vdp) * kVtPitch + key0]) = lo;
+      *reinterpret_cast<uint4*>(&Vt[(2 * vdp + 1) * kVtPitch + key0]) = hi;
     }
   };
   // scores of key block kb for this lane: s[sb][r] (key kb*64 + 16 sb + lane % 16)
@@ -728,9 +762,11 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(DfAttnPrefillArgs 
   };
 
   // ---- pass 1: row max and sum --------------------------------------------------------
+  load_rows(kr, kbase, 0);
   for (int kb = 0; kb < nkb; ++kb) {
-    stage_k(kb);
+    put_k();
     __syncthreads();
+    if (kb + 1 < nkb) load_rows(kr, kbase, kb + 1);
     float s[4][4];
     scores(kb, s);
 #pragma unroll
@@ -755,20 +791,16 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(DfAttnPrefillArgs 
 #pragma unroll
   for (int db = 0; db < 16; ++db) o[db] = df_f32x4{0.f, 0.f, 0.f, 0.f};
   uint16_t* pt = Pt[wave];
+  load_rows(kr, kbase, 0);
+  load_v(0);
   for (int kb = 0; kb < nkb; ++kb) {
-    stage_k(kb);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {  // V transposed: Vt[d][key]
-      const int ch = tid + 256 * i, key = ch >> 5, cc = ch & 31;
-      const int kg = kb * kAtKeys + key;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (kg < nkeys) v = *reinterpret_cast<const uint4*>(vbase + (size_t)kg * kHd + cc * 8);
-      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        Vt[(cc * 8 + e) * kVtPitch + key] = static_cast<uint16_t>(vw[e >> 1] >> (16 * (e & 1)));
-    }
+    put_k();
+    put_v();
     __syncthreads();
+    if (kb + 1 < nkb) {
+      load_rows(kr, kbase, kb + 1);
+      load_v(kb + 1);
+    }
     float s[4][4];
     scores(kb, s);
 #pragma unroll
