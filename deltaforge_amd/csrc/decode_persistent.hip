@@ -31,12 +31,16 @@
 // ds_read so the compiler does not insert a vmcnt(0) before them (it cannot tell which
 // slot a DMA targets); the kernel waits explicitly for exactly the block it consumes.
 //
-// GEMV arithmetic. A block's B operand is bf16(128 + nibble) (exact, the nibble in the low
-// mantissa bits), built in 7 VALU ops per 8 weights; per 128-group the MFMA gives
-// D = sum x_k (128 + n_k), and y += s * (D - 136 * sum x_k) = s * sum x_k (n_k - 8). This is
-// the reference's sum x_k * ((n_k - 8) * s) with the scale applied once per group instead of
-// rounding each weight to bf16 first: the per-weight bf16 rounding the reference does
-// (relative 2^-9) is not reproduced, which moves outputs by well under the bf16 tolerance.
+// GEMV arithmetic (fp16 MFMA). A block's B operand holds each nibble in the mantissa of an
+// fp16 with exponent 2^10: 1024 + n (nibble in bits 0..3 of a half) or 1024 + 16 n (bits
+// 4..7), so one shift and four v_and_or build 8 weights from a dword (5 VALU ops). The input
+// row is staged in fp16 as x' = x, or x / 16 at the 1024 + 16 n positions (k % 8 in 2, 3, 6,
+// 7); bf16 activations are exact in fp16 within its normal range. Per 128-group the MFMA gives
+// D = sum x'_k B_k = sum x_k n_k + 1024 sum x'_k, and y += s * (D - xs) with the staged
+// xs = 1024 sum x'_k + 8 sum x_k, i.e. y += s * sum x_k (n_k - 8). This is the reference's
+// sum x_k * ((n_k - 8) * s) with the scale applied once per group instead of rounding each
+// weight to bf16 first: the per-weight bf16 rounding the reference does (relative 2^-9) is
+// not reproduced, which moves outputs by well under the bf16 tolerance.
 //
 // Other arithmetic is the per-op kernels' (gated_delta.hip, attention.hip, small_ops.hip),
 // with the reference's rounding points; only fp32 summation orders differ.
@@ -81,9 +85,17 @@ constexpr int kTileKeys = kCompute * 16;            // 128 keys per attention ti
 constexpr int kSplits = 2 * kPerXcd;                // key splits of a KV head over its XCD pair
 constexpr int kPairHeads = 4;                       // query heads of a KV head (2 per XCD of the pair);
                                                     // an XCD's own two are its slots 0, 1
-// factored int4 dot product: B = bf16(128 + n), n - 8 = B - 136
-constexpr uint32_t kBiasPair = 0x43004300u;         // bf16 128.0 in both halves
-constexpr float kBias = 136.0f;
+// factored int4 dot product: B = fp16(1024 + n) or fp16(1024 + 16 n) (see the file comment)
+constexpr uint32_t kBiasPair = 0x64006400u;         // fp16 1024.0 in both halves
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 df_f16x8;
+
+// The fp16 GEMV input x' of element k (x / 16 where the weight enters as 1024 + 16 n), and
+// its term of the group correction xs = 1024 sum x' + 8 sum x.
+DF_DEVICE _Float16 xh_of(float x, int k) { return static_cast<_Float16>((k & 2) ? x * 0.0625f : x); }
+DF_DEVICE float xs_term(float x, _Float16 xh) { return 1024.0f * static_cast<float>(xh) + 8.0f * x; }
+DF_DEVICE uint32_t pack_h2(_Float16 a, _Float16 b) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) | (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+}
 
 constexpr uint64_t kTimeout = 50000000ull;          // 0.5 s of s_memrealtime (100 MHz)
 constexpr int kRegBase = 4;                         // ctl[4..11]: per-XCD registration tickets
@@ -239,14 +251,15 @@ DF_DEVICE float row_sum_mod4(float v) {
 
 __shared__ __align__(16) uint4 g_ring_w[kCompute][kRing][64];     // 1 KB blocks
 __shared__ __align__(16) uint32_t g_ring_s[kCompute][kRing][16];  // scale dword of lane i < 16: columns (i & 14), +1
-__shared__ __align__(16) uint16_t g_x[kMaxHidden + 8];            // GEMV input row (bf16)
+__shared__ __align__(16) uint16_t g_x[kMaxHidden + 8];            // the staged core (bf16), GatedRMSNorm's input
+__shared__ __align__(16) uint16_t g_xh[kMaxHidden + 8];           // GEMV input row x' (fp16)
 
 struct Lds {
   __align__(16) uint16_t h[kMaxHidden];          // the hidden vector (bf16)
   __align__(16) uint16_t nw[kMaxHidden];         // the next RMSNorm's weight (LDS DMA, a phase ahead)
   __align__(16) uint16_t gnw[kDk];               // GatedRMSNorm weight (LDS DMA, a phase ahead)
   __align__(16) float zs[512];                   // out_proj: SiLU inputs of the GatedRMSNorm (staged during delta)
-  float xs[kMaxGroups];                          // 136 * sum of each 128-group of g_x
+  float xs[kMaxGroups];                          // each 128-group's 1024 sum x' + 8 sum x
   float ss;                                      // sum of squares of h (for the next RMSNorm)
   __align__(16) float part[kMaxWgTiles][16][kCompute];  // per-wave tile partials (a column's 8 adjacent)
   float red[64];
@@ -323,7 +336,7 @@ constexpr int kMaxLayers = 32;
 static_assert(sizeof(DfPersistLayer) % 8 == 0, "layer table copied in 8-byte words");
 __shared__ __align__(16) DfPersistLayer g_layers[kMaxLayers];
 
-constexpr size_t kLdsBytes = sizeof(Lds) + sizeof(g_ring_w) + sizeof(g_ring_s) + sizeof(g_x) + sizeof(g_layers);
+constexpr size_t kLdsBytes = sizeof(Lds) + sizeof(g_ring_w) + sizeof(g_ring_s) + sizeof(g_x) + sizeof(g_xh) + sizeof(g_layers);
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
 
 typedef const DfPersistLayer* LayerPtr;  // points into g_layers
@@ -475,8 +488,8 @@ DF_DEVICE bool poll_tagged(const Ctx& c, F&& load) {
 // GEMV input rows
 // ---------------------------------------------------------------------------------------
 
-// Compute waves (1 barrier; the control wave passes 1): g_x = bf16(RMSNorm(h) * (1 + w))
-// over `hidden` (w staged in L.nw) and the group sums L.xs. Every wave sums the squares of
+// Compute waves (1 barrier; the control wave passes 1): x = bf16(RMSNorm(h) * (1 + w)) over
+// `hidden` (w staged in L.nw) as the fp16 row g_xh, and the group corrections L.xs. Every wave sums the squares of
 // all of h itself (identical code and order in every wave, so all agree on the factor), which
 // saves the cross-wave exchange and its barrier; a wave then produces whole 128-groups
 // (2 elements per lane).
@@ -488,11 +501,12 @@ DF_DEVICE void norm_w(Lds& L, Ctx& c, int hidden, float eps) {
     const int k = g * kGroup + 2 * c.lane;
     const uint32_t hv = *reinterpret_cast<const uint32_t*>(&L.h[k]);
     const uint32_t wv = *reinterpret_cast<const uint32_t*>(&L.nw[k]);
-    const uint16_t b0 = f2bf(__uint_as_float(hv << 16) * r * (1.0f + __uint_as_float(wv << 16)));
-    const uint16_t b1 = f2bf(__uint_as_float(hv & 0xFFFF0000u) * r * (1.0f + __uint_as_float(wv & 0xFFFF0000u)));
-    *reinterpret_cast<uint32_t*>(&g_x[k]) = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
-    const float sg = dsum(bf2f(b0) + bf2f(b1));
-    if (c.lane == 0) L.xs[g] = kBias * sg;
+    const float x0 = round_bf(__uint_as_float(hv << 16) * r * (1.0f + __uint_as_float(wv << 16)));
+    const float x1 = round_bf(__uint_as_float(hv & 0xFFFF0000u) * r * (1.0f + __uint_as_float(wv & 0xFFFF0000u)));
+    const _Float16 h0 = xh_of(x0, k), h1 = xh_of(x1, k + 1);
+    *reinterpret_cast<uint32_t*>(&g_xh[k]) = pack_h2(h0, h1);
+    const float sg = dsum(xs_term(x0, h0) + xs_term(x1, h1));
+    if (c.lane == 0) L.xs[g] = sg;
   }
   sync(c);
 }
@@ -864,30 +878,28 @@ DF_DEVICE void take_pair(Stream& st, const Ctx& c, const uint16_t* xg0, const ui
   st.rslot = next_slot(next_slot(st.rslot));
 }
 
-// Two weights k = 2j, 2j+1 of a dword (nibbles at bits 4j and 16 + 4j) as bf16(128 + n):
-// ((w >> 4j) & mask) | bias. The mask and bias arrive as opaque register values (mask in an
-// SGPR, bias in a VGPR), so the compiler emits one v_and_or_b32 (gfx9 VOP3 encodes no
-// literal) and its hazard checks still cover the result, which feeds an MFMA.
-DF_DEVICE uint32_t bias_pair(uint32_t w, int j, uint32_t mask, uint32_t bias) {
-  return ((j == 0 ? w : w >> (4 * j)) & mask) | bias;
-}
-
 // Row 0 of one block's product: lanes 0..15 return s_col * sum_k x_k (n_k - 8) over the
-// block's 128 k (x = the group's input chunks at this lane's k slot, xs = 136 * the group's
-// sum, sh = 16 * (lane & 1) selects this lane's scale in the dword).
+// block's 128 k (x = the group's fp16 input chunks x' at this lane's k slot, xs = the group's
+// correction, sh = 16 * (lane & 1) selects this lane's scale in the dword). A dword's nibble
+// pairs (bits 4j, 16 + 4j) become the fp16 pairs (w & m_lo) | bias, (w & m_hi) | bias,
+// ((w >> 8) & m_lo) | bias, ((w >> 8) & m_hi) | bias: weights 1024 + n for k % 8 in 0, 1, 4, 5
+// and 1024 + 16 n for k % 8 in 2, 3, 6, 7. The masks and bias arrive as opaque register values
+// (masks in SGPRs, bias in a VGPR), so the compiler emits one v_and_or_b32 each (gfx9 VOP3
+// encodes no literal) and its hazard checks still cover the results, which feed an MFMA.
 DF_DEVICE float block_dot_r(const uint4& wv, uint32_t sd, const uint4 (&x)[4], float xs, uint32_t sh) {
   const float s = __uint_as_float((sd >> sh) << 16);
   const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
-  uint32_t mask = 0x000F000Fu, bias = kBiasPair;
-  asm("" : "+s"(mask));
+  uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, bias = kBiasPair;
+  asm("" : "+s"(mlo));
+  asm("" : "+s"(mhi));
   asm("" : "+v"(bias));
   df_f32x4 d4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    const uint4 bw = make_uint4(bias_pair(words[d], 0, mask, bias), bias_pair(words[d], 1, mask, bias),
-                                bias_pair(words[d], 2, mask, bias), bias_pair(words[d], 3, mask, bias));
-    d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, x[d]), __builtin_bit_cast(df_bf16x8, bw),
-                                                 d4, 0, 0, 0);
+    const uint32_t w = words[d], t = w >> 8;
+    const uint4 bw = make_uint4((w & mlo) | bias, (w & mhi) | bias, (t & mlo) | bias, (t & mhi) | bias);
+    d4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(df_f16x8, x[d]), __builtin_bit_cast(df_f16x8, bw),
+                                                d4, 0, 0, 0);
   }
   return s * (d4[0] - xs);
 }
@@ -910,7 +922,7 @@ DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPer
   // this wave's partial of every tile starts at zero (only this wave writes its column, and
   // the control wave read the previous phase's partials before the barrier that began this one)
   for (int e = c.lane; e < kMaxWgTiles * 16; e += 64) L.part[e / 16][e % 16][c.wave] = 0.0f;
-  const uint16_t* xb = g_x + (c.lane >> 4) * 32;
+  const uint16_t* xb = g_xh + (c.lane >> 4) * 32;
   int tr = lo / g.ng - g.b_lo / g.ng;
   int gl = lo % g.ng;
   float acc = 0.0f;
@@ -1147,7 +1159,7 @@ DF_DEVICE void stage_gu(const Ctx& c, int inter_x, float* gu) {
 }
 
 // Compute waves (1 barrier; the control wave passes 1): the down projection's input
-// act = bf16(bf16(silu(g)) * u) into g_x and its group sums L.xs. The gate|up columns come
+// act = bf16(bf16(silu(g)) * u) as the fp16 row g_xh, and its group corrections L.xs. The gate|up columns come
 // in 32-column pairs (16 gate columns, then their 16 up columns), so act j reads gate
 // column 32 (j / 16) + j % 16 and the up column 16 further. A wave produces whole
 // 128-groups (2 elements per lane).
@@ -1159,19 +1171,21 @@ DF_DEVICE void swiglu_act(Lds& L, Ctx& c, int inter_x) {
     const int col = (j >> 4) * 32 + (j & 15);
     const float2 gv = *reinterpret_cast<const float2*>(gu + col);
     const float2 uv = *reinterpret_cast<const float2*>(gu + col + 16);
-    const uint16_t b0 = f2bf(round_bf(silu(round_bf(gv.x))) * round_bf(uv.x));
-    const uint16_t b1 = f2bf(round_bf(silu(round_bf(gv.y))) * round_bf(uv.y));
-    *reinterpret_cast<uint32_t*>(&g_x[j]) = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
-    const float sg = dsum(bf2f(b0) + bf2f(b1));
-    if (c.lane == 0) L.xs[g] = kBias * sg;
+    const float x0 = round_bf(round_bf(silu(round_bf(gv.x))) * round_bf(uv.x));
+    const float x1 = round_bf(round_bf(silu(round_bf(gv.y))) * round_bf(uv.y));
+    const _Float16 h0 = xh_of(x0, j), h1 = xh_of(x1, j + 1);
+    *reinterpret_cast<uint32_t*>(&g_xh[j]) = pack_h2(h0, h1);
+    const float sg = dsum(xs_term(x0, h0) + xs_term(x1, h1));
+    if (c.lane == 0) L.xs[g] = sg;
   }
   sync(c);
 }
 
 // Control wave: the XCD's 512 merged attention / delta outputs (tagged bf16, published by the
-// workgroups of the XCD at epoch `want`) into g_x, with the group sums L.xs of its four
-// 128-groups when `sums` (a group is one 16-lane row of 8 values per lane).
-DF_DEVICE bool stage_core(Lds& L, const Ctx& c, uint32_t want, bool sums) {
+// workgroups of the XCD at epoch `want`) into g_x (the GatedRMSNorm's input) or, as the GEMV
+// input itself (`direct`), into g_xh with the group corrections L.xs of its four 128-groups
+// (a group is one 16-lane row of 8 values per lane).
+DF_DEVICE bool stage_core(Lds& L, const Ctx& c, uint32_t want, bool direct) {
   const auto r = rsrc(c.w.core + (size_t)c.xcd * 512);
   uint4 v0, v1;
   if (!poll_tagged(c, [&]() {
@@ -1182,14 +1196,22 @@ DF_DEVICE bool stage_core(Lds& L, const Ctx& c, uint32_t want, bool sums) {
     return false;
   const uint4 v = make_uint4((v0.x & 0xFFFFu) | (v0.y << 16), (v0.z & 0xFFFFu) | (v0.w << 16),
                              (v1.x & 0xFFFFu) | (v1.y << 16), (v1.z & 0xFFFFu) | (v1.w << 16));
-  *reinterpret_cast<uint4*>(&g_x[c.lane * 8]) = v;
-  if (sums) {
+  if (!direct) {
+    *reinterpret_cast<uint4*>(&g_x[c.lane * 8]) = v;
+  } else {
     float s = 0.0f;
+    uint32_t hw[4];
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) s += __uint_as_float(w[e] << 16) + __uint_as_float(w[e] & 0xFFFF0000u);
+    for (int e = 0; e < 4; ++e) {  // elements 8 lane + 2 e, + 1
+      const float x0 = __uint_as_float(w[e] << 16), x1 = __uint_as_float(w[e] & 0xFFFF0000u);
+      const _Float16 h0 = xh_of(x0, 2 * e), h1 = xh_of(x1, 2 * e + 1);
+      hw[e] = pack_h2(h0, h1);
+      s += xs_term(x0, h0) + xs_term(x1, h1);
+    }
+    *reinterpret_cast<uint4*>(&g_xh[c.lane * 8]) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
     s = row_sum(s);
-    if ((c.lane & 15) == 0) L.xs[c.lane >> 4] = kBias * s;
+    if ((c.lane & 15) == 0) L.xs[c.lane >> 4] = s;
   }
   return true;
 }
@@ -1860,12 +1882,13 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
             const float rr = 1.0f / sqrtf(tot / 128.0f + M.eps);
             const float t0 = round_bf(bf2f(L.gnw[c.lane]) * round_bf(v0 * rr));
             const float t1 = round_bf(bf2f(L.gnw[64 + c.lane]) * round_bf(v1 * rr));
-            const uint16_t xb0 = f2bf(t0 * silu(L.zs[i0]));
-            const uint16_t xb1 = f2bf(t1 * silu(L.zs[i1]));
-            g_x[i0] = xb0;
-            g_x[i1] = xb1;
-            const float gs = dsum(bf2f(xb0)) + dsum(bf2f(xb1));
-            if (c.lane == 0) L.xs[c.wave] = kBias * gs;
+            const float xv0 = round_bf(t0 * silu(L.zs[i0]));
+            const float xv1 = round_bf(t1 * silu(L.zs[i1]));
+            const _Float16 h0 = xh_of(xv0, i0), h1 = xh_of(xv1, i1);
+            g_xh[i0] = __builtin_bit_cast(uint16_t, h0);
+            g_xh[i1] = __builtin_bit_cast(uint16_t, h1);
+            const float gs = dsum(xs_term(xv0, h0)) + dsum(xs_term(xv1, h1));
+            if (c.lane == 0) L.xs[c.wave] = gs;
           }
           sync(c);
           gemv_consume(g, c, st, M, q, steps, L);
@@ -2078,7 +2101,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       norm_w(L, c, hidden, M.eps);
       // tiles t_lo + wave + 8 j, all groups, from the weight stream
       const int ntw = head_tiles_of_wave(q, c.wave);
-      const uint16_t* xb = g_x + (c.lane >> 4) * 32;
+      const uint16_t* xb = g_xh + (c.lane >> 4) * 32;
       const uint32_t sh = 16u * (c.lane & 1);
       float bv = -INFINITY;
       int bi = 0x7FFFFFFF;
