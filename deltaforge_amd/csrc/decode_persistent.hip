@@ -569,10 +569,19 @@ DF_DEVICE Gemv gemv_of(LayerPtr Lp, const Geo& q, int k, int xcd, int r) {
   return g;
 }
 
+// A compute wave's share of a workgroup's blocks. Wave w runs on SIMD w % 4, so waves 4..7
+// share their SIMD with the older waves 0..3, which win the issue arbitration: with equal
+// shares the younger waves finished 15-25 % later and the phase waited for them while each
+// SIMD ran one wave. Shares of 5 : 4 (waves 0..3 : 4..7) let both halves finish together.
+constexpr int kShareOld = 5, kShareYoung = 4, kShares = 4 * (kShareOld + kShareYoung);
+static_assert(kCompute == 8, "two waves per SIMD");
+DF_DEVICE int share_before(int wave) {
+  return wave <= 4 ? kShareOld * wave : 4 * kShareOld + kShareYoung * (wave - 4);
+}
 DF_DEVICE void wave_range(const Gemv& g, int wave, int& lo, int& n) {
   const int len = g.b_hi - g.b_lo;
-  lo = g.b_lo + (len * wave) / kCompute;
-  n = g.b_lo + (len * (wave + 1)) / kCompute - lo;
+  lo = g.b_lo + (len * share_before(wave)) / kShares;
+  n = g.b_lo + (len * share_before(wave + 1)) / kShares - lo;
 }
 
 DF_DEVICE int head_tiles_of_wave(const Geo& q, int wave) {
