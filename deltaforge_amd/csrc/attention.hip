@@ -13,10 +13,11 @@
 //   per tile  64 keys: QK on MFMA (16x16x32 bf16, query heads as rows, keys as columns,
 //             fp32 scores x head_dim^-0.5); fp32 online softmax per head; PV on VALU
 //             with each lane owning 4 output dims for all 4 heads.
-//   merge     each split writes (acc[256], m, l) per head with write-through stores; the
-//             last workgroup of the KV head (atomic counter) combines the splits in split order with the
-//             log-sum-exp identity (flash_decode_splitkv.py:135-174), rounds to bf16 and
-//             applies the bf16 output gate (reference.py:558-568, 674-676).
+//   merge     each split writes (acc[256], m, l) per head with write-through stores; a second
+//             kernel (attn_merge_kernel: one workgroup per batch row, query head and 64 output
+//             dims, its 4 waves splitting the splits) combines them with the log-sum-exp
+//             identity (flash_decode_splitkv.py:135-174), rounds to bf16 and applies the bf16
+//             output gate (reference.py:558-568, 674-676). A single split finishes in place.
 //
 // Scores and probabilities stay fp32 (the reference rounds both to bf16); this is the
 // more accurate function and is checked against the reference within tolerance.
@@ -33,24 +34,15 @@ constexpr int kTile = 64;
 constexpr int kMaxSplits = 256;
 
 struct AttnWs {
-  int* counters;
   float* acc;  // [B][Hq][S][256]
   float* ml;   // [B][Hq][S][2]
 };
 
-// Workspace layout: a fixed block of merge counters, then the partials. The counter block has
-// the same size and place for every call shape: the kernel leaves its counters at zero, and a
-// workspace reused by a call of another shape must find zeros there, not an earlier call's
-// partials (with a shape-sized counter block, a later call with more (batch, KV head) pairs
-// read a previous call's partials as counters, and its merge never ran).
-constexpr int kMaxCounters = 4096;  // batch * num_kv_heads per launch
-constexpr size_t kCounterBytes = kMaxCounters * sizeof(int);
-
+// Workspace layout: the split partials only. Every call writes all of its partials before
+// the merge kernel reads them, so a workspace needs no clearing and serves calls of any shape.
 inline AttnWs attn_ws(void* base, int batch, int hq, int splits) {
   AttnWs w;
-  char* p = reinterpret_cast<char*>(base);
-  w.counters = reinterpret_cast<int*>(p);
-  w.acc = reinterpret_cast<float*>(p + kCounterBytes);
+  w.acc = reinterpret_cast<float*>(base);
   w.ml = w.acc + (size_t)batch * hq * splits * kHd;
   return w;
 }
@@ -104,7 +96,6 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
   __shared__ float alpha_s[kQPerKv];
   __shared__ float red[kQPerKv][kQPerKv][kHd];
   __shared__ float ml_s[kQPerKv][2];
-  __shared__ int last_s;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -168,20 +159,31 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
     for (int i = 0; i < 4; ++i) acc[h][i] = 0.0f;
 
   for (int t0 = j0; t0 < j1; t0 += kTile) {
+    // The tile's K and V rows, all loads issued before any is used (one memory round trip):
+    // keys past the split load row j1 - 1 instead (in bounds, ignored), and the new
+    // position's row is replaced by the staged key / value.
+    uint4 kb[8];
+    uint2 vb[16];
+    {
+      const int krow = min(t0 + wave * 16 + col, j1 - 1);
+      const uint16_t* kp = p.k_cache + (kv_base + krow) * kHd + slot * 8;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) kb[d] = *reinterpret_cast<const uint4*>(kp + d * 32);
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const int vrow = min(t0 + wave * 16 + jj, j1 - 1);
+        vb[jj] = *reinterpret_cast<const uint2*>(p.v_cache + (kv_base + vrow) * kHd + lane * 4);
+      }
+    }
     // QK: wave covers keys t0 + 16*wave + col.
     {
       const int key = t0 + wave * 16 + col;
       const bool live = key < j1;
-      const int krow = min(key, p.max_len - 1);
-      const uint16_t* kp = p.k_cache + (kv_base + krow) * kHd + slot * 8;
       df_f32x4 d4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
         uint4 bw = make_uint4(0u, 0u, 0u, 0u);
-        if (live) {
-          bw = key == pos ? *reinterpret_cast<const uint4*>(knew + d * 32 + slot * 8)
-                          : *reinterpret_cast<const uint4*>(kp + d * 32);
-        }
+        if (live) bw = key == pos ? *reinterpret_cast<const uint4*>(knew + d * 32 + slot * 8) : kb[d];
         uint4 aw = make_uint4(0u, 0u, 0u, 0u);
         if (col < kQPerKv) aw = *reinterpret_cast<const uint4*>(&q_s[col][d * 32 + slot * 8]);
         d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, aw),
@@ -217,12 +219,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[h][i] *= a;
       }
+      const uint2 vn = *reinterpret_cast<const uint2*>(vnew + lane * 4);
+#pragma unroll
       for (int jj = 0; jj < 16; ++jj) {
         const int key = t0 + wave * 16 + jj;
         if (key >= j1) break;
-        uint2 raw;
-        if (key == pos) raw = *reinterpret_cast<const uint2*>(vnew + lane * 4);
-        else raw = *reinterpret_cast<const uint2*>(p.v_cache + (kv_base + key) * kHd + lane * 4);
+        const uint2 raw = key == pos ? vn : vb[jj];
         const float v0 = __uint_as_float(raw.x << 16), v1 = __uint_as_float(raw.x & 0xFFFF0000u);
         const float v2 = __uint_as_float(raw.y << 16), v3 = __uint_as_float(raw.y & 0xFFFF0000u);
 #pragma unroll
@@ -259,20 +261,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
       store_through(ws.ml + row * 2 + 1, ml_s[h][1]);
     }
   }
-  if (S > 1) {
-    publish_wait();
-    __syncthreads();
-    if (tid == 0) last_s = arrive(ws.counters + b * p.num_kv_heads + kvh) == S - 1;
-    __syncthreads();
-    if (!last_s) return;
-  } else {
-    __syncthreads();
-  }
+  if (S > 1) return;  // attn_merge_kernel combines the splits
+  __syncthreads();
 
-  // Merge splits (deterministic order), normalise, round, gate. All (m, l) pairs are loaded
-  // at once into LDS; wave h turns head h's into split weights w_s = exp(m_s - m*) (0 for an
-  // empty split) and the denominator; then each thread (one output dim) sums its S partials
-  // with independent loads.
+  // One split: normalise, round, gate (the same steps as attn_merge_kernel, over S = 1).
   float* wgt = &red[0][0][0];     // reuse: [2 * kQPerKv][kMaxSplits] = 2048 of the 4096 floats
   float* den_s = &red[3][0][0];   // past them
   for (int e = tid; e < kQPerKv * S; e += 256) {
@@ -325,30 +317,91 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
     const float gate = round_bf(p.gate == 0 ? sigmoid(gx) : silu(gx));
     p.out[(size_t)b * p.num_q_heads * kHd + (size_t)(hq0 + h) * kHd + tid] = f2bf(o * gate);
   }
-  if (S > 1 && tid == 0) ws.counters[b * p.num_kv_heads + kvh] = 0;
+}
+
+// The splits' merge, after attn_decode_kernel: workgroup (chunk, query head, batch row), 64
+// output dims each. Wave 0 turns the S (m, l) pairs into split weights w_s = exp(m_s - m*) (0
+// for an empty split) and the denominator; wave w then sums splits w, w + 4, ... of each dim
+// with 16 independent loads in flight per lane, and the 4 wave sums are added in wave order.
+// The partials were written through to memory by workgroups on any XCD; they are read at
+// system scope (a plain load could hit a line this XCD's L2 kept from an earlier call).
+constexpr int kMergeBatch = 16;
+template <bool PLAIN>
+__global__ __launch_bounds__(256) void attn_merge_kernel(DfAttnDecodeArgs p, AttnWs ws) {
+  __shared__ float w_s[kMaxSplits];
+  __shared__ float part[kQPerKv][64];
+  __shared__ float den_s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int chunk = blockIdx.x, hq = blockIdx.y, b = blockIdx.z;
+  const int S = p.splits;
+  if (!PLAIN) {
+    const int pos = *p.position;
+    if (pos < 0 || pos >= p.max_len) return;  // the split kernel refused too
+  }
+  const size_t row0 = ((size_t)b * p.num_q_heads + hq) * S;
+  if (wave == 0) {
+    float mstar = -INFINITY;
+    for (int sp = lane; sp < S; sp += 64) {
+      const float m = load_through(ws.ml + (row0 + sp) * 2), l = load_through(ws.ml + (row0 + sp) * 2 + 1);
+      mstar = fmaxf(mstar, l > 0.0f ? m : -INFINITY);
+    }
+    mstar = wave_max(mstar);
+    float den = 0.0f;
+    for (int sp = lane; sp < S; sp += 64) {
+      const float m = load_through(ws.ml + (row0 + sp) * 2), l = load_through(ws.ml + (row0 + sp) * 2 + 1);
+      const float w = (l > 0.0f && m != -INFINITY) ? expf(m - mstar) : 0.0f;
+      den += w * l;
+      w_s[sp] = w;
+    }
+    den = wave_sum(den);
+    if (lane == 0) den_s = den;
+  }
+  __syncthreads();
+  const int d = chunk * 64 + lane;
+  const float* accp = ws.acc + row0 * kHd + d;
+  float num = 0.0f;
+  for (int s0 = wave; s0 < S; s0 += kQPerKv * kMergeBatch) {
+    float a[kMergeBatch];
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i) {
+      const int sp = s0 + kQPerKv * i;
+      a[i] = sp < S ? load_through(accp + (size_t)sp * kHd) : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i) {
+      const int sp = s0 + kQPerKv * i;
+      if (sp < S) num += w_s[sp] * a[i];
+    }
+  }
+  part[wave][lane] = num;
+  __syncthreads();
+  if (wave == 0) {
+    const float o = round_bf((((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane]) / den_s);
+    if (PLAIN) {
+      p.out[((size_t)b * p.num_q_heads + hq) * kHd + d] = f2bf(o);
+    } else {
+      const float gx = bf2f(p.q[(size_t)b * p.ld_q + (size_t)hq * 2 * kHd + kHd + d]);
+      const float gate = round_bf(p.gate == 0 ? sigmoid(gx) : silu(gx));
+      p.out[(size_t)b * p.num_q_heads * kHd + (size_t)hq * kHd + d] = f2bf(o * gate);
+    }
+  }
 }
 
 // ---- the allocation-free variant -------------------------------------------------------
 //
-// df_attention_decode_static runs the same kernel with its workspace in this file-scope
-// device array instead of a caller's buffer: the merge counters (first kCounterBytes) and
-// room for kStaticPartialRows (batch x query head x split) partials of 258 floats. Each GPU
-// the library runs on holds its own copy until the process ends. In host code the name
-// `scratch` is only a stand-in: its device address comes from hipGetSymbolAddress, once per
-// device, and only that address is handed to kernels.
+// df_attention_decode_static runs the same kernels with their workspace in this file-scope
+// device array instead of a caller's buffer: room for kStaticPartialRows (batch x query head
+// x split) partials of 258 floats. Each GPU the library runs on holds its own copy until the
+// process ends. In host code the name `scratch` is only a stand-in: its device address comes
+// from hipGetSymbolAddress, once per device, and only that address is handed to kernels.
 constexpr int kStaticPartialRows = 8192;
-constexpr size_t kStaticScratchBytes = kCounterBytes + (size_t)kStaticPartialRows * (kHd + 2) * sizeof(float);
+constexpr size_t kStaticScratchBytes = (size_t)kStaticPartialRows * (kHd + 2) * sizeof(float);
 __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
-
-__global__ void clear_counters_kernel(int* counters) {
-  for (int i = threadIdx.x; i < kMaxCounters; i += blockDim.x) counters[i] = 0;
-}
 
 constexpr int kMaxDevices = 64;
 struct StaticScratch {
   std::mutex lock;
   void* ptr[kMaxDevices] = {};
-  bool cleared[kMaxDevices] = {};
 };
 inline StaticScratch& static_scratch() {
   static StaticScratch s;
@@ -379,7 +432,7 @@ extern "C" {
 size_t df_attention_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                            int splits) {
   (void)num_kv_heads;
-  return kCounterBytes + (size_t)batch * num_q_heads * splits * (head_dim + 2) * sizeof(float);
+  return (size_t)batch * num_q_heads * splits * (head_dim + 2) * sizeof(float);
 }
 
 int df_attention_decode_splits(int batch, int num_kv_heads, int max_keys) {
@@ -406,10 +459,11 @@ int df_attention_decode(const DfAttnDecodeArgs* args, void* workspace, size_t wo
   if (!workspace ||
       workspace_bytes < df_attention_decode_workspace_bytes(a.batch, a.num_q_heads, a.num_kv_heads, kHd, a.splits))
     return DF_WORKSPACE_TOO_SMALL;
-  if ((size_t)a.batch * a.num_kv_heads > (size_t)kMaxCounters) return DF_BAD_ARGUMENT;
   const AttnWs ws = attn_ws(workspace, a.batch, a.num_q_heads, a.splits);
   hipLaunchKernelGGL(attn_decode_kernel<false>, dim3(a.splits, a.num_kv_heads, a.batch), dim3(256), 0, stream, a,
                      ws, PlainAttn{0, 0.0f});
+  if (a.splits > 1 && hipGetLastError() == hipSuccess)
+    hipLaunchKernelGGL(attn_merge_kernel<false>, dim3(kHd / 64, a.num_q_heads, a.batch), dim3(256), 0, stream, a, ws);
   DF_RETURN_LAUNCH_STATUS();
 }
 
@@ -434,10 +488,11 @@ int df_split_kv_decode_attention(const uint16_t* query, const uint16_t* key, con
   a.head_dim = kHd;
   a.max_len = key_len;
   a.splits = splits;
-  if ((size_t)batch * num_kv_heads > (size_t)kMaxCounters) return DF_BAD_ARGUMENT;
   const AttnWs ws = attn_ws(workspace, batch, num_q_heads, splits);
   hipLaunchKernelGGL(attn_decode_kernel<true>, dim3(splits, num_kv_heads, batch), dim3(256), 0, stream, a, ws,
                      PlainAttn{key_len, scale});
+  if (splits > 1 && hipGetLastError() == hipSuccess)
+    hipLaunchKernelGGL(attn_merge_kernel<true>, dim3(kHd / 64, num_q_heads, batch), dim3(256), 0, stream, a, ws);
   DF_RETURN_LAUNCH_STATUS();
 }
 
@@ -446,23 +501,12 @@ size_t df_attention_decode_static_capacity(void) { return kStaticScratchBytes; }
 int df_attention_decode_static(const DfAttnDecodeArgs* args, hipStream_t stream) {
   if (!args) return DF_BAD_ARGUMENT;
   const DfAttnDecodeArgs& a = *args;
-  if ((size_t)a.batch * a.num_q_heads * a.splits > (size_t)kStaticPartialRows ||
-      (size_t)a.batch * a.num_kv_heads > (size_t)kMaxCounters)
+  if (a.batch < 1 || a.num_q_heads < 1 || a.splits < 1 ||
+      (size_t)a.batch * a.num_q_heads * a.splits > (size_t)kStaticPartialRows)
     return DF_WORKSPACE_TOO_SMALL;
   int dev = -1;
   void* base = scratch_for_current_device(&dev);
   if (!base) return DF_LAUNCH_FAILED;
-  {
-    // the counters start at zero on the first call on a device (the kernel leaves them at
-    // zero after every call); cleared by a kernel, not a memset, so the call can be captured
-    StaticScratch& s = static_scratch();
-    std::lock_guard<std::mutex> guard(s.lock);
-    if (!s.cleared[dev]) {
-      hipLaunchKernelGGL(clear_counters_kernel, dim3(1), dim3(256), 0, stream, reinterpret_cast<int*>(base));
-      if (hipGetLastError() != hipSuccess) return DF_LAUNCH_FAILED;
-      s.cleared[dev] = true;
-    }
-  }
   return df_attention_decode(args, base, kStaticScratchBytes, stream);
 }
 

@@ -145,9 +145,8 @@ typedef struct DfAttnDecodeArgs {
   float eps;
 } DfAttnDecodeArgs;
 
-/* Workspace of df_attention_decode / df_split_kv_decode_attention: a fixed 16 KB block of
- * merge counters (batch * num_kv_heads <= 4096), then the per-split partials. Zero-fill it
- * once before first use; every call leaves the counters at zero, whatever its shape, so one
+/* Workspace of df_attention_decode / df_split_kv_decode_attention: the per-split partials
+ * (a merge kernel combines them after the split kernel). It needs no clearing, and one
  * workspace serves calls of any shape on one stream (calls that overlap must not share it). */
 size_t df_attention_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads,
                                            int head_dim, int splits);
@@ -165,8 +164,8 @@ int df_attention_decode(const DfAttnDecodeArgs* args, void* workspace, size_t wo
  * [B][Hq][D] bf16 (already normed and rotated), key/value [B][Hkv][L][D] bf16 contiguous,
  * out[b][h] = sum_j softmax_j(scale q.k_j) v_j as bf16, split over `splits` (1..256) KV
  * ranges merged by the log-sum-exp identity. D == 256 and Hq == 4 Hkv. The workspace is
- * df_attention_decode_workspace_bytes(B, Hq, Hkv, D, splits), zero-filled before first use
- * and left zeroed. Replaces deltaforge::split_kv_decode_attention
+ * df_attention_decode_workspace_bytes(B, Hq, Hkv, D, splits). Replaces
+ * deltaforge::split_kv_decode_attention
  * (kernels/flash_decode_splitkv.py:177-261). */
 int df_split_kv_decode_attention(const uint16_t* query, const uint16_t* key, const uint16_t* value, int batch,
                                  int num_q_heads, int num_kv_heads, int key_len, int head_dim, float scale,
@@ -175,10 +174,10 @@ int df_split_kv_decode_attention(const uint16_t* query, const uint16_t* key, con
 
 /* df_attention_decode without a workspace argument, for callers that cannot allocate (code
  * under HIP graph capture, serving loops, harnesses that forbid hipMalloc). It has no
- * counterpart in the reference. Its scratch (merge counters and split partials) is a
- * file-scope device array of df_attention_decode_static_capacity() bytes (about 8.5 MB),
- * one per GPU, held until the process ends; calls with batch * num_q_heads * splits > 8192
- * or batch * num_kv_heads > 4096 return DF_WORKSPACE_TOO_SMALL. No call allocates. Every
+ * counterpart in the reference. Its scratch (the split partials) is a file-scope device
+ * array of df_attention_decode_static_capacity() bytes (about 8.5 MB), one per GPU, held
+ * until the process ends; calls with batch * num_q_heads * splits > 8192 return
+ * DF_WORKSPACE_TOO_SMALL. No call allocates. Every
  * call on a GPU shares that GPU's array, so calls that overlap on one GPU (two streams, or
  * two threads) race: serialise them. */
 size_t df_attention_decode_static_capacity(void);

@@ -165,11 +165,9 @@ def test_standalone_op_check_builders_pass():
 
 
 def test_split_kv_workspace_reused_across_shapes():
-    """Regression: calls of different shapes share one workspace. Its merge counters must sit
-    where no shape puts partials: with a counter block sized by batch * KV heads, a
-    (batch 1, 256 splits) call wrote partials over the slots a later (batch 32) call used as
-    counters, whose merge then never ran and left the output unwritten. Alternating shapes,
-    each call against the oracle."""
+    """Calls of different shapes share one workspace (an earlier counter-based merge once let
+    a (batch 1, 256 splits) call's partials land on the counters of a later batch-32 call).
+    Alternating shapes, each call against the oracle."""
     gen = torch.Generator().manual_seed(11)
     scale = 256 ** -0.5
     for batch, key_len, splits in ((1, 4097, 256), (32, 2048, 8), (1, 4097, 256), (32, 2048, 8), (8, 300, 64)):
