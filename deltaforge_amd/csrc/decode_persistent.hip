@@ -584,9 +584,10 @@ DF_DEVICE void wave_range(const Gemv& g, int wave, int& lo, int& n) {
   n = g.b_lo + (len * share_before(wave + 1)) / kShares - lo;
 }
 
-DF_DEVICE int head_tiles_of_wave(const Geo& q, int wave) {
-  const int n = q.t_hi - q.t_lo - wave;
-  return n > 0 ? (n + kCompute - 1) / kCompute : 0;
+// The head's vocabulary tiles t_lo .. t_hi of the workgroup, in the same weighted shares: wave
+// w takes the contiguous tiles head_tile(w) .. head_tile(w + 1), one run of its stream.
+DF_DEVICE int head_tile(const Geo& q, int wave) {
+  return q.t_lo + ((q.t_hi - q.t_lo) * share_before(wave)) / kShares;
 }
 
 // A compute wave's weight stream: the wave's 1 KB blocks of every GEMV phase of every layer
@@ -606,7 +607,7 @@ struct RunDesc {
 };
 // per wave and token: 6 per layer (<= 2 per row-parallel phase), a marker per attention layer
 // and the head's tiles
-constexpr int kMaxRuns = 232;
+constexpr int kMaxRuns = 225;
 constexpr uint64_t kPtrMask = (1ull << 48) - 1;
 __shared__ __align__(16) RunDesc g_runs[kCompute][kMaxRuns];
 
@@ -659,18 +660,16 @@ DF_DEVICE int build_runs(const DfPersistModel& M, const Geo& q, const Ctx& c) {
       }
     }
   }
-  const int ntw = head_tiles_of_wave(q, c.wave);
-  for (int j = 0; j < ntw; ++j) {
-    const size_t blk = (size_t)(q.t_lo + c.wave + j * kCompute) * q.Gh;
-    put(M.head_w + blk * kBlockBytes, M.head_s + blk * kTileCols, q.Gh, hold);
-    hold = false;
+  const int t0 = head_tile(q, c.wave), ntw = head_tile(q, c.wave + 1) - t0;
+  if (ntw > 0) {  // consecutive tiles are contiguous (tile-major, Gh groups per tile)
+    const size_t blk = (size_t)t0 * q.Gh;
+    put(M.head_w + blk * kBlockBytes, M.head_s + blk * kTileCols, ntw * q.Gh, hold);
   }
   // Every geometry the launcher accepts fits: per layer at most 1 run each for the
   // column-parallel phases and 2 for each row-parallel one (a wave's share of out_proj /
   // o_proj is at most 3 blocks of 4-group runs, of down at most 5/8 of a run of ngx blocks),
-  // a marker per attention layer, and at most 8 head tiles per wave (64 per workgroup), so
-  // 7 x 32 + 8 = kMaxRuns.
-  static_assert(kMaxRuns == 7 * kMaxLayers + 8, "run list capacity");
+  // a marker per attention layer, and one run of head tiles, so 7 x 32 + 1 = kMaxRuns.
+  static_assert(kMaxRuns == 7 * kMaxLayers + 1, "run list capacity");
   return min(n, kMaxRuns);
 }
 
@@ -2108,8 +2107,8 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       fence(c);
       auto& H = L.hd;
       norm_w(L, c, hidden, M.eps);
-      // tiles t_lo + wave + 8 j, all groups, from the weight stream
-      const int ntw = head_tiles_of_wave(q, c.wave);
+      // tiles t0 .. t0 + ntw, all groups, from the weight stream
+      const int t0 = head_tile(q, c.wave), ntw = head_tile(q, c.wave + 1) - t0;
       const uint16_t* xb = g_xh + (c.lane >> 4) * 32;
       const uint32_t sh = 16u * (c.lane & 1);
       float bv = -INFINITY;
@@ -2128,7 +2127,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         acc += v1;
         gl += 2;
         if (gl == G) {  // tile complete: logits of 16 columns in lanes 0..15
-          const int t = q.t_lo + c.wave + j * kCompute;
+          const int t = t0 + j;
           const uint16_t lb = f2bf(acc);
           if (c.lane < 16) {
             H.logit[(t - q.t_lo) * 16 + c.lane] = lb;
