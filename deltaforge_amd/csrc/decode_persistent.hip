@@ -729,12 +729,14 @@ DF_DEVICE void dma4_16(const void* gaddr, uint32_t lds_base) {
       : "memory", "m0");
 }
 
-// Issue the cursor's block into the next ring slot (weights + scales) and advance. Every
-// block is two vector memory operations, weights then scales: the consumer's vmcnt waits
-// count on it.
+// Issue the cursor's block into the next ring slot (scales, then weights) and advance. A block
+// issued alone is two vector memory operations, scales then weights; a pair issued by refill2
+// is three, both blocks' scales then the two weight blocks. Every block's scales are issued
+// before its weights, so a completed weight DMA implies its scales; the consumer's vmcnt
+// waits count on these groupings (wait_oldest).
 DF_DEVICE void issue_one(Stream& st, const Ctx& c) {
-  dma16(st.wp + c.lane * 16, lds_addr(&g_ring_w[c.wave][st.wslot][0]));
   dma4_16(st.sp + (c.lane & 14), lds_addr(&g_ring_s[c.wave][st.wslot][0]));
+  dma16(st.wp + c.lane * 16, lds_addr(&g_ring_w[c.wave][st.wslot][0]));
   st.issued += 1;
   st.wslot = (st.wslot + 1) & (kRing - 1);
   st.wp += kBlockBytes;
@@ -759,11 +761,12 @@ DF_DEVICE void dma16s(const void* sbase, uint32_t voff, uint32_t lds_base) {
                "s"(lds_base)
                : "memory", "m0");
 }
-DF_DEVICE void dma4_16s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+// Both blocks' scale dwords of a pair on lanes 0..31 (lane i < 16: block 0's, i >= 16: block
+// 1's), landing in the pair's two adjacent ring slots.
+DF_DEVICE void dma4_32s(const void* sbase, uint32_t voff, uint32_t lds_base) {
   uint64_t saved;
   asm volatile(
       "s_mov_b64 %0, exec\n\t"
-      "s_mov_b32 exec_lo, 0xffff\n\t"
       "s_mov_b32 exec_hi, 0\n\t"
       "s_mov_b32 m0, %3\n\t"
       "s_nop 0\n\t"
@@ -775,15 +778,17 @@ DF_DEVICE void dma4_16s(const void* sbase, uint32_t voff, uint32_t lds_base) {
 }
 
 // After the consumer took two blocks from a full ring: refill both slots. The common case
-// (two more blocks in the current run) is straight-line code; anything else goes through fill.
+// (two more blocks in the current run, landing in two adjacent slots: not the ring's last and
+// first) is straight-line code of three DMAs; anything else goes through fill.
 DF_DEVICE void refill2(Stream& st, int steps, const Ctx& c) {
-  if (__builtin_expect(st.state == kStreaming && st.left >= 2 && st.issued - st.consumed == kRing - 2, 1)) {
-    const uint32_t voff = c.lane * 16, soff = (c.lane & 14) * 2;
-    const int s0 = st.wslot, s1 = (st.wslot + 1) & (kRing - 1);
+  if (__builtin_expect(st.state == kStreaming && st.left >= 2 && st.wslot != kRing - 1 &&
+                           st.issued - st.consumed == kRing - 2,
+                       1)) {
+    const uint32_t voff = c.lane * 16, soff = ((c.lane >> 4) * kTileCols + (c.lane & 14)) * 2;
+    const int s0 = st.wslot;
+    dma4_32s(st.sp, soff, lds_addr(&g_ring_s[c.wave][s0][0]));
     dma16s(st.wp, voff, lds_addr(&g_ring_w[c.wave][s0][0]));
-    dma4_16s(st.sp, soff, lds_addr(&g_ring_s[c.wave][s0][0]));
-    dma16s(st.wp + kBlockBytes, voff, lds_addr(&g_ring_w[c.wave][s1][0]));
-    dma4_16s(st.sp + kTileCols, soff, lds_addr(&g_ring_s[c.wave][s1][0]));
+    dma16s(st.wp, voff + kBlockBytes, lds_addr(&g_ring_w[c.wave][s0 + 1][0]));  // same base, next 1 KB
     st.issued += 2;
     st.wslot = (st.wslot + 2) & (kRing - 1);
     st.wp += 2 * kBlockBytes;
@@ -796,10 +801,16 @@ DF_DEVICE void refill2(Stream& st, int steps, const Ctx& c) {
 
 // Wait for the oldest `need` pending blocks (need = 1 or 2). The ring is full except while
 // it drains before an attention layer's hold or at the end of a launch, where waiting for
-// every block in flight costs nothing extra.
+// every block in flight costs nothing extra. With the ring full (blocks i .. i + 7 issued,
+// as groups of (scales, weights) singles and (scales, weights, weights) pairs), at least 9
+// operations were issued after block i + 1's weights and at least 10 after block i's: the
+// fewest come from pairs, and a pair that starts at the awaited block adds its second
+// weight DMA. Waiting until no more than that many are outstanding completes the awaited
+// blocks and, issued before them, their scales.
 template <int NEED>
 DF_DEVICE void wait_oldest(const Stream& st) {
-  if (st.issued - st.consumed == kRing) wait_vm<2 * (kRing - NEED)>();
+  static_assert(kRing == 8, "wait counts derived for an 8-slot ring");
+  if (st.issued - st.consumed == kRing) wait_vm<NEED == 2 ? 9 : 10>();
   else wait_vm<0>();
 }
 
@@ -819,9 +830,11 @@ DF_DEVICE void ring_read1(int slot, const Ctx& c, uint4& wv, uint32_t& sd) {
 // scale dword), the two groups' input chunks of this lane's k slot and their group sums.
 // Only row 0 of each product is used: its A operand comes from lanes 0, 16, 32 and 48, and
 // its scales, group sums and results live in lanes 0..15. The input chunks are read by
-// those four lanes only and the scale dwords and group sums by lanes 0..15 (exec masked
-// inside the asm and restored before it ends), which cuts the LDS traffic of a pair from
-// 11 KB to under 3 KB; the other lanes' copies hold stale values that only feed rows 1..15.
+// those four lanes only (exec masked inside the asm and restored before it ends), which
+// cuts the LDS traffic of a pair from 11 KB to under 4 KB; the other lanes' copies hold
+// stale values that only feed rows 1..15. The scale dwords (16 distinct per slot) and the
+// group sums (one address) are read by every lane: broadcasts, cheaper than two more exec
+// switches.
 struct PairIn {
   uint4 w0, w1;
   uint32_t s0, s1;
@@ -841,6 +854,10 @@ DF_DEVICE void pair_read(int slot, const Ctx& c, const uint16_t* xg0, const uint
   asm volatile(
       "ds_read_b128 %0, %15\n\t"
       "ds_read_b128 %1, %17\n\t"
+      "ds_read_b32 %2, %16\n\t"
+      "ds_read_b32 %3, %18\n\t"
+      "ds_read_b32 %12, %21\n\t"
+      "ds_read_b32 %13, %22\n\t"
       "s_mov_b64 %14, exec\n\t"
       "s_mov_b32 exec_lo, 0x10001\n\t"
       "s_mov_b32 exec_hi, 0x10001\n\t"
@@ -853,13 +870,6 @@ DF_DEVICE void pair_read(int slot, const Ctx& c, const uint16_t* xg0, const uint
       "ds_read_b128 %9, %20 offset:16\n\t"
       "ds_read_b128 %10, %20 offset:32\n\t"
       "ds_read_b128 %11, %20 offset:48\n\t"
-      "s_mov_b32 exec_lo, 0xffff\n\t"
-      "s_mov_b32 exec_hi, 0\n\t"
-      "s_nop 0\n\t"
-      "ds_read_b32 %2, %16\n\t"
-      "ds_read_b32 %3, %18\n\t"
-      "ds_read_b32 %12, %21\n\t"
-      "ds_read_b32 %13, %22\n\t"
       "s_mov_b64 exec, %14\n\t"
       "s_nop 0\n\t"
       "s_waitcnt lgkmcnt(0)"
@@ -894,13 +904,20 @@ DF_DEVICE void take_pair(Stream& st, const Ctx& c, const uint16_t* xg0, const ui
 // and 1024 + 16 n for k % 8 in 2, 3, 6, 7. The masks and bias arrive as opaque register values
 // (masks in SGPRs, bias in a VGPR), so the compiler emits one v_and_or_b32 each (gfx9 VOP3
 // encodes no literal) and its hazard checks still cover the results, which feed an MFMA.
-DF_DEVICE float block_dot_r(const uint4& wv, uint32_t sd, const uint4 (&x)[4], float xs, uint32_t sh) {
+struct DotK {
+  uint32_t mlo, mhi, bias;
+};
+// Made once per loop, outside it: opaque to the compiler, so they stay in registers.
+DF_DEVICE DotK dot_consts() {
+  DotK k{0x000F000Fu, 0x00F000F0u, kBiasPair};
+  asm volatile("" : "+s"(k.mlo), "+s"(k.mhi));
+  asm volatile("" : "+v"(k.bias));
+  return k;
+}
+DF_DEVICE float block_dot_r(const uint4& wv, uint32_t sd, const uint4 (&x)[4], float xs, uint32_t sh, const DotK& K) {
   const float s = __uint_as_float((sd >> sh) << 16);
   const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
-  uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, bias = kBiasPair;
-  asm("" : "+s"(mlo));
-  asm("" : "+s"(mhi));
-  asm("" : "+v"(bias));
+  const uint32_t mlo = K.mlo, mhi = K.mhi, bias = K.bias;
   df_f32x4 d4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
@@ -917,7 +934,7 @@ DF_DEVICE float block_dot(const uint4& wv, uint32_t sd, const uint16_t* x, float
   uint4 xv[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) xv[d] = *reinterpret_cast<const uint4*>(x + d * 8);
-  return block_dot_r(wv, sd, xv, xs, 16u * (lane & 1));
+  return block_dot_r(wv, sd, xv, xs, 16u * (lane & 1), dot_consts());
 }
 
 // Compute waves: consume this wave's blocks of GEMV phase g (input row g_x, group sums
@@ -944,14 +961,15 @@ DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPer
     }
   };
   const uint32_t sh = 16u * (c.lane & 1);
+  const DotK K = dot_consts();
   int i = 0;
 #pragma unroll 1
   for (; i + 1 < n; i += 2) {
     const int gl1 = gl + 1 == g.ng ? 0 : gl + 1;
     PairIn in;
     take_pair(st, c, xb + gl * kGroup, xb + gl1 * kGroup, &L.xs[gl], &L.xs[gl1], in);
-    const float v0 = block_dot_r(in.w0, in.s0, in.x0, in.xs0, sh);
-    const float v1 = block_dot_r(in.w1, in.s1, in.x1, in.xs1, sh);
+    const float v0 = block_dot_r(in.w0, in.s0, in.x0, in.xs0, sh, K);
+    const float v1 = block_dot_r(in.w1, in.s1, in.x1, in.xs1, sh, K);
     refill2(st, steps, c);
     add(v0);
     add(v1);
@@ -2111,6 +2129,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       const int t0 = head_tile(q, c.wave), ntw = head_tile(q, c.wave + 1) - t0;
       const uint16_t* xb = g_xh + (c.lane >> 4) * 32;
       const uint32_t sh = 16u * (c.lane & 1);
+      const DotK K = dot_consts();
       float bv = -INFINITY;
       int bi = 0x7FFFFFFF;
       float acc = 0.0f;
@@ -2120,8 +2139,8 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       for (int i = 0; i < ntw * G; i += 2) {
         PairIn in;
         take_pair(st, c, xb + gl * kGroup, xb + (gl + 1) * kGroup, &L.xs[gl], &L.xs[gl + 1], in);
-        const float v0 = block_dot_r(in.w0, in.s0, in.x0, in.xs0, sh);
-        const float v1 = block_dot_r(in.w1, in.s1, in.x1, in.xs1, sh);
+        const float v0 = block_dot_r(in.w0, in.s0, in.x0, in.xs0, sh, K);
+        const float v1 = block_dot_r(in.w1, in.s1, in.x1, in.xs1, sh, K);
         refill2(st, steps, c);
         acc += v0;
         acc += v1;
