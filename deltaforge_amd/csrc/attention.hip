@@ -48,8 +48,11 @@ inline AttnWs attn_ws(void* base, int batch, int hq, int splits) {
 }
 
 // RMSNorm(1+w) over 256 dims held 4 per lane, then partial RoPE over the first `rot` dims.
-DF_DEVICE void norm_rope4(float x[4], const uint16_t* norm_w, float eps, const float* inv_freq, int rot,
-                          float posf, int lane) {
+// The lane's norm weights (4 bf16) and inverse frequencies (of its dims' rotary pairs) come
+// loaded, so the caller can issue those loads ahead of others.
+DF_DEVICE void norm_rope4(float x[4], uint2 wraw, const float (&inv)[4], float eps, int rot, float posf, int lane) {
+  const uint16_t norm_w4[4] = {static_cast<uint16_t>(wraw.x), static_cast<uint16_t>(wraw.x >> 16),
+                               static_cast<uint16_t>(wraw.y), static_cast<uint16_t>(wraw.y >> 16)};
   float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
   ss = wave_sum(ss);
   const float r = 1.0f / sqrtf(ss / static_cast<float>(kHd) + eps);
@@ -57,7 +60,7 @@ DF_DEVICE void norm_rope4(float x[4], const uint16_t* norm_w, float eps, const f
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float scaled = x[i] * r;
-    n[i] = round_bf(scaled * (1.0f + bf2f(norm_w[lane * 4 + i])));
+    n[i] = round_bf(scaled * (1.0f + bf2f(norm_w4[i])));
   }
   const int half = rot / 2;
   // dim d's partner d +- half sits half/4 lanes away; the xor reaches lane +- half/4 because
@@ -69,7 +72,7 @@ DF_DEVICE void norm_rope4(float x[4], const uint16_t* norm_w, float eps, const f
   for (int i = 0; i < 4; ++i) {
     const int dim = lane * 4 + i;
     if (dim < rot) {
-      const float ang = posf * inv_freq[dim % half];
+      const float ang = posf * inv[i];
       const float c = round_bf(cosf(ang)), s = round_bf(sinf(ang));
       const float rotated = dim < half ? -partner[i] : partner[i];
       x[i] = round_bf(round_bf(n[i] * c) + round_bf(rotated * s));
@@ -77,6 +80,19 @@ DF_DEVICE void norm_rope4(float x[4], const uint16_t* norm_w, float eps, const f
       x[i] = n[i];
     }
   }
+}
+
+struct NormIn {
+  uint2 w;       // the lane's 4 norm weights (bf16)
+  float inv[4];  // inverse frequency of each of its dims' rotary pairs
+};
+DF_DEVICE NormIn norm_in(const uint16_t* norm_w, const float* inv_freq, int rot, int lane) {
+  NormIn n;
+  n.w = *reinterpret_cast<const uint2*>(norm_w + lane * 4);
+  const int half = rot / 2;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) n.inv[i] = inv_freq[(lane * 4 + i) % half];
+  return n;
 }
 
 // What the plain entry point (no prologue, no gate: df_split_kv_decode_attention) changes in
@@ -111,33 +127,78 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
   const int j1 = min(j0 + per, nkeys);
   const float posf = static_cast<float>(pos);
   const size_t kv_base = ((size_t)b * p.num_kv_heads + kvh) * p.max_len;
+  const int col = lane & 15, slot = lane >> 4;
 
-  // Prologue: queries, new key, new value.
-  if (PLAIN) {
-    const int hq = kvh * kQPerKv + wave;
-    *reinterpret_cast<uint2*>(&q_s[wave][lane * 4]) =
-        *reinterpret_cast<const uint2*>(p.q + ((size_t)b * p.num_q_heads + hq) * kHd + lane * 4);
-  } else {
-    const int hq = kvh * kQPerKv + wave;
-    const uint16_t* src = p.q + (size_t)b * p.ld_q + (size_t)hq * 2 * kHd + lane * 4;
-    float x[4];
+  // A tile's K and V rows, all loads issued before any is used (one memory round trip): keys
+  // past the split load row j1 - 1 instead (in bounds, ignored), and the new position's row
+  // is replaced by the staged key / value. K rows use two register sets in turn, so the next
+  // tile's keys are in flight while this one is computed; a tile's V rows are loaded when the
+  // previous tile is done with the V registers, and the first tile's K and V rows go out
+  // during the prologue, which they do not depend on. The loads are unconditional (rows clamp
+  // into [0, j1), j1 >= 1): on every path the same loads are outstanding, so the compiler's
+  // waits for one register set never include a younger one.
+  auto load_k = [&](int t0, uint4 (&kb)[8]) {
+    const int krow = min(t0 + wave * 16 + col, j1 - 1);
+    const uint16_t* kp = p.k_cache + (kv_base + krow) * kHd + slot * 8;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = bf2f(src[i]);
-    norm_rope4(x, p.q_norm_w, p.eps, p.inv_freq, p.rotary_dim, posf, lane);
+    for (int d = 0; d < 8; ++d) kb[d] = *reinterpret_cast<const uint4*>(kp + d * 32);
+  };
+  auto load_v = [&](int t0, uint2 (&vb)[16]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) q_s[wave][lane * 4 + i] = f2bf(x[i]);
+    for (int jj = 0; jj < 16; ++jj) {
+      const int vrow = min(t0 + wave * 16 + jj, j1 - 1);
+      vb[jj] = *reinterpret_cast<const uint2*>(p.v_cache + (kv_base + vrow) * kHd + lane * 4);
+    }
+  };
+  // Prologue: queries, new key, new value. Its operands are loaded first and the first tile's
+  // rows after them, so the prologue's waits do not include the tile (a wave's loads complete
+  // in order).
+  const int hq = kvh * kQPerKv + wave;
+  uint16_t qe[4], ke[4] = {0, 0, 0, 0}, ve[4] = {0, 0, 0, 0};
+  NormIn qn{}, kn{};
+  {
+    const uint16_t* src = PLAIN ? p.q + ((size_t)b * p.num_q_heads + hq) * kHd + lane * 4
+                                : p.q + (size_t)b * p.ld_q + (size_t)hq * 2 * kHd + lane * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qe[i] = src[i];
+  }
+  if (!PLAIN) {
+    qn = norm_in(p.q_norm_w, p.inv_freq, p.rotary_dim, lane);
     if (wave == 0) {
       const uint16_t* ks = p.k + (size_t)b * p.ld_kv + (size_t)kvh * kHd + lane * 4;
-      float kx[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kx[i] = bf2f(ks[i]);
-      norm_rope4(kx, p.k_norm_w, p.eps, p.inv_freq, p.rotary_dim, posf, lane);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) knew[lane * 4 + i] = f2bf(kx[i]);
+      for (int i = 0; i < 4; ++i) ke[i] = ks[i];
+      kn = norm_in(p.k_norm_w, p.inv_freq, p.rotary_dim, lane);
     } else if (wave == 1) {
       const uint16_t* vsrc = p.v + (size_t)b * p.ld_kv + (size_t)kvh * kHd + lane * 4;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vnew[lane * 4 + i] = vsrc[i];
+      for (int i = 0; i < 4; ++i) ve[i] = vsrc[i];
+    }
+  }
+  uint4 kA[8], kB[8];
+  uint2 vt[16];
+  load_k(j0, kA);
+  load_v(j0, vt);
+  if (PLAIN) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q_s[wave][lane * 4 + i] = qe[i];
+  } else {
+    float x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = bf2f(qe[i]);
+    norm_rope4(x, qn.w, qn.inv, p.eps, p.rotary_dim, posf, lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q_s[wave][lane * 4 + i] = f2bf(x[i]);
+    if (wave == 0) {
+      float kx[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kx[i] = bf2f(ke[i]);
+      norm_rope4(kx, kn.w, kn.inv, p.eps, p.rotary_dim, posf, lane);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) knew[lane * 4 + i] = f2bf(kx[i]);
+    } else if (wave == 1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vnew[lane * 4 + i] = ve[i];
     }
   }
   __syncthreads();
@@ -149,7 +210,6 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
     vd[tid] = vnew[tid];
   }
 
-  const int col = lane & 15, slot = lane >> 4;
   const float scale = PLAIN ? pl.scale : 1.0f / sqrtf(static_cast<float>(kHd));
   float m_run = -INFINITY, l_run = 0.0f;  // for head `wave`
   float acc[kQPerKv][4];
@@ -158,23 +218,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[h][i] = 0.0f;
 
-  for (int t0 = j0; t0 < j1; t0 += kTile) {
-    // The tile's K and V rows, all loads issued before any is used (one memory round trip):
-    // keys past the split load row j1 - 1 instead (in bounds, ignored), and the new
-    // position's row is replaced by the staged key / value.
-    uint4 kb[8];
-    uint2 vb[16];
-    {
-      const int krow = min(t0 + wave * 16 + col, j1 - 1);
-      const uint16_t* kp = p.k_cache + (kv_base + krow) * kHd + slot * 8;
-#pragma unroll
-      for (int d = 0; d < 8; ++d) kb[d] = *reinterpret_cast<const uint4*>(kp + d * 32);
-#pragma unroll
-      for (int jj = 0; jj < 16; ++jj) {
-        const int vrow = min(t0 + wave * 16 + jj, j1 - 1);
-        vb[jj] = *reinterpret_cast<const uint2*>(p.v_cache + (kv_base + vrow) * kHd + lane * 4);
-      }
-    }
+  auto tile = [&](int t0, const uint4 (&kb)[8], const uint2 (&vb)[16]) {
     // QK: wave covers keys t0 + 16*wave + col.
     {
       const int key = t0 + wave * 16 + col;
@@ -238,6 +282,16 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
       }
     }
     __syncthreads();
+  };
+  for (int t0 = j0; t0 < j1; t0 += 2 * kTile) {
+    load_k(t0 + kTile, kB);
+    tile(t0, kA, vt);
+    if (t0 + kTile >= j1) break;
+    load_v(t0 + kTile, vt);
+    load_k(t0 + 2 * kTile, kA);
+    tile(t0 + kTile, kB, vt);
+    if (t0 + 2 * kTile >= j1) break;
+    load_v(t0 + 2 * kTile, vt);
   }
 
   // Combine the four waves' PV partials; publish this split's (acc, m, l) per head.
