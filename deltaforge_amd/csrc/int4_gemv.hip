@@ -36,6 +36,7 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kMaxRows = 16;
 constexpr int kDepth = 8;  // groups in flight per wave
 constexpr int kNormChunks = 3;  // RMSNorm prologue: K <= kNormChunks * kThreads * 8 = 12288
+constexpr int kRowChunks = 5;   // ... one wave per row when K <= kRowChunks * 64 * 8 = 2560
 
 struct GemvSmem {
   int xs_ld;  // bf16 elements per LDS row of x
@@ -59,7 +60,7 @@ __host__ __device__ inline GemvSmem gemv_smem(int rows, int kx, int nt) {
 // Prologues: this workgroup's K range of the bf16 activation rows, into LDS.
 // ---------------------------------------------------------------------------------------
 
-template <int PRO>
+template <int PRO, bool WROWS>
 DF_DEVICE void gemv_prologue(const DfInt4GemvArgs& p, uint16_t* xs, int xs_ld, float* red, int k0, int kc) {
   const int tid = threadIdx.x;
   if (p.rows < kMaxRows) {
@@ -80,6 +81,78 @@ DF_DEVICE void gemv_prologue(const DfInt4GemvArgs& p, uint16_t* xs, int xs_ld, f
     const bool write_h =
         (PRO == DF_PRO_ADD_RMSNORM) && p.h_out && blockIdx.x == 0 && blockIdx.y == 0;
     const int nchunks = p.K / 8;
+    if (WROWS && nchunks <= 64 * kRowChunks) {
+      // Many rows (the WROWS instance): one wave per row (rows w, w + 8, ...), the row and the
+      // norm weight of this workgroup's K range loaded at once into the wave's registers, its
+      // sum of squares reduced within the wave. Rows proceed in parallel with no block-wide
+      // reduction (and no second memory round trip) per row; the sum's order differs from the
+      // block form's only in fp32 rounding. Few rows keep the block form: this one holds more
+      // registers, and the occupancy it costs outweighs what it saves for one row.
+      const int lane = tid & 63, wave = tid >> 6;
+      for (int m = wave; m < p.rows; m += kWaves) {
+        const uint16_t* xr = p.x + (size_t)m * p.ldx;
+        const uint16_t* rr = p.x2 + (size_t)m * p.ldx2;
+        uint32_t v[kRowChunks][4];
+        uint4 wreg[kRowChunks];
+#pragma unroll
+        for (int j = 0; j < kRowChunks; ++j) {
+          const int c = lane + 64 * j, k = c * 8;
+          wreg[j] = make_uint4(0u, 0u, 0u, 0u);
+          v[j][0] = v[j][1] = v[j][2] = v[j][3] = 0u;
+          if (c < nchunks) {
+            const uint4 raw = load16(xr + k);
+            v[j][0] = raw.x, v[j][1] = raw.y, v[j][2] = raw.z, v[j][3] = raw.w;
+            if constexpr (PRO == DF_PRO_ADD_RMSNORM) {
+              const uint4 rraw = load16(rr + k);
+              const uint32_t rw[4] = {rraw.x, rraw.y, rraw.z, rraw.w};
+#pragma unroll
+              for (int e2 = 0; e2 < 4; ++e2) {
+                const uint16_t lo = f2bf(bf2f(static_cast<uint16_t>(v[j][e2])) + bf2f(static_cast<uint16_t>(rw[e2])));
+                const uint16_t hi = f2bf(bf2f(static_cast<uint16_t>(v[j][e2] >> 16)) +
+                                         bf2f(static_cast<uint16_t>(rw[e2] >> 16)));
+                v[j][e2] = lo | (static_cast<uint32_t>(hi) << 16);
+              }
+            }
+            if (k >= k0 && k < k0 + kc) wreg[j] = load16(p.norm_w + k);
+          }
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kRowChunks; ++j) {
+          const int c = lane + 64 * j;
+          if (c < nchunks) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float val = bf2f(static_cast<uint16_t>(v[j][e >> 1] >> (16 * (e & 1))));
+              ss += val * val;
+            }
+            if (write_h)
+              *reinterpret_cast<uint4*>(p.h_out + (size_t)m * p.K + c * 8) = make_uint4(v[j][0], v[j][1], v[j][2], v[j][3]);
+          }
+        }
+        ss = wave_sum(ss);
+        const float r = 1.0f / sqrtf(ss / static_cast<float>(p.K) + p.eps);
+#pragma unroll
+        for (int j = 0; j < kRowChunks; ++j) {
+          const int c = lane + 64 * j, k = c * 8;
+          if (c < nchunks && k >= k0 && k < k0 + kc) {
+            const uint32_t ww[4] = {wreg[j].x, wreg[j].y, wreg[j].z, wreg[j].w};
+            uint32_t o[4];
+#pragma unroll
+            for (int e2 = 0; e2 < 4; ++e2) {
+              uint16_t pr[2];
+#pragma unroll
+              for (int h = 0; h < 2; ++h) {
+                const float scaled = bf2f(static_cast<uint16_t>(v[j][e2] >> (16 * h))) * r;
+                pr[h] = f2bf(scaled * (1.0f + bf2f(static_cast<uint16_t>(ww[e2] >> (16 * h)))));
+              }
+              o[e2] = pr[0] | (static_cast<uint32_t>(pr[1]) << 16);
+            }
+            *reinterpret_cast<uint4*>(xs + m * xs_ld + (k - k0)) = make_uint4(o[0], o[1], o[2], o[3]);
+          }
+        }
+      }
+    } else
     for (int m = 0; m < p.rows; ++m) {
       const uint16_t* xr = p.x + (size_t)m * p.ldx;
       const uint16_t* rr = p.x2 + (size_t)m * p.ldx2;
@@ -201,7 +274,7 @@ DF_DEVICE void gemv_epilogue(const DfInt4GemvArgs& p, const float* y, int col0, 
   }
 }
 
-template <int PRO, int EPI, int NT>
+template <int PRO, int EPI, int NT, bool WROWS>
 __global__ __launch_bounds__(kThreads) void w4_gemv_kernel(DfInt4GemvArgs p) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int KS = kWaves / NT;
@@ -238,7 +311,7 @@ __global__ __launch_bounds__(kThreads) void w4_gemv_kernel(DfInt4GemvArgs p) {
     }
   }
 
-  gemv_prologue<PRO>(p, xs, L.xs_ld, red, gx0 * kGroup, ngx * kGroup);
+  gemv_prologue<PRO, WROWS>(p, xs, L.xs_ld, red, gx0 * kGroup, ngx * kGroup);
 
   const int col = lane & 15;   // A row, B/C column, scale column
   const int slot = lane >> 4;  // K slot of A and B; C row block
@@ -380,7 +453,11 @@ static hipError_t launch_gemv(const DfInt4GemvArgs& a, hipStream_t stream) {
   const int gps = a.groups_per_split;
   const GemvSmem L = gemv_smem(a.rows, min(gps, G) * kGroup, NT);
   dim3 grid(a.N / (NT * kTileCols), a.ksplit);
-  hipLaunchKernelGGL((w4_gemv_kernel<PRO, EPI, NT>), grid, dim3(kThreads), L.total, stream, a);
+  constexpr bool kNorm = PRO == DF_PRO_RMSNORM || PRO == DF_PRO_ADD_RMSNORM;
+  if (kNorm && a.rows > 4 && a.K <= kRowChunks * 64 * 8)
+    hipLaunchKernelGGL((w4_gemv_kernel<PRO, EPI, NT, kNorm>), grid, dim3(kThreads), L.total, stream, a);
+  else
+    hipLaunchKernelGGL((w4_gemv_kernel<PRO, EPI, NT, false>), grid, dim3(kThreads), L.total, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.ksplit == 1) return e;
   hipLaunchKernelGGL((w4_reduce_kernel<EPI>), dim3(a.N / 64), dim3(256), 0, stream, a);
