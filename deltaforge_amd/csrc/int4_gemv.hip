@@ -37,6 +37,7 @@ constexpr int kMaxRows = 16;
 constexpr int kDepth = 8;  // groups in flight per wave
 constexpr int kNormChunks = 3;  // RMSNorm prologue: K <= kNormChunks * kThreads * 8 = 12288
 constexpr int kRowChunks = 5;   // ... one wave per row when K <= kRowChunks * 64 * 8 = 2560
+constexpr int kGemvLds = 100 * 1024;  // LDS bytes a workgroup may take
 
 struct GemvSmem {
   int xs_ld;  // bf16 elements per LDS row of x
@@ -498,10 +499,11 @@ int df_int4_gemv_plan(int rows, int K, int N, int epilogue, int target_waves, in
   const int min_nt = epilogue == DF_EPI_SWIGLU ? 2 : 1;
   int nt = 8;
   while (nt > min_nt && (tiles % nt || (tiles / nt) * kWaves < target_waves)) nt /= 2;
-  // The activation rows of one workgroup's K range must fit in LDS (<= 48 KB).
+  // A workgroup's LDS (the activation rows of its K range, partial sums) must fit kGemvLds of
+  // gfx950's 160 KB: 16 rows of K = 2560 fit, so that shape needs no K split, partials or
+  // reduce launch.
   int gps = G;
-  const int max_groups = (48 * 1024) / (rows * kGroup * 2);
-  if (gps > max_groups) gps = max_groups;
+  while (gps > 1 && gemv_smem(rows, gps * kGroup, nt).total > kGemvLds) --gps;
   int ks = (G + gps - 1) / gps;
   gps = (G + ks - 1) / ks;
   *tiles_per_workgroup = nt;
@@ -528,7 +530,7 @@ int df_int4_gemv(const DfInt4GemvArgs* args, void* workspace, size_t workspace_b
   if (a.epilogue == DF_EPI_SWIGLU && (nt < 2 || a.N % 32)) return DF_BAD_ARGUMENT;
   const int out_cols = a.epilogue == DF_EPI_SWIGLU ? a.N / 2 : a.N;
   if (a.ldo < out_cols) return DF_BAD_ARGUMENT;
-  if (gemv_smem(a.rows, min(a.groups_per_split, G) * kGroup, nt).total > 64 * 1024) return DF_BAD_ARGUMENT;
+  if (gemv_smem(a.rows, min(a.groups_per_split, G) * kGroup, nt).total > kGemvLds) return DF_BAD_ARGUMENT;
   if ((a.prologue == DF_PRO_ADD_RMSNORM || a.prologue == DF_PRO_GATED_RMSNORM) && !a.x2) return DF_BAD_ARGUMENT;
   if (a.prologue != DF_PRO_NONE && !a.norm_w) return DF_BAD_ARGUMENT;
   if (a.epilogue == DF_EPI_RESIDUAL && !a.res) return DF_BAD_ARGUMENT;
