@@ -572,8 +572,9 @@ DF_DEVICE Gemv gemv_of(LayerPtr Lp, const Geo& q, int k, int xcd, int r) {
 // A compute wave's share of a workgroup's blocks. Wave w runs on SIMD w % 4, so waves 4..7
 // share their SIMD with the older waves 0..3, which win the issue arbitration: with equal
 // shares the younger waves finished 15-25 % later and the phase waited for them while each
-// SIMD ran one wave. Shares of 5 : 4 (waves 0..3 : 4..7) let both halves finish together.
-constexpr int kShareOld = 5, kShareYoung = 4, kShares = 4 * (kShareOld + kShareYoung);
+// SIMD ran one wave. Shares of 3 : 2 (waves 0..3 : 4..7) decode fastest of 1 : 1, 6 : 5,
+// 5 : 4, 3 : 2, 7 : 4 and 2 : 1 (same-box A/B).
+constexpr int kShareOld = 3, kShareYoung = 2, kShares = 4 * (kShareOld + kShareYoung);
 static_assert(kCompute == 8, "two waves per SIMD");
 DF_DEVICE int share_before(int wave) {
   return wave <= 4 ? kShareOld * wave : 4 * kShareOld + kShareYoung * (wave - 4);
