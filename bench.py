@@ -67,9 +67,9 @@ GATE_UP_KERNEL = "w4_gemv_kernel<RMSNORM, SWIGLU> (post-attention norm + gate/up
 # WRITE_SIZE). Re-measure when the kernel changes.
 GATE_UP_TRAFFIC_BYTES = 12049 * 1024 * 2 + 18 * 1024
 # HBM bytes per decode token of the persistent kernel from the calibrated PMC passes over the
-# timed 256-token launch (332,249,031 KiB fetched x 1.9998, 17,708,842 KiB written, / 256),
+# timed 256-token launch (332,334,028 KiB fetched x 1.9998, 17,707,377 KiB written, / 256),
 # recorded with their commands in PERSISTENT_TRAFFIC_SOURCE. Re-measure when the kernel changes.
-PERSISTENT_TRAFFIC_BYTES_PER_TOKEN = 2728594429
+PERSISTENT_TRAFFIC_BYTES_PER_TOKEN = 2729268486
 PERSISTENT_TRAFFIC_SOURCE = ("profiles/decode_persistent_config5.md: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
                              "over bench.py --steps 256, scaled by a 256 MiB copy in the same process")
 
