@@ -77,7 +77,7 @@ class PersistModel(C.Structure):
     _fields_ = [
         ("hidden", _i), ("inter", _i), ("vocab", _i), ("num_layers", _i), ("max_len", _i), ("gate_kind", _i),
         ("eps", _f),
-        ("layers", _vp), ("head_w", _vp), ("head_s", _vp), ("final_norm", _vp), ("inv_freq", _vp),
+        ("layers", _vp), ("head_w", _vp), ("head_s", _vp), ("final_norm", _vp), ("rope", _vp),
         ("position", _vp), ("tokens", _vp), ("prompt", _vp), ("prompt_len", _i),
         ("token_log", _vp), ("log_capacity", _i), ("step", _vp), ("logits", _vp),
         ("trace", _vp), ("trace_step", _i), ("trace_capacity", _i), ("embed_table", _vp),

@@ -1,6 +1,8 @@
 """Build the gfx950 HIP library ``deltaforge_amd/_lib/libdeltaforge_hip.so`` in-tree.
 
     python -m deltaforge_amd.build          # compile every csrc/*.hip, link one .so
+    python -m deltaforge_amd.build --trace  # the same with the persistent kernel's phase stamps
+                                            # (DF_TRACE), as _lib/libdeltaforge_hip_trace.so
 
 hipcc cross-compiles for gfx950 without a GPU. Packed-FP32 codegen is disabled
 (``-packed-fp32-ops``); the host pass warns that it does not know the feature, which is
@@ -44,8 +46,11 @@ def hipcc() -> str:
     return found
 
 
-def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+TRACE_LIB = OUT_DIR / "libdeltaforge_hip_trace.so"
+
+
+def _compile(src: Path, obj: Path, extra: tuple[str, ...] = ()) -> None:
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     errs = "\n".join(line for line in res.stderr.splitlines() if noise not in line)
@@ -55,24 +60,28 @@ def _compile(src: Path, obj: Path) -> None:
         print(errs, file=sys.stderr)
 
 
-def build(verbose: bool = True) -> Path:
+def build(verbose: bool = True, trace: bool = False) -> Path:
+    """Compile and link the library; ``trace`` builds the phase-stamping variant
+    (``PersistentDecoder.trace_decode`` needs it) beside the product library."""
     OUT_DIR.mkdir(exist_ok=True)
-    objdir = OUT_DIR / "obj"
+    objdir = OUT_DIR / ("obj_trace" if trace else "obj")
     objdir.mkdir(exist_ok=True)
+    out = TRACE_LIB if trace else LIB
+    extra = ("-DDF_TRACE",) if trace else ()
     sources = sorted(CSRC.glob("*.hip"))
     objs = [objdir / (s.stem + ".o") for s in sources]
     with ThreadPoolExecutor(max_workers=min(8, len(sources))) as pool:
-        list(pool.map(lambda pair: _compile(*pair), zip(sources, objs)))
-    tmp = LIB.with_suffix(".so.tmp")
+        list(pool.map(lambda pair: _compile(*pair, extra), zip(sources, objs)))
+    tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    tmp.replace(LIB)
+    tmp.replace(out)
     if verbose:
-        print(f"built {LIB.relative_to(ROOT)} from {len(sources)} sources for {ARCH}")
-    return LIB
+        print(f"built {out.relative_to(ROOT)} from {len(sources)} sources for {ARCH}")
+    return out
 
 
 if __name__ == "__main__":
-    build()
+    build(trace="--trace" in sys.argv[1:])

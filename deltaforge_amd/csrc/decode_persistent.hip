@@ -31,16 +31,20 @@
 // ds_read so the compiler does not insert a vmcnt(0) before them (it cannot tell which
 // slot a DMA targets); the kernel waits explicitly for exactly the block it consumes.
 //
-// GEMV arithmetic (fp16 MFMA). A block's B operand holds each nibble in the mantissa of an
-// fp16 with exponent 2^10: 1024 + n (nibble in bits 0..3 of a half) or 1024 + 16 n (bits
-// 4..7), so one shift and four v_and_or build 8 weights from a dword (5 VALU ops). The input
-// row is staged in fp16 as x' = x, or x / 16 at the 1024 + 16 n positions (k % 8 in 2, 3, 6,
-// 7); bf16 activations are exact in fp16 within its normal range. Per 128-group the MFMA gives
-// D = sum x'_k B_k = sum x_k n_k + 1024 sum x'_k, and y += s * (D - xs) with the staged
-// xs = 1024 sum x'_k + 8 sum x_k, i.e. y += s * sum x_k (n_k - 8). This is the reference's
-// sum x_k * ((n_k - 8) * s) with the scale applied once per group instead of rounding each
-// weight to bf16 first: the per-weight bf16 rounding the reference does (relative 2^-9) is
-// not reproduced, which moves outputs by well under the bf16 tolerance.
+// GEMV arithmetic (fp16 MFMA). A block's B operand holds each nibble as an fp16 subnormal: one
+// shift and four v_and per dword leave nibble n in bits 0..3 of a half (the value n * 2^-24) or
+// in bits 4..7 (16 n * 2^-24), 5 VALU ops per 8 weights and no offset to cancel. The input row
+// is staged in fp16 as x' = x, or x / 16 where the weight carries the extra 16 (k % 8 in 2, 3,
+// 6, 7). Per 128-group the MFMA gives D = 2^-24 sum x_k n_k, a sum of exact products in fp32, and
+// with the group's c = 8 * 2^-24 sum x_k, y += (s 2^24) (D - c) = s sum x_k (n_k - 8). That is
+// the reference's sum x_k * bf16((n_k - 8) s) without the per-weight bf16 rounding (relative
+// 2^-9), i.e. the exact-weight product; D and c differ by about the ratio of the group's mean to
+// its spread, so the subtraction costs a few of fp32's 24 bits.
+// Range: fp16 holds every bf16 value below 2^15 = 32768 exactly in its normal range (values
+// under 2^-14 become subnormals, an absolute error under 2^-25). RMSNorm outputs are bounded by
+// sqrt(hidden) * max |1 + w| (the host refuses norm weights that could reach 2^15); the other
+// GEMV inputs (SwiGLU, GatedRMSNorm, attention outputs) are checked as they are staged, and a
+// value at or above 2^15 aborts the launch (kErrRange) rather than overflow to inf.
 //
 // Other arithmetic is the per-op kernels' (gated_delta.hip, attention.hip, small_ops.hip),
 // with the reference's rounding points; only fp32 summation orders differ.
@@ -85,14 +89,16 @@ constexpr int kTileKeys = kCompute * 16;            // 128 keys per attention ti
 constexpr int kSplits = 2 * kPerXcd;                // key splits of a KV head over its XCD pair
 constexpr int kPairHeads = 4;                       // query heads of a KV head (2 per XCD of the pair);
                                                     // an XCD's own two are its slots 0, 1
-// factored int4 dot product: B = fp16(1024 + n) or fp16(1024 + 16 n) (see the file comment)
-constexpr uint32_t kBiasPair = 0x64006400u;         // fp16 1024.0 in both halves
+// int4 dot product: B = the nibbles as fp16 subnormals, the input row staged as fp16 (see the
+// file comment)
 typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 df_f16x8;
+constexpr float kStageMax = 32768.0f;               // staged inputs must lie below 2^15
+constexpr float kTwo24 = 16777216.0f;                // 2^24, the subnormal weights' scale
 
-// The fp16 GEMV input x' of element k (x / 16 where the weight enters as 1024 + 16 n), and
-// its term of the group correction xs = 1024 sum x' + 8 sum x.
+// The fp16 GEMV input x' of element k (x / 16 where the weight carries the factor 16), and its
+// term of the group sum c = 8 * 2^-24 sum x.
 DF_DEVICE _Float16 xh_of(float x, int k) { return static_cast<_Float16>((k & 2) ? x * 0.0625f : x); }
-DF_DEVICE float xs_term(float x, _Float16 xh) { return 1024.0f * static_cast<float>(xh) + 8.0f * x; }
+DF_DEVICE float c_of(float sum_x) { return sum_x * (8.0f / kTwo24); }
 DF_DEVICE uint32_t pack_h2(_Float16 a, _Float16 b) {
   return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) | (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
 }
@@ -100,7 +106,8 @@ DF_DEVICE uint32_t pack_h2(_Float16 a, _Float16 b) {
 constexpr uint64_t kTimeout = 50000000ull;          // 0.5 s of s_memrealtime (100 MHz)
 constexpr int kRegBase = 4;                         // ctl[4..11]: per-XCD registration tickets
 
-enum Err : int { kErrNone = 0, kErrTimeout = 1, kErrXcd = 2, kErrPosition = 3, kErrToken = 4, kErrSchedule = 5 };
+enum Err : int { kErrNone = 0, kErrTimeout = 1, kErrXcd = 2, kErrPosition = 3, kErrToken = 4, kErrSchedule = 5,
+                 kErrRange = 6 };
 
 struct Ws {
   int* ctl;          // [16]: epoch, abort, error, -, 8 registration tickets, -
@@ -259,7 +266,7 @@ struct Lds {
   __align__(16) uint16_t nw[kMaxHidden];         // the next RMSNorm's weight (LDS DMA, a phase ahead)
   __align__(16) uint16_t gnw[kDk];               // GatedRMSNorm weight (LDS DMA, a phase ahead)
   __align__(16) float zs[512];                   // out_proj: SiLU inputs of the GatedRMSNorm (staged during delta)
-  float xs[kMaxGroups];                          // each 128-group's 1024 sum x' + 8 sum x
+  float xs[kMaxGroups];                          // each 128-group's c = 8 * 2^-24 sum x
   float ss;                                      // sum of squares of h (for the next RMSNorm)
   __align__(16) float part[kMaxWgTiles][16][kCompute];  // per-wave tile partials (a column's 8 adjacent)
   float red[64];
@@ -288,7 +295,7 @@ struct Lds {
       float vraw[kHd];
       __align__(16) uint16_t qn_w[kHd];
       __align__(16) uint16_t kn_w[kHd];
-      float inv[kRot / 2];
+      uint32_t rope[kRot / 2];                   // this position's RoPE row (cos | sin << 16)
       float sc[2][kTileKeys];
       float alpha[2];
       float ml[2][2];
@@ -310,7 +317,7 @@ struct Lds {
       float vraw[kHd];
       __align__(16) uint16_t qn_w[kHd];
       __align__(16) uint16_t kn_w[kHd];
-      float inv[kRot / 2];
+      uint32_t rope[kRot / 2];                   // this position's RoPE row (cos | sin << 16)
       float sc[kPairHeads][kTileKeys];
       float alpha[kPairHeads];
       float ml[kPairHeads][2];
@@ -389,11 +396,18 @@ struct Geo {
 // staged after the hand-off, 30 signalled).
 enum Tag : int { kTProj = 1, kTDelta, kTOut, kTAttn, kTMerge, kTOProj, kTGateUp, kTDown, kTHead, kTEmbed,
                  kTReduce, kTStaged = 20, kTSignal = 30 };
+// Compiled in only with DF_TRACE defined (a separate build of the library): the stamps' code sits
+// between the phases of every token, in the instruction cache the decode depends on.
 DF_DEVICE void stamp(Ctx& c, int tag) {
+#ifdef DF_TRACE
   if (__builtin_expect(c.tr != nullptr, 0)) {  // only workgroup (0, 0)'s control wave, traced step
     if (c.lane == 0 && c.tn < c.tcap) c.tr[c.tn] = (now() << 8) | static_cast<uint64_t>(tag);
     c.tn += 1;
   }
+#else
+  (void)c;
+  (void)tag;
+#endif
 }
 
 // Re-derive the thread's coordinates at the start of a phase behind an opaque asm, so the
@@ -489,7 +503,7 @@ DF_DEVICE bool poll_tagged(const Ctx& c, F&& load) {
 // ---------------------------------------------------------------------------------------
 
 // Compute waves (1 barrier; the control wave passes 1): x = bf16(RMSNorm(h) * (1 + w)) over
-// `hidden` (w staged in L.nw) as the fp16 row g_xh, and the group corrections L.xs. Every wave sums the squares of
+// `hidden` (w staged in L.nw) as the fp16 row g_xh, and the group sums L.xs. Every wave sums the squares of
 // all of h itself (identical code and order in every wave, so all agree on the factor), which
 // saves the cross-wave exchange and its barrier; a wave then produces whole 128-groups
 // (2 elements per lane).
@@ -503,9 +517,8 @@ DF_DEVICE void norm_w(Lds& L, Ctx& c, int hidden, float eps) {
     const uint32_t wv = *reinterpret_cast<const uint32_t*>(&L.nw[k]);
     const float x0 = round_bf(__uint_as_float(hv << 16) * r * (1.0f + __uint_as_float(wv << 16)));
     const float x1 = round_bf(__uint_as_float(hv & 0xFFFF0000u) * r * (1.0f + __uint_as_float(wv & 0xFFFF0000u)));
-    const _Float16 h0 = xh_of(x0, k), h1 = xh_of(x1, k + 1);
-    *reinterpret_cast<uint32_t*>(&g_xh[k]) = pack_h2(h0, h1);
-    const float sg = dsum(xs_term(x0, h0) + xs_term(x1, h1));
+    *reinterpret_cast<uint32_t*>(&g_xh[k]) = pack_h2(xh_of(x0, k), xh_of(x1, k + 1));
+    const float sg = c_of(dsum(x0 + x1));
     if (c.lane == 0) L.xs[g] = sg;
   }
   sync(c);
@@ -899,35 +912,33 @@ DF_DEVICE void take_pair(Stream& st, const Ctx& c, const uint16_t* xg0, const ui
 
 // Row 0 of one block's product: lanes 0..15 return s_col * sum_k x_k (n_k - 8) over the
 // block's 128 k (x = the group's fp16 input chunks x' at this lane's k slot, xs = the group's
-// correction, sh = 16 * (lane & 1) selects this lane's scale in the dword). A dword's nibble
-// pairs (bits 4j, 16 + 4j) become the fp16 pairs (w & m_lo) | bias, (w & m_hi) | bias,
-// ((w >> 8) & m_lo) | bias, ((w >> 8) & m_hi) | bias: weights 1024 + n for k % 8 in 0, 1, 4, 5
-// and 1024 + 16 n for k % 8 in 2, 3, 6, 7. The masks and bias arrive as opaque register values
-// (masks in SGPRs, bias in a VGPR), so the compiler emits one v_and_or_b32 each (gfx9 VOP3
+// c, sh = 16 * (lane & 1) selects this lane's scale in the dword). A dword's nibble pairs
+// (bits 4j, 16 + 4j) become the fp16 pairs w & m_lo, w & m_hi, (w >> 8) & m_lo, (w >> 8) & m_hi:
+// subnormals n * 2^-24 for k % 8 in 0, 1, 4, 5 and 16 n * 2^-24 for k % 8 in 2, 3, 6, 7. The
+// masks arrive as opaque SGPR values, so the compiler emits one v_and_b32 each (gfx9 VOP3
 // encodes no literal) and its hazard checks still cover the results, which feed an MFMA.
 struct DotK {
-  uint32_t mlo, mhi, bias;
+  uint32_t mlo, mhi;
 };
 // Made once per loop, outside it: opaque to the compiler, so they stay in registers.
 DF_DEVICE DotK dot_consts() {
-  DotK k{0x000F000Fu, 0x00F000F0u, kBiasPair};
+  DotK k{0x000F000Fu, 0x00F000F0u};
   asm volatile("" : "+s"(k.mlo), "+s"(k.mhi));
-  asm volatile("" : "+v"(k.bias));
   return k;
 }
 DF_DEVICE float block_dot_r(const uint4& wv, uint32_t sd, const uint4 (&x)[4], float xs, uint32_t sh, const DotK& K) {
   const float s = __uint_as_float((sd >> sh) << 16);
   const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
-  const uint32_t mlo = K.mlo, mhi = K.mhi, bias = K.bias;
+  const uint32_t mlo = K.mlo, mhi = K.mhi;
   df_f32x4 d4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
     const uint32_t w = words[d], t = w >> 8;
-    const uint4 bw = make_uint4((w & mlo) | bias, (w & mhi) | bias, (t & mlo) | bias, (t & mhi) | bias);
+    const uint4 bw = make_uint4(w & mlo, w & mhi, t & mlo, t & mhi);
     d4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(df_f16x8, x[d]), __builtin_bit_cast(df_f16x8, bw),
                                                 d4, 0, 0, 0);
   }
-  return s * (d4[0] - xs);
+  return (s * kTwo24) * (d4[0] - xs);
 }
 
 // Single-block form reading its input from LDS.
@@ -1186,7 +1197,7 @@ DF_DEVICE void stage_gu(const Ctx& c, int inter_x, float* gu) {
 }
 
 // Compute waves (1 barrier; the control wave passes 1): the down projection's input
-// act = bf16(bf16(silu(g)) * u) as the fp16 row g_xh, and its group corrections L.xs. The gate|up columns come
+// act = bf16(bf16(silu(g)) * u) as the fp16 row g_xh, and its group sums L.xs. The gate|up columns come
 // in 32-column pairs (16 gate columns, then their 16 up columns), so act j reads gate
 // column 32 (j / 16) + j % 16 and the up column 16 further. A wave produces whole
 // 128-groups (2 elements per lane).
@@ -1200,9 +1211,9 @@ DF_DEVICE void swiglu_act(Lds& L, Ctx& c, int inter_x) {
     const float2 uv = *reinterpret_cast<const float2*>(gu + col + 16);
     const float x0 = round_bf(round_bf(silu(round_bf(gv.x))) * round_bf(uv.x));
     const float x1 = round_bf(round_bf(silu(round_bf(gv.y))) * round_bf(uv.y));
-    const _Float16 h0 = xh_of(x0, j), h1 = xh_of(x1, j + 1);
-    *reinterpret_cast<uint32_t*>(&g_xh[j]) = pack_h2(h0, h1);
-    const float sg = dsum(xs_term(x0, h0) + xs_term(x1, h1));
+    if (!__all(fmaxf(fabsf(x0), fabsf(x1)) < kStageMax)) raise_abort(c, kErrRange);
+    *reinterpret_cast<uint32_t*>(&g_xh[j]) = pack_h2(xh_of(x0, j), xh_of(x1, j + 1));
+    const float sg = c_of(dsum(x0 + x1));
     if (c.lane == 0) L.xs[g] = sg;
   }
   sync(c);
@@ -1210,7 +1221,7 @@ DF_DEVICE void swiglu_act(Lds& L, Ctx& c, int inter_x) {
 
 // Control wave: the XCD's 512 merged attention / delta outputs (tagged bf16, published by the
 // workgroups of the XCD at epoch `want`) into g_x (the GatedRMSNorm's input) or, as the GEMV
-// input itself (`direct`), into g_xh with the group corrections L.xs of its four 128-groups
+// input itself (`direct`), into g_xh with the group sums L.xs of its four 128-groups
 // (a group is one 16-lane row of 8 values per lane).
 DF_DEVICE bool stage_core(Lds& L, const Ctx& c, uint32_t want, bool direct) {
   const auto r = rsrc(c.w.core + (size_t)c.xcd * 512);
@@ -1226,18 +1237,19 @@ DF_DEVICE bool stage_core(Lds& L, const Ctx& c, uint32_t want, bool direct) {
   if (!direct) {
     *reinterpret_cast<uint4*>(&g_x[c.lane * 8]) = v;
   } else {
-    float s = 0.0f;
+    float s = 0.0f, amax = 0.0f;
     uint32_t hw[4];
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {  // elements 8 lane + 2 e, + 1
       const float x0 = __uint_as_float(w[e] << 16), x1 = __uint_as_float(w[e] & 0xFFFF0000u);
-      const _Float16 h0 = xh_of(x0, 2 * e), h1 = xh_of(x1, 2 * e + 1);
-      hw[e] = pack_h2(h0, h1);
-      s += xs_term(x0, h0) + xs_term(x1, h1);
+      hw[e] = pack_h2(xh_of(x0, 2 * e), xh_of(x1, 2 * e + 1));
+      s += x0 + x1;
+      amax = fmaxf(amax, fmaxf(fabsf(x0), fabsf(x1)));
     }
+    if (!__all(amax < kStageMax)) raise_abort(c, kErrRange);
     *reinterpret_cast<uint4*>(&g_xh[c.lane * 8]) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    s = row_sum(s);
+    s = c_of(row_sum(s));
     if ((c.lane & 15) == 0) L.xs[c.lane >> 4] = s;
   }
   return true;
@@ -1535,7 +1547,8 @@ DF_DEVICE bool dn_step(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_in, uint32_t 
 // ---------------------------------------------------------------------------------------
 
 // RMSNorm(1+w) over 256 dims held 4 per lane, then partial RoPE (attention.hip's order).
-DF_DEVICE void norm_rope4_lds(float x[4], const uint16_t* nw, float eps, const float* inv, float posf, int lane) {
+// rope: this position's row of the RoPE table in LDS, rotary pair j as bf16 cos | bf16 sin << 16.
+DF_DEVICE void norm_rope4_lds(float x[4], const uint16_t* nw, float eps, const uint32_t* rope, int lane) {
   float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
   ss = dsum(ss);
   const float r = 1.0f / sqrtf(ss / static_cast<float>(kHd) + eps);
@@ -1547,15 +1560,11 @@ DF_DEVICE void norm_rope4_lds(float x[4], const uint16_t* nw, float eps, const f
 #pragma unroll
   for (int i = 0; i < 4; ++i) partner[i] = dpp<kDppRor8>(n[i]);  // lane ^ 8 = (lane + 8) mod 16 in a row
   static_assert(half / 4 == 8, "the partner of a rotary dim is 8 lanes away");
-  // lane j < half holds the angle of rotary pair j (one cosf / sinf per lane instead of one
-  // per element: the library's argument reduction is large code); lane 4l + i's element reads
-  // pair (4l + i) % half from there
-  const float ang = posf * inv[lane & (half - 1)];
-  const float cs_l = round_bf(cosf(ang)), sn_l = round_bf(sinf(ang));
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int dim = lane * 4 + i;
-    const float cs = __shfl(cs_l, dim & (half - 1), 64), sn = __shfl(sn_l, dim & (half - 1), 64);
+    const uint32_t cw = rope[dim & (half - 1)];
+    const float cs = bf2f(static_cast<uint16_t>(cw)), sn = bf2f(static_cast<uint16_t>(cw >> 16));
     if (dim < kRot) {
       const float rotated = dim < half ? -partner[i] : partner[i];
       x[i] = round_bf(round_bf(n[i] * cs) + round_bf(rotated * sn));
@@ -1911,10 +1920,10 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
             const float t1 = round_bf(bf2f(L.gnw[64 + c.lane]) * round_bf(v1 * rr));
             const float xv0 = round_bf(t0 * silu(L.zs[i0]));
             const float xv1 = round_bf(t1 * silu(L.zs[i1]));
-            const _Float16 h0 = xh_of(xv0, i0), h1 = xh_of(xv1, i1);
-            g_xh[i0] = __builtin_bit_cast(uint16_t, h0);
-            g_xh[i1] = __builtin_bit_cast(uint16_t, h1);
-            const float gs = dsum(xs_term(xv0, h0)) + dsum(xs_term(xv1, h1));
+            if (!__all(fmaxf(fabsf(xv0), fabsf(xv1)) < kStageMax)) raise_abort(c, kErrRange);
+            g_xh[i0] = __builtin_bit_cast(uint16_t, xh_of(xv0, i0));
+            g_xh[i1] = __builtin_bit_cast(uint16_t, xh_of(xv1, i1));
+            const float gs = c_of(dsum(xv0 + xv1));
             if (c.lane == 0) L.xs[c.wave] = gs;
           }
           sync(c);
@@ -1932,14 +1941,13 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           auto& A = L.u.at4;
           sync(c);  // q/k/v staged
           if (!L.ok) return stop();
-          const float posf = static_cast<float>(c.pos);
           const int nh = at_pair(c.pos + 1) ? kPairHeads : 2;  // head slots in use
           if (c.wave < nh || c.wave == kPairHeads) {  // waves 0..nh-1: the query heads, wave 4: the new key
             const bool qw = c.wave < kPairHeads;
             float x[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) x[i] = qw ? A.qraw[c.wave][c.lane * 4 + i] : A.kraw[c.lane * 4 + i];
-            norm_rope4_lds(x, qw ? A.qn_w : A.kn_w, M.eps, A.inv, posf, c.lane);
+            norm_rope4_lds(x, qw ? A.qn_w : A.kn_w, M.eps, A.rope, c.lane);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               if (qw) A.q[c.wave][c.lane * 4 + i] = f2bf(x[i]);
@@ -2027,12 +2035,11 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           auto& A = L.u.at;
           sync(c);  // q/k/v staged
           if (!L.ok) return stop();
-          const float posf = static_cast<float>(c.pos);
           if (c.wave < 3) {
             float x[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) x[i] = c.wave < 2 ? A.qraw[c.wave][c.lane * 4 + i] : A.kraw[c.lane * 4 + i];
-            norm_rope4_lds(x, c.wave < 2 ? A.qn_w : A.kn_w, M.eps, A.inv, posf, c.lane);
+            norm_rope4_lds(x, c.wave < 2 ? A.qn_w : A.kn_w, M.eps, A.rope, c.lane);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               if (c.wave < 2) A.q[c.wave][c.lane * 4 + i] = f2bf(x[i]);
@@ -2186,7 +2193,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
   const int step0 = M.step ? *M.step : 0;
   int64_t token = M.tokens[0];
   dma_row(LF(layer_at(M, 0), in_norm), L.nw, hidden, c.lane);
-  float pre_inv = 0.0f;  // inv_freq of the next attention layer's RoPE
+  uint32_t pre_rope = 0;  // the next attention layer's RoPE row entry of this lane
   auto fail = [&](int nbars) {  // pass the barriers the compute waves still wait at, then stop
     if (c.lane == 0) L.ok = 0;
     for (int i = 0; i < nbars; ++i) bar();
@@ -2289,7 +2296,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           dma_row128(LF(Lp, q_norm) + 128, qn_w + 128, c.lane);
           dma_row128(LF(Lp, k_norm), kn_w, c.lane);
           dma_row128(LF(Lp, k_norm) + 128, kn_w + 128, c.lane);
-          pre_inv = c.lane < kRot / 2 ? M.inv_freq[c.lane] : 0.0f;
+          pre_rope = c.lane < kRot / 2 ? M.rope[(size_t)c.pos * (kRot / 2) + c.lane] : 0u;
         }
         sync(c);  // blocks consumed
         c.epoch += 1;
@@ -2325,7 +2332,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           auto& A = L.u.at4;
           {
             if (!gather_attn(c, A.qraw, A.kraw, c.epoch, at_pair(c.pos + 1))) return fail(1);  // kraw, vraw adjacent
-            if (c.lane < kRot / 2) A.inv[c.lane] = pre_inv;
+            if (c.lane < kRot / 2) A.rope[c.lane] = pre_rope;
             if (c.lane < kPairHeads) {
               A.ml[c.lane][0] = -INFINITY;
               A.ml[c.lane][1] = 0.0f;
@@ -2457,7 +2464,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           {
             const Seg seg[3] = {{0, kHd, A.qraw[0]}, {512, kHd, A.qraw[1]}, {kAttnK, 2 * kHd, A.kraw}};
             if (!gather_colpar<3, 8>(c, seg, c.epoch)) return fail(1);  // kraw and vraw are adjacent in LDS
-            if (c.lane < kRot / 2) A.inv[c.lane] = pre_inv;
+            if (c.lane < kRot / 2) A.rope[c.lane] = pre_rope;
             if (c.lane < 2) {
               A.ml[c.lane][0] = -INFINITY;
               A.ml[c.lane][1] = 0.0f;
@@ -2759,7 +2766,7 @@ extern "C" int df_decode_persistent(const DfPersistModel* model, int steps, int 
   DfPersistModel m = *model;
   if (m.hidden <= 0 || m.hidden > kMaxHidden || m.hidden % 512 || m.inter <= 0 || m.inter % 1024 ||
       m.vocab <= 0 || m.vocab % 128 || m.vocab > (1 << 18) || m.num_layers < 1 || m.num_layers > kMaxLayers || m.max_len < 1 || !m.layers ||
-      !m.head_w || !m.head_s || !m.final_norm || !m.inv_freq || !m.position || !m.tokens)
+      !m.head_w || !m.head_s || !m.final_norm || !m.rope || !m.position || !m.tokens)
     return DF_BAD_ARGUMENT;
   if (2 * (m.inter / kXcd) > kColparMax) return DF_BAD_ARGUMENT;
   if (m.inter / kXcd / kGroup > kMaxGroups || m.hidden / kGroup > kMaxGroups) return DF_BAD_ARGUMENT;

@@ -22,7 +22,7 @@ from . import ops
 from .config import FULL_ATTENTION, SIGMOID_GATE, ModelConfig
 from .synth import SynthModel, inv_freq
 
-__all__ = ["PersistentDecoder", "attention_proj_columns", "check_geometry", "linear_proj_columns"]
+__all__ = ["PersistentDecoder", "attention_proj_columns", "check_geometry", "check_norm_range", "linear_proj_columns", "rope_table"]
 
 BF16 = torch.bfloat16
 XCD = 8
@@ -30,7 +30,8 @@ LIN_COLS = 1552  # per XCD: q 256, k 256, v 512, z 512, a 4, b 4, 8 zero columns
 ATTN_COLS = 1536  # per XCD: 2 x (query 256 | gate 256), k 256, v 256
 ERRORS = {1: "a cross-workgroup hand-off timed out", 2: "a workgroup ran on an unexpected XCD",
           3: "position, prompt or token log out of range", 4: "token id out of range",
-          5: "control/compute barrier schedules disagree"}
+          5: "control/compute barrier schedules disagree",
+          6: "a GEMV input reached 2^15, beyond the kernel's fp16 staging range"}
 
 
 def linear_proj_columns(c: ModelConfig) -> torch.Tensor:
@@ -75,6 +76,32 @@ def _select_cols(packed: torch.Tensor, scale: torch.Tensor, cols: torch.Tensor):
     return p.contiguous(), s.contiguous()
 
 
+def rope_table(c: ModelConfig, max_len: int) -> torch.Tensor:
+    """The persistent kernel's RoPE table: int32 ``[max_len, rotary/2]``, pair j of position p
+    as ``bf16(cos(p * f_j)) | bf16(sin(p * f_j)) << 16``, where ``f_j`` is the bf16-rounded
+    inverse frequency and the angle is an fp32 product: the reference's cos/sin
+    (reference.py:165-200 with the module buffer cast to bf16), computed once on the host
+    instead of by the kernel for every attention layer of every token."""
+    f = inv_freq(c)  # fp32 holding the bf16-rounded values
+    ang = torch.arange(max_len, dtype=torch.float32).unsqueeze(1) * f.unsqueeze(0)
+    cs = ang.cos().to(torch.bfloat16).view(torch.int16).to(torch.int32) & 0xFFFF
+    sn = ang.sin().to(torch.bfloat16).view(torch.int16).to(torch.int32) & 0xFFFF
+    return (cs | (sn << 16)).contiguous()
+
+
+def check_norm_range(config: ModelConfig, params: dict) -> None:
+    """The persistent kernel stages RMSNorm outputs in fp16 unchecked: x = h r (1 + w) with
+    sum (h r)^2 <= hidden, so |x| <= sqrt(hidden) * max |1 + w|, which must stay below 2^15 for
+    every RMSNorm weight (the layers' input and post-attention norms and the final norm)."""
+    bound = 32768.0 / config.hidden_size ** 0.5
+    for name, w in params.items():
+        if name == "norm.weight" or name.endswith("input_layernorm.weight") or name.endswith("post_attention_layernorm.weight"):
+            peak = float((1.0 + w.float()).abs().max())
+            if peak >= bound:
+                raise ValueError(f"{name}: max |1 + w| = {peak:.4g} reaches {bound:.4g}, where the persistent "
+                                 f"kernel's fp16 staging of the normed row could overflow")
+
+
 def check_geometry(c: ModelConfig) -> None:
     ok = (c.linear_num_key_heads == 16 and c.linear_num_value_heads == 32 and c.linear_key_head_dim == 128
           and c.linear_value_head_dim == 128 and c.num_attention_heads == 16 and c.num_key_value_heads == 4
@@ -101,6 +128,7 @@ class PersistentDecoder:
         self.max_new_tokens = max_new_tokens
         self.device = dev = torch.device(device)
         ops.require_gpu(torch.empty(0, device=dev), "decode_persistent")
+        check_norm_range(c, model.params)
         p = {k: v.to(dev) for k, v in model.params.items()}
         lin = model.linears
 
@@ -165,7 +193,7 @@ class PersistentDecoder:
         self.params = p
         self.head = repack(lin["lm_head"].packed, lin["lm_head"].scale)
         self.final_norm = p["norm.weight"]
-        self.inv_freq = inv_freq(c).to(dev)
+        self.rope = rope_table(c, max_seq_len).to(dev)
         # a checkpoint's own bf16 embedding table (``checkpoint.load_checkpoint``); without one the
         # token rows come from the tied int4 head, which is the synthetic model's table
         table = p.get("embed_tokens.weight")
@@ -202,7 +230,7 @@ class PersistentDecoder:
         m.layers = self.layers_dev.data_ptr()
         m.head_w, m.head_s = self.head.w.data_ptr(), self.head.s.data_ptr()
         m.final_norm = self.final_norm.data_ptr()
-        m.inv_freq = self.inv_freq.data_ptr()
+        m.rope = self.rope.data_ptr()
         m.position, m.tokens = self.position.data_ptr(), self.tokens.data_ptr()
         m.prompt, m.prompt_len = self.prompt.data_ptr(), self.prompt_len
         m.token_log, m.log_capacity = self.token_log.data_ptr(), self.max_new_tokens
@@ -216,7 +244,9 @@ class PersistentDecoder:
     def trace_decode(self, steps: int, trace_step: int) -> list[int]:
         """Greedy ``steps`` with the phase trace of step ``trace_step``: the s_memrealtime
         (100 MHz) stamps workgroup (XCD 0, rank 0) takes at each phase's start, after its
-        hand-off, and at its signal."""
+        hand-off, and at its signal. Only the traced build of the library stamps
+        (``python -m deltaforge_amd.build --trace``, loaded with ``lib=``); the product build
+        compiles the stamps out and returns an empty list."""
         self._trace = torch.zeros(4096, dtype=torch.int64, device=self.device)
         self._trace_step = trace_step
         try:

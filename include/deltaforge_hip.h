@@ -377,7 +377,9 @@ typedef struct DfPersistModel {
   const uint8_t* head_w;           /* tied head, natural columns: K = hidden, N = vocab  */
   const uint16_t* head_s;
   const uint16_t* final_norm;      /* [hidden]                                           */
-  const float* inv_freq;           /* [32] bf16-rounded inverse frequencies, as fp32     */
+  const uint32_t* rope;            /* [max_len][32] RoPE table: rotary pair j of position */
+                                   /* p as bf16(cos(p * f_j)) | bf16(sin(p * f_j)) << 16, */
+                                   /* f_j the bf16-rounded inverse frequency (fp32 angle) */
   int* position;                   /* tokens already cached (read at launch, advanced)   */
   int64_t* tokens;                 /* [1] token the next step embeds (argmax written back) */
   const int64_t* prompt;           /* [prompt_len], teacher-forced steps read prompt[pos] */
@@ -388,7 +390,8 @@ typedef struct DfPersistModel {
   uint16_t* logits;                /* [vocab] bf16 logits of the last step (or NULL)     */
   uint64_t* trace;                 /* optional: s_memrealtime (100 MHz) stamps of one    */
   int trace_step;                  /* step's phases (start, staged, end), as seen by     */
-  int trace_capacity;              /* workgroup (XCD 0, rank 0); NULL disables           */
+  int trace_capacity;              /* workgroup (XCD 0, rank 0); NULL disables. Honoured */
+                                   /* only by a build with DF_TRACE defined              */
   const uint16_t* embed_table;     /* [vocab][hidden] bf16 embedding rows, or NULL to    */
                                    /* embed from the int4 head (the tied table)          */
 } DfPersistModel;

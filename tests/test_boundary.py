@@ -364,3 +364,35 @@ def test_registry_index_detects_an_entry_changed_behind_its_back():
     assert reg.champion("rms_norm") is None
     reg.promote("b")
     assert reg.champion("rms_norm").name == "b"
+
+
+def test_persistent_rope_table_matches_the_oracle_bit_for_bit():
+    """The persistent kernel reads cos/sin from a host-built table: pair j of position p must be
+    the oracle's bf16 cos/sin of p * bf16(inv_freq_j) (reference.py:165-200)."""
+    from deltaforge_amd.config import qwen3_5_4b_config
+    from deltaforge_amd.persistent import rope_table
+    from oracle.model import rope_cos_sin
+
+    cfg = qwen3_5_4b_config()
+    positions = torch.tensor([0, 1, 2, 7, 4095, 4096, 32767, 131071])
+    table = rope_table(cfg, 131072)[positions]
+    cos, sin = rope_cos_sin(positions.view(1, -1), cfg, torch.bfloat16, inv_freq_dtype=torch.bfloat16)
+    half = cfg.rotary_dim // 2
+    want_cos = cos[0, :, :half].contiguous().view(torch.int16).to(torch.int32) & 0xFFFF
+    want_sin = sin[0, :, :half].contiguous().view(torch.int16).to(torch.int32) & 0xFFFF
+    assert torch.equal(table & 0xFFFF, want_cos)
+    assert torch.equal((table >> 16) & 0xFFFF, want_sin)
+
+
+def test_persistent_refuses_norm_weights_beyond_the_fp16_staging_range():
+    from deltaforge_amd import synth
+    from deltaforge_amd.persistent import check_norm_range
+
+    cfg = mid_config(4)
+    params = dict(synth.synth_model(cfg, seed=0).params)
+    check_norm_range(cfg, params)  # the synthetic model's (1 + w) ~ 1
+    bound = 32768.0 / cfg.hidden_size ** 0.5
+    w = params["layers.2.post_attention_layernorm.weight"].clone()
+    w[7] = bound  # 1 + w just above the bound
+    with pytest.raises(ValueError, match="post_attention_layernorm"):
+        check_norm_range(cfg, {**params, "layers.2.post_attention_layernorm.weight": w})

@@ -180,3 +180,26 @@ def test_greedy_decode_through_the_promoted_persistent_candidate(mid):
     assert got[0, :4].tolist() == ref_tokens[0, :4].tolist()
     again = greedy_decode(model, prompt, 6)
     assert torch.equal(again, got)
+
+
+def test_persistent_aborts_when_a_gemv_input_leaves_the_fp16_range(mid):
+    """The persistent kernel stages GEMV inputs in fp16, exact below 2^15. A SwiGLU output at or
+    above 2^15 (one layer's up_proj scales raised 10^5-fold, so act = silu(g) * u reaches ~10^5)
+    must abort the launch with the range error instead of computing with inf; the per-op engine,
+    whose bf16 dequant has no such limit, decodes the same model to finite logits."""
+    from deltaforge_amd._native import NativeError
+
+    cfg, model, prompt, _, _ = mid
+    big = synth.SynthModel(config=model.config, params=dict(model.params), linears=dict(model.linears))
+    up = big.linears["layers.1.mlp.up_proj.weight"]
+    big.linears["layers.1.mlp.up_proj.weight"] = dataclasses.replace(
+        up, scale=(up.scale.float() * 1e5).to(up.scale.dtype))
+    eng = DecodeEngine(big, max_seq_len=64, max_new_tokens=16)
+    eng.prefill(prompt[:, :4].cuda())
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(eng.logits.float()).all())
+    dec = PersistentDecoder(big, max_seq_len=64, max_new_tokens=16)
+    for _ in range(2):  # the abort leaves the decoder usable after reset (prefill resets)
+        dec.prefill(prompt[:, :4].cuda())
+        with pytest.raises(NativeError, match="fp16 staging range"):
+            dec.check()
