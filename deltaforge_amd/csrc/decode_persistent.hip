@@ -75,7 +75,7 @@ constexpr int kMaxGroups = 24;                      // 128-groups of a GEMV phas
 constexpr int kMaxHeadTiles = 64;                   // head tiles per workgroup
 constexpr int kColparMax = 2304;
 // Gated DeltaNet geometry
-constexpr int kKH = 16, kVH = 32, kDk = 128;
+constexpr int kKH = 16, kDk = 128;
 constexpr int kKeyDim = kKH * kDk;                  // 2048
 constexpr int kLinCols = 1552;
 constexpr int kLinQ = 0, kLinK = 256, kLinV = 512, kLinZ = 1024, kLinA = 1536;
@@ -279,12 +279,15 @@ struct Lds {
     int bi[kCompute];
   } hd;
   union {
-    struct {                                     // Gated DeltaNet step (control wave)
+    struct {                                     // Gated DeltaNet step
       __align__(16) float4 S[kDk / 16][64];      // state slice by DMA: [row block][lane]
       float qkv_in[kDnCh];                       // pre-conv inputs: q 128, k 128, v 16
-      __align__(16) float q[kDk], k[kDk], v[16];
-      float sred[4][16];                         // per 16-lane row: column sums
+      __align__(16) uint2 cw[kDnCh];             // their conv taps (bf16 x 4)
+      __align__(16) uint2 hist[kDnCh];           // their conv history ring (bf16 x 4)
+      float y[kDnCh];                            // conv + SiLU outputs
+      float core[16];                            // the unit's 16 outputs
       float ab8[8];                              // a of the XCD's 4 value heads, then b
+      float gp[2];                               // A_log, dt_bias of the unit's value head
     } dn;
     struct {                                     // attention split
       __align__(16) uint16_t q[2][kHd];
@@ -395,7 +398,12 @@ struct Geo {
 // Phase trace of the traced step: s_memrealtime << 8 | tag (tags: 1-15 phase starts, 20
 // staged after the hand-off, 30 signalled).
 enum Tag : int { kTProj = 1, kTDelta, kTOut, kTAttn, kTMerge, kTOProj, kTGateUp, kTDown, kTHead, kTEmbed,
-                 kTReduce, kTStaged = 20, kTSignal = 30 };
+                 kTReduce, kTStaged = 20, kTSignal = 30,
+                 // finer points: control wave (delta step, all-reduce, down's hand-off)
+                 kTDnLanded = 21, kTDnState = 22, kTDnDone = 23, kTArLanded = 31, kTArLocal = 32, kTGuLanded = 34,
+                 // compute waves (their own trace rows): GEMV consume, attention split
+                 kTConsume = 40, kTConsumed = 42, kTAtStaged = 60, kTAtRoped = 61, kTAtQk = 62, kTAtSoftmax = 63,
+                 kTAtPv = 64, kTAtDone = 65 };
 // Compiled in only with DF_TRACE defined (a separate build of the library): the stamps' code sits
 // between the phases of every token, in the instruction cache the decode depends on.
 DF_DEVICE void stamp(Ctx& c, int tag) {
@@ -954,6 +962,7 @@ DF_DEVICE float block_dot(const uint4& wv, uint32_t sd, const uint16_t* x, float
 // Blocks are taken two at a time (two independent MFMA chains per iteration).
 DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPersistModel& M, const Geo& q,
                             int steps, Lds& L) {
+  stamp(const_cast<Ctx&>(c), kTConsume);
   int lo, n;
   wave_range(g, c.wave, lo, n);
   // this wave's partial of every tile starts at zero (only this wave writes its column, and
@@ -994,6 +1003,7 @@ DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPer
     fill(st, steps, c);
   }
   if (n > 0 && gl != 0 && c.lane < 16) L.part[tr][c.lane][c.wave] = acc;
+  stamp(const_cast<Ctx&>(c), kTConsumed);
 }
 
 // Sum of the waves' partials for relative tile t (fixed wave order).
@@ -1328,6 +1338,7 @@ DF_DEVICE bool allreduce_residual(Ctx& c, Lds& L, int hidden) {
     __builtin_amdgcn_s_sleep(1);
   }
   if (!ok) return false;
+  stamp(c, kTArLanded);
   uint16_t* hx = c.w.hloc + (size_t)c.xcd * hidden;
   if (mine) {
     float y0 = 0.0f, y1 = 0.0f;
@@ -1346,6 +1357,7 @@ DF_DEVICE bool allreduce_residual(Ctx& c, Lds& L, int hidden) {
   // bytes, re-read by every workgroup of the XCD while the slices arrive)
   signal_local(c, c.epoch);
   if (!wait_local(c, c.epoch)) return false;
+  stamp(c, kTArLocal);
   // h into LDS with its sum of squares for the next RMSNorm (the same order in every
   // workgroup, so all agree)
   const auto rh = rsrc(hx);
@@ -1388,25 +1400,45 @@ DF_DEVICE int dn_channel(const Ctx& c, int i) {
   return 2 * kKeyDim + hv * kDk + vs * 16 + (i - 256);
 }
 
-// Control wave: the whole Gated DeltaNet step of this workgroup's unit (value head hv, value
-// columns 16 vs .. 16 vs + 15) in one wave, with no barrier: the 4-tap conv + SiLU over its
-// 272 channels (q, k of the key head, its 16 v), q/k L2 norms, the gates and the delta rule on
-// its 128 x 16 fp32 state slice, held in registers (lane l: columns 4 (l % 4) .. + 3 of rows
-// l / 4 + 16 j, j < 8). Publishes the 16 core outputs tagged with `epoch_out`, and stages the
-// XCD's z columns (out_proj's gated-norm gates) from the same hand-off poll. The arithmetic and
-// rounding points are the reference's (reference.py:407-461, 496-545); fp32 sums over the
-// state rows run in a fixed order of their own.
-DF_DEVICE bool dn_step(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_in, uint32_t epoch_out) {
-#pragma clang fp contract(off)
+// Control wave, at the start of a Gated DeltaNet layer's input projection: this workgroup's
+// 128 x 16 fp32 state slice into LDS (L.u.dn.S) by DMA, lane l's 16 bytes of row l / 4 + 16 j
+// into S[j][l]. Issued a whole GEMV phase before the delta step reads it, so its HBM round trip
+// is off the step's critical path; the hand-off poll the step begins with waits for every
+// earlier memory operation of the wave (in-order vmcnt), this DMA included.
+DF_DEVICE void dn_state_prefetch(const Ctx& c, LayerPtr Lp, Lds& L) {
+  auto& D = L.u.dn;
+  const int hv = 4 * c.xcd + (c.r >> 3), vs = c.r & 7;
+  const int row0 = c.lane >> 2, col4 = (c.lane & 3) * 4;
+  const float* sbase = LF(Lp, state) + ((size_t)hv * kDk + row0) * kDk + vs * 16 + col4;
+#pragma unroll
+  for (int i = 0; i < kDk / 16; ++i) dma16(sbase + (size_t)16 * i * kDk, lds_addr(&D.S[i][0]));
+}
+
+// The Gated DeltaNet step of this workgroup's unit (value head hv = 4 x + r / 8, value columns
+// 16 (r % 8) .. + 15), in three parts around two barriers, so that the eight compute waves (idle
+// at out_proj's first barrier otherwise) carry the arithmetic:
+//   dn_stage    control wave: the in_proj hand-off (q, k of the key head, the unit's 16 v, a/b,
+//               the XCD's z) and the unit's conv taps and history into LDS;     | barrier
+//   dn_conv     compute waves: the 4-tap conv + SiLU of the 272 channels, 34 per wave;
+//                                                                                | barrier
+//   dn_math     compute waves: q/k L2 norms and the gates (each wave, identically), then wave w
+//               runs the delta rule on value columns 2 w, 2 w + 1 over all 128 state rows (two
+//               rows per lane), so each column's recall and output are one wave's sums; the
+//               updated slice goes back to the LDS copy, the outputs to LDS;   | barrier
+//   dn_publish  control wave: the 16 outputs (tagged with their epoch), the new state slice and
+//               this position's conv history slots, to memory.
+// The arithmetic and rounding points are the reference's (reference.py:407-461, 496-545); fp32
+// sums over the state rows run in a fixed order of their own.
+constexpr int kDnBars = 3;
+constexpr int kDnConvPerWave = (kDnCh + kCompute - 1) / kCompute;  // 34
+static_assert(kDnConvPerWave <= 64, "one channel per lane");
+
+DF_DEVICE bool dn_stage(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_in) {
   auto& D = L.u.dn;
   const int hvl = c.r >> 3, vs = c.r & 7;
   const int hv = 4 * c.xcd + hvl;
-  constexpr int kRows = kDk / 16;            // state rows per lane
-  constexpr int kCh = (kDnCh + 63) / 64;     // conv channels per lane
+  constexpr int kCh = (kDnCh + 63) / 64;     // channels per lane
   // loads that do not depend on the hand-off go out first
-  float* state = LF(Lp, state);
-  const int row0 = c.lane >> 2, col4 = (c.lane & 3) * 4;
-  float* sbase = state + ((size_t)hv * kDk + row0) * kDk + vs * 16 + col4;
   uint2 tp[kCh];
   uint64_t hs[kCh];
 #pragma unroll
@@ -1426,120 +1458,112 @@ DF_DEVICE bool dn_step(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_in, uint32_t 
                       {kLinV + hvl * 128 + vs * 16, 16, D.qkv_in + 256},
                       {kLinA, 8, D.ab8},
                       {kLinZ, 512, L.zs}};
+  // the state slice is in LDS: its DMA (dn_state_prefetch) preceded this poll
   if (!gather_colpar<5, 7>(c, seg, epoch_in)) return false;
-  // the state slice goes to LDS by DMA once the hand-off has landed: issued before the poll,
-  // its HBM round trip would be one more thing the poll's first round waits for (a wave's
-  // memory operations complete in order); here it overlaps the conv, norms and gates
-#pragma unroll
-  for (int i = 0; i < kRows; ++i) dma16(sbase + (size_t)16 * i * kDk, lds_addr(&D.S[i][0]));
-  // conv + SiLU (fp32 sum in tap order, bf16, SiLU, bf16); history slots (pos+1)&3, (pos+2)&3,
-  // (pos+3)&3 hold positions pos-3, pos-2, pos-1 (slot pos&3 is written at the end).
-  float y[kCh];
+  stamp(c, kTDnLanded);
 #pragma unroll
   for (int i = 0; i < kCh; ++i) {
     const int ch = c.lane + 64 * i;
-    y[i] = 0.0f;
     if (ch < kDnCh) {
-      const uint2 wt = tp[i];
-      const uint2 hr = __builtin_bit_cast(uint2, hs[i]);
-      const float w0 = __uint_as_float(wt.x << 16), w1 = __uint_as_float(wt.x & 0xFFFF0000u);
-      const float w2 = __uint_as_float(wt.y << 16), w3 = __uint_as_float(wt.y & 0xFFFF0000u);
-      const uint16_t sl[4] = {static_cast<uint16_t>(hr.x), static_cast<uint16_t>(hr.x >> 16),
-                              static_cast<uint16_t>(hr.y), static_cast<uint16_t>(hr.y >> 16)};
-      const float h0 = bf2f(sl[(c.pos + 1) & 3]), h1 = bf2f(sl[(c.pos + 2) & 3]), h2 = bf2f(sl[(c.pos + 3) & 3]);
-      const float x = D.qkv_in[ch];
-      float acc = h0 * w0;
-      acc = acc + h1 * w1;
-      acc = acc + h2 * w2;
-      acc = acc + x * w3;
-      y[i] = round_bf(silu(round_bf(acc)));
+      D.cw[ch] = tp[i];
+      D.hist[ch] = __builtin_bit_cast(uint2, hs[i]);
     }
   }
-  static_assert(kCh == 5 && kDk == 128, "q = channels l, l + 64; k = 128 + l, 192 + l; v = 256 + l");
-  // L2 norms of q (then scaled by dk^-1/2) and k
-  {
-    const float rq = 1.0f / sqrtf(dsum(y[0] * y[0] + y[1] * y[1]) + 1e-6f);
-    const float rk = 1.0f / sqrtf(dsum(y[2] * y[2] + y[3] * y[3]) + 1e-6f);
-    const float scale = sqrtf(static_cast<float>(kDk));
-    D.q[c.lane] = (y[0] * rq) / scale;
-    D.q[c.lane + 64] = (y[1] * rq) / scale;
-    D.k[c.lane] = y[2] * rk;
-    D.k[c.lane + 64] = y[3] * rk;
-    if (c.lane < 16) D.v[c.lane] = y[4];
+  if (c.lane == 0) {
+    D.gp[0] = alog;
+    D.gp[1] = dtb;
   }
+  return true;
+}
+
+// Compute waves: conv + SiLU (fp32 sum in tap order, bf16, SiLU, bf16) of channels
+// 34 w .. 34 w + 33. History slots (pos+1)&3, (pos+2)&3, (pos+3)&3 hold positions pos-3, pos-2,
+// pos-1 (slot pos&3 is written by dn_publish).
+DF_DEVICE void dn_conv(const Ctx& c, Lds& L) {
+#pragma clang fp contract(off)
+  auto& D = L.u.dn;
+  const int ch = c.wave * kDnConvPerWave + c.lane;
+  if (c.lane < kDnConvPerWave && ch < kDnCh) {
+    const uint2 wt = D.cw[ch];
+    const uint2 hr = D.hist[ch];
+    const float w0 = __uint_as_float(wt.x << 16), w1 = __uint_as_float(wt.x & 0xFFFF0000u);
+    const float w2 = __uint_as_float(wt.y << 16), w3 = __uint_as_float(wt.y & 0xFFFF0000u);
+    const uint16_t sl[4] = {static_cast<uint16_t>(hr.x), static_cast<uint16_t>(hr.x >> 16),
+                            static_cast<uint16_t>(hr.y), static_cast<uint16_t>(hr.y >> 16)};
+    const float h0 = bf2f(sl[(c.pos + 1) & 3]), h1 = bf2f(sl[(c.pos + 2) & 3]), h2 = bf2f(sl[(c.pos + 3) & 3]);
+    float acc = h0 * w0;
+    acc = acc + h1 * w1;
+    acc = acc + h2 * w2;
+    acc = acc + D.qkv_in[ch] * w3;
+    D.y[ch] = round_bf(silu(round_bf(acc)));
+  }
+}
+
+// Compute waves: the norms, the gates and the delta rule on value columns 2 w, 2 w + 1 of the
+// unit (rows lane and lane + 64 in each lane). The state slice in LDS is S[j][l] = row l / 4 +
+// 16 j, columns 4 (l % 4) .. + 3.
+DF_DEVICE void dn_math(const Ctx& c, Lds& L) {
+#pragma clang fp contract(off)
+  auto& D = L.u.dn;
+  const int hvl = c.r >> 3;
+  // L2 norms of q (then scaled by dk^-1/2) and k, in every wave alike
+  const float q0 = D.y[c.lane], q1 = D.y[c.lane + 64];
+  const float k0 = D.y[kDk + c.lane], k1 = D.y[kDk + c.lane + 64];
+  const float rq = 1.0f / sqrtf(dsum(q0 * q0 + q1 * q1) + 1e-6f);
+  const float rk = 1.0f / sqrtf(dsum(k0 * k0 + k1 * k1) + 1e-6f);
+  const float scale = sqrtf(static_cast<float>(kDk));
+  const float qn0 = (q0 * rq) / scale, qn1 = (q1 * rq) / scale;
+  const float kn0 = k0 * rk, kn1 = k1 * rk;
   // gates
   const float a = D.ab8[hvl], b = D.ab8[4 + hvl];
   const float beta = round_bf(sigmoid(b));
-  const float eg = expf(-expf(alog) * softplus(a + dtb));
-  // state decay, and the recall k^T S over the unit's rows
-  float kr[kRows], qr[kRows];
-#pragma unroll
-  for (int i = 0; i < kRows; ++i) {
-    kr[i] = D.k[row0 + 16 * i];
-    qr[i] = D.q[row0 + 16 * i];
+  const float eg = expf(-expf(D.gp[0]) * softplus(a + D.gp[1]));
+  // this wave's two columns of rows lane and lane + 64
+  const int c0 = 2 * c.wave;
+  float* s0 = reinterpret_cast<float*>(&D.S[c.lane / 16][(c.lane % 16) * 4 + c0 / 4]) + (c0 % 4);
+  float* s1 = reinterpret_cast<float*>(&D.S[(c.lane + 64) / 16][(c.lane % 16) * 4 + c0 / 4]) + (c0 % 4);
+  float2 r0 = *reinterpret_cast<const float2*>(s0), r1 = *reinterpret_cast<const float2*>(s1);
+  r0.x = r0.x * eg;
+  r0.y = r0.y * eg;
+  r1.x = r1.x * eg;
+  r1.y = r1.y * eg;
+  const float p0 = dsum(r0.x * kn0 + r1.x * kn1), p1 = dsum(r0.y * kn0 + r1.y * kn1);
+  const float d0 = (D.y[2 * kDk + c0] - p0) * beta;
+  const float d1 = (D.y[2 * kDk + c0 + 1] - p1) * beta;
+  r0.x = r0.x + kn0 * d0;
+  r0.y = r0.y + kn0 * d1;
+  r1.x = r1.x + kn1 * d0;
+  r1.y = r1.y + kn1 * d1;
+  const float o0 = dsum(r0.x * qn0 + r1.x * qn1), o1 = dsum(r0.y * qn0 + r1.y * qn1);
+  *reinterpret_cast<float2*>(s0) = r0;
+  *reinterpret_cast<float2*>(s1) = r1;
+  if (c.lane == 0) {
+    D.core[c0] = o0;
+    D.core[c0 + 1] = o1;
   }
-  float4 S[kRows];
-  wait_vm<0>();  // the state DMA (the only memory operation since the poll)
+}
+
+// Control wave, after the compute waves' delta rule: the 16 outputs tagged with `epoch_out`,
+// then the stores nobody waits for (a wave's memory operations leave in order): the new state
+// slice, and this position's conv history slot of the channels this unit owns (its v slice; the
+// key head's q/k for the (even value head, slice 0) unit).
+DF_DEVICE void dn_publish(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_out) {
+  auto& D = L.u.dn;
+  const int hvl = c.r >> 3, vs = c.r & 7;
+  const int hv = 4 * c.xcd + hvl;
+  if (c.lane < 16) c.w.core[(size_t)c.xcd * 512 + hvl * kDk + vs * 16 + c.lane] = tag_bf16(f2bf(D.core[c.lane]), epoch_out);
+  stamp(c, kTDnDone);
+  const int row0 = c.lane >> 2, col4 = (c.lane & 3) * 4;
+  float* sbase = LF(Lp, state) + ((size_t)hv * kDk + row0) * kDk + vs * 16 + col4;
 #pragma unroll
-  for (int i = 0; i < kRows; ++i) S[i] = D.S[i][c.lane];
-  float p[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < kRows; ++i) {
-    S[i].x = S[i].x * eg;
-    S[i].y = S[i].y * eg;
-    S[i].z = S[i].z * eg;
-    S[i].w = S[i].w * eg;
-    p[0] = p[0] + S[i].x * kr[i];
-    p[1] = p[1] + S[i].y * kr[i];
-    p[2] = p[2] + S[i].z * kr[i];
-    p[3] = p[3] + S[i].w * kr[i];
-  }
-  // column sums over the 64 lanes' rows: lanes l, l+4, l+8, l+12 of a 16-lane row (DPP),
-  // then the 4 rows through LDS (the wave's own LDS accesses complete in order)
-  auto col_sums = [&](float (&v)[4]) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = row_sum_mod4(v[j]);
-    if ((c.lane & 15) < 4) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) D.sred[c.lane >> 4][col4 + j] = v[j];
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = ((D.sred[0][col4 + j] + D.sred[1][col4 + j]) + D.sred[2][col4 + j]) + D.sred[3][col4 + j];
-  };
-  col_sums(p);
-  const float4 vv = *reinterpret_cast<const float4*>(&D.v[col4]);
-  const float delta[4] = {(vv.x - p[0]) * beta, (vv.y - p[1]) * beta, (vv.z - p[2]) * beta, (vv.w - p[3]) * beta};
-  // rank-1 update, the new state out, and o = S^T q
-  float o[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < kRows; ++i) {
-    S[i].x = S[i].x + kr[i] * delta[0];
-    S[i].y = S[i].y + kr[i] * delta[1];
-    S[i].z = S[i].z + kr[i] * delta[2];
-    S[i].w = S[i].w + kr[i] * delta[3];
-    o[0] = o[0] + S[i].x * qr[i];
-    o[1] = o[1] + S[i].y * qr[i];
-    o[2] = o[2] + S[i].z * qr[i];
-    o[3] = o[3] + S[i].w * qr[i];
-  }
-  col_sums(o);
-  if (c.lane < 4) {
-    uint32_t* cp = c.w.core + (size_t)c.xcd * 512 + hvl * kDk + vs * 16 + col4;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) cp[j] = tag_bf16(f2bf(o[j]), epoch_out);
-  }
-  // the stores nobody waits for go out after the core (a wave's memory operations leave in
-  // order): the new state slice, and this position's conv history slot of the channels this
-  // unit owns (its v slice; the key head's q/k for the (even value head, slice 0) unit)
-#pragma unroll
-  for (int i = 0; i < kRows; ++i) *reinterpret_cast<float4*>(sbase + (size_t)16 * i * kDk) = S[i];
+  for (int i = 0; i < kDk / 16; ++i) *reinterpret_cast<float4*>(sbase + (size_t)16 * i * kDk) = D.S[i][c.lane];
+  constexpr int kCh = (kDnCh + 63) / 64;
 #pragma unroll
   for (int i = 0; i < kCh; ++i) {
     const int ch = c.lane + 64 * i;
     const bool owner = ch >= 2 * kDk || ((hvl & 1) == 0 && vs == 0);
     if (ch < kDnCh && owner) LF(Lp, conv_ring)[(size_t)dn_channel(c, ch) * 4 + (c.pos & 3)] = f2bf(D.qkv_in[ch]);
   }
-  return true;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1576,6 +1600,11 @@ DF_DEVICE void norm_rope4_lds(float x[4], const uint16_t* nw, float eps, const u
 
 struct AtPre {
   uint4 kb[8];   // K rows: this lane's key (t0 + 16 wave + col), dims d*32 + slot*8 ..+7
+};
+// A tile's K and V rows, loaded together (the per-XCD key split).
+struct AtPreKV {
+  uint4 kb[8];   // as AtPre
+  uint2 vb[16];  // V rows: keys t0 + 16 wave + j, dims 4 lane ..+3
 };
 
 DF_DEVICE void at_keys(const Ctx& c, int& j0, int& j1) {
@@ -1614,16 +1643,37 @@ DF_DEVICE void at_issue_k(const Ctx& c, LayerPtr Lp, int t0, int j1, AtPre& P) {
   }
 }
 
-// Compute waves (kTileBars barriers): one 128-key tile: QK (MFMA), then the V rows are loaded
-// while the online softmax runs (waves 0 / 1 for heads 0 / 1), then PV.
+// Compute waves: the K and V rows of one 128-key tile (not the new position's, which the tile
+// takes from LDS), issued together so the tile waits one memory round trip instead of two.
+DF_DEVICE void at_issue_kv(const Ctx& c, LayerPtr Lp, int t0, int j1, AtPreKV& P) {
+  const int col = c.lane & 15, slot = c.lane >> 4;
+  const size_t base = (size_t)(c.xcd >> 1) * c.max_len;
+  const int key = t0 + c.wave * 16 + col;
+  // defined on every path: a conditionally-set register array is a value the compiler carries
+  // around the whole layer loop (spilled across every other phase)
+#pragma unroll
+  for (int d = 0; d < 8; ++d) P.kb[d] = make_uint4(0u, 0u, 0u, 0u);
+  if (key < j1 && key != c.pos) {
+    GlobalBf16 kp = (GlobalBf16)LF(Lp, k_cache) + (base + key) * kHd + slot * 8;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) P.kb[d] = gload16(kp + d * 32);
+  }
+  GlobalBf16 vc = (GlobalBf16)LF(Lp, v_cache);
+#pragma unroll
+  for (int jj = 0; jj < 16; ++jj) {
+    const int kk = t0 + c.wave * 16 + jj;
+    P.vb[jj] = make_uint2(0u, 0u);
+    if (kk < j1 && kk != c.pos) P.vb[jj] = gload8(vc + (base + kk) * kHd + c.lane * 4);
+  }
+}
+
+// Compute waves (kTileBars barriers): one 128-key tile whose K and V rows are in flight in P:
+// QK (MFMA), the online softmax (waves 0 / 1 for heads 0 / 1), then PV.
 constexpr int kTileBars = 3;
-DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, float acc[2][4], Lds& L) {
+DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPreKV& P, float acc[2][4], Lds& L) {
   auto& A = L.u.at;
   const int col = c.lane & 15, slot = c.lane >> 4;
   const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
-  // the tile's K loads are the only vector loads in flight (the weight stream is held):
-  // waiting for all of them here also tells the compiler that none is pending afterwards
-  wait_vm<0>();
   {
     const int key = t0 + c.wave * 16 + col;
     const bool live = key < j1;
@@ -1644,18 +1694,7 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, floa
       A.sc[1][c.wave * 16 + col] = live ? d4[1] * scale : -INFINITY;
     }
   }
-  // V rows: keys t0 + 16 wave + j, dims 4 lane ..+3
-  uint2 vb[16];
-  {
-    const size_t base = (size_t)(c.xcd >> 1) * c.max_len;
-    GlobalBf16 vc = (GlobalBf16)LF(Lp, v_cache);
-#pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      const int kk = t0 + c.wave * 16 + jj;
-      vb[jj] = make_uint2(0u, 0u);
-      if (kk < j1 && kk != c.pos) vb[jj] = gload8(vc + (base + kk) * kHd + c.lane * 4);
-    }
-  }
+  stamp(c, kTAtQk);
   sync(c);
   if (c.wave < 2) {
     const int h = c.wave;
@@ -1679,7 +1718,7 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, floa
     }
   }
   sync(c);
-  wait_vm<0>();  // the V rows (nothing else is in flight)
+  stamp(c, kTAtSoftmax);
   {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -1693,7 +1732,7 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, floa
     for (int jj = 0; jj < 16; ++jj) {
       const int kk = t0 + c.wave * 16 + jj;
       if (kk < j1) {
-        const uint2 raw = kk == c.pos ? vn : vb[jj];
+        const uint2 raw = kk == c.pos ? vn : P.vb[jj];
         const float v0 = __uint_as_float(raw.x << 16), v1 = __uint_as_float(raw.x & 0xFFFF0000u);
         const float v2 = __uint_as_float(raw.y << 16), v3 = __uint_as_float(raw.y & 0xFFFF0000u);
 #pragma unroll
@@ -1707,6 +1746,7 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, floa
       }
     }
   }
+  stamp(c, kTAtPv);
   sync(c);
 }
 
@@ -1843,7 +1883,9 @@ DF_DEVICE void at_tile4(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, flo
 //   in_proj    W: RMSNorm -> g_x, group sums (h, its sum of squares and| kNormBars
 //                 the norm weight are in LDS since the last barrier)
 //              W: consume blocks                                       | 1, then C: epilogue (tagged)
-//   delta      C only: hand-off, conv, gates, delta rule, z; publishes the core (tagged)
+//   delta      C: hand-off, conv inputs                                 | 1
+//              W: conv + SiLU                                          | 1
+//              W: norms, gates, delta rule                             | 1, then C: core (tagged), state
 //   out_proj   C: hand-off, core                                       | 1
 //              W: GatedRMSNorm -> g_x, group sums                      | 1
 //              W: consume                                              | 1
@@ -1889,6 +1931,13 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
   for (int step = 0; step < steps; ++step) {
     c.pos = pos0 + step;
     c.nb = 0;
+#ifdef DF_TRACE
+    // each compute wave of workgroup (0, 0) stamps into its own row after the control wave's
+    const bool traced = M.trace && step == M.trace_step && c.xcd == 0 && c.r == 0 && M.trace_capacity >= 4096;
+    c.tr = traced ? M.trace + 2048 + c.wave * 240 : nullptr;
+    c.tn = 0;
+    c.tcap = 240;
+#endif
     fence(c);
     sync(c);  // embed
     if (!L.ok) return stop();
@@ -1903,7 +1952,15 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         sync(c);
       }
       if (kind == 0) {
-        // the control wave runs the delta step meanwhile
+        {  // the Gated DeltaNet step's arithmetic (dn_conv, dn_math); the control wave stages it
+          sync(c);  // inputs in LDS
+          if (!L.ok) return stop();
+          dn_conv(c, L);
+          sync(c);
+          dn_math(c, L);
+          sync(c);
+          static_assert(kDnBars == 3, "the control wave passes the same barriers");
+        }
         {  // gated norm + out_proj
           fence(c);
           const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
@@ -2035,6 +2092,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           auto& A = L.u.at;
           sync(c);  // q/k/v staged
           if (!L.ok) return stop();
+          stamp(c, kTAtStaged);
           if (c.wave < 3) {
             float x[4];
 #pragma unroll
@@ -2050,6 +2108,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
             for (int i = 0; i < 4; ++i) A.vnew[c.lane * 4 + i] = f2bf(A.vraw[c.lane * 4 + i]);
           }
           sync(c);
+          stamp(c, kTAtRoped);
           // the even XCD of the pair writes the new key/value (write-through: the odd XCD
           // reads this row in later steps)
           if ((c.xcd & 1) == 0 && c.pos >= j0 && c.pos < j1 && c.tid < kHd / 2) {
@@ -2061,11 +2120,11 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           }
           float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
           for (int t0 = j0; t0 < j1; t0 += kTileKeys) {
-            // K rows are loaded here, in straight-line code with their use (a prefetch across
-            // the staging barrier leaves the compiler unsure they completed, and it then makes
-            // the weight-stream loops wait for them)
-            AtPre P;
-            at_issue_k(c, Lp, t0, j1, P);
+            // K and V rows are loaded here, in straight-line code with their use (loads held
+            // across the staging code raise the register pressure of the whole kernel, which then
+            // spills around the GEMV phases)
+            AtPreKV P;
+            at_issue_kv(c, Lp, t0, j1, P);
             at_tile(c, Lp, t0, j1, P, acc, L);
           }
           // the split's KV loads are consumed (wait unconditionally: the compiler cannot pair
@@ -2086,6 +2145,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
             A.red[0][hh][d] = sum;
           }
           sync(c);
+          stamp(c, kTAtDone);
           // the weight stream resumes with o_proj while the control wave merges the splits: two
           // blocks per wave at a time, spaced out, so the refill (64 KB per CU) does not hold up
           // the control wave's hand-off loads, which share the CU's memory pipeline
@@ -2288,6 +2348,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         for (int i = 0; i < kNormBars; ++i) sync(c);
         // the next phase's small parameters, while the compute waves consume
         if (kind == 0) {
+          dn_state_prefetch(c, Lp, L);
           dma_row128(LF(Lp, gnorm_w), L.gnw, c.lane);
         } else {
           uint16_t* qn_w = PAIR ? L.u.at4.qn_w : L.u.at.qn_w;
@@ -2308,8 +2369,10 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         // ================= conv + gated delta step ===================================
         fence(c, kTDelta);
         c.epoch += 1;
-        // the compute waves wait at out_proj's first barrier meanwhile
-        if (!dn_step(c, Lp, L, c.epoch - 1, c.epoch)) return fail(1);
+        // the compute waves run the conv and the delta rule between these barriers
+        if (!dn_stage(c, Lp, L, c.epoch - 1)) return fail(1);
+        for (int i = 0; i < kDnBars; ++i) sync(c);
+        dn_publish(c, Lp, L, c.epoch);
         // ================= gated norm + out_proj (row-parallel) ======================
         {
           fence(c, kTOut);
@@ -2562,6 +2625,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         fence(c, kTDown);
         const Gemv g = gemv_of(Lp, q, 3, c.xcd, c.r);
         if (!wait_local(c, c.epoch)) return fail(1);
+        stamp(c, kTGuLanded);
         stage_gu<(kColparMax / 4 + 63) / 64>(c, q.inter_x, L.u.ac.gu);
         sync(c);
         stamp(c, kTStaged);
