@@ -277,12 +277,20 @@ def _(query, key, value, scale, splits):
     return torch.empty_like(query)
 
 
-def delta_rule_step_checks(model=None, *, device="cuda", dtype=None, seed: int = 0) -> tuple:
-    """The step against the oracle's restatement of the reference loop body
-    (reference.py:450-458) at Qwen3.5's DeltaNet head shape, batch 1 and 8: state within 1e-4
-    (the north star's bar for the fp32 state), output within atol 2e-2 / rtol 1e-2."""
-    from oracle.model import delta_rule_step as oracle_step
+def _delta_rule_definition(state: Tensor, q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor):
+    """The op's definition in fp32, as matrix products per head: decay the state by exp(g),
+    recall k^T S, write beta * (v - recall) along k, read q^T S (reference.py:450-458)."""
+    s = state.float() * torch.exp(g.float())[..., None, None]
+    kf, qf = k.float().unsqueeze(-2), q.float().unsqueeze(-2)  # (B, H, 1, Dk)
+    recall = (kf @ s).squeeze(-2)
+    s = s + kf.transpose(-1, -2) @ ((v.float() - recall) * beta.float().unsqueeze(-1)).unsqueeze(-2)
+    return (qf @ s).squeeze(-2), s
 
+
+def delta_rule_step_checks(model=None, *, device="cuda", dtype=None, seed: int = 0) -> tuple:
+    """The step against its fp32 definition (reference.py:450-458) at Qwen3.5's DeltaNet head
+    shape, batch 1 and 8: state within 1e-4 (the north star's bar for the fp32 state), output
+    within atol 2e-2 / rtol 1e-2."""
     from ..harness.correctness import check_kernel
 
     gen = torch.Generator().manual_seed(seed)
@@ -294,7 +302,7 @@ def delta_rule_step_checks(model=None, *, device="cuda", dtype=None, seed: int =
         v = torch.randn((batch, 32, 128), generator=gen)
         g = -torch.nn.functional.softplus(torch.randn((batch, 32), generator=gen))
         beta = torch.sigmoid(torch.randn((batch, 32), generator=gen))
-        want_out, want_state = oracle_step(state, q, k, v, g, beta)
+        want_out, want_state = _delta_rule_definition(state, q, k, v, g, beta)
         got_out, got_state = delta_rule_step(*(t.to(device) for t in (state, q, k, v, g, beta)))
         checks.append(check_kernel(f"hip_delta_rule_step state B={batch}", lambda: want_state, lambda: got_state.cpu(),
                                    replaces="gated_delta_rule", atol=1e-4, rtol=0.0))
@@ -303,12 +311,20 @@ def delta_rule_step_checks(model=None, *, device="cuda", dtype=None, seed: int =
     return tuple(checks)
 
 
+def _attention_definition(query: Tensor, key: Tensor, value: Tensor, scale: float) -> Tensor:
+    """Single-token GQA attention in fp32: query head h reads KV head h // (Hq / Hkv);
+    softmax over every key, rounded to the query's dtype at the end."""
+    batch, hq, dim = query.shape
+    hkv = key.shape[1]
+    q = query.float().reshape(batch, hkv, hq // hkv, dim)
+    probs = torch.softmax((q @ key.float().transpose(-1, -2)) * scale, dim=-1)
+    return (probs @ value.float()).reshape(batch, hq, dim).to(query.dtype)
+
+
 def split_kv_decode_attention_checks(model=None, *, device="cuda", dtype=None, seed: int = 0) -> tuple:
     """The reference's own cases for the op (flash_decode_splitkv.py:365-372: batch 1 and 32
     at 2048 keys, fewer keys than splits, a key count no tile divides) at Qwen3.5's attention
-    head shape, against the oracle's expression of the reference layer (gqa_decode.py:322-335)."""
-    from oracle.ops import decode_attention
-
+    head shape, against the attention's fp32 definition (gqa_decode.py:322-335)."""
     from ..harness.correctness import check_kernel
 
     gen = torch.Generator().manual_seed(seed)
@@ -320,7 +336,7 @@ def split_kv_decode_attention_checks(model=None, *, device="cuda", dtype=None, s
         q = torch.randn((batch, 16, 256), generator=gen).to(BF16)
         k = torch.randn((batch, 4, key_len, 256), generator=gen).to(BF16)
         v = torch.randn((batch, 4, key_len, 256), generator=gen).to(BF16)
-        want = decode_attention(q, k, v, scale)
+        want = _attention_definition(q, k, v, scale)
         got = split_kv_decode_attention(q.to(device), k.to(device), v.to(device), scale, 8).cpu()
         checks.append(check_kernel(f"hip_split_kv_decode_attention {label}", lambda: want, lambda: got,
                                    replaces="gqa_attention", atol=2e-2, rtol=1e-2))

@@ -348,6 +348,42 @@ def test_standalone_ops_are_registered_candidates_with_checks():
         assert name in INSTALLERS and name in CHECK_BUILDERS
 
 
+def test_check_builders_definitions_agree_with_the_oracle():
+    """The package's check builders carry their own fp32 definitions of the two standalone
+    ops (the package never imports the oracle); those definitions agree with the oracle's
+    restatement of the reference on the builders' shapes."""
+    from oracle.model import delta_rule_step as oracle_step
+    from oracle.ops import decode_attention
+
+    gen = torch.Generator().manual_seed(5)
+    state = torch.randn((2, 4, 128, 128), generator=gen) * 0.1
+    q = torch.nn.functional.normalize(torch.randn((2, 4, 128), generator=gen), dim=-1) / 128 ** 0.5
+    k = torch.nn.functional.normalize(torch.randn((2, 4, 128), generator=gen), dim=-1)
+    v = torch.randn((2, 4, 128), generator=gen)
+    g = -torch.nn.functional.softplus(torch.randn((2, 4), generator=gen))
+    beta = torch.sigmoid(torch.randn((2, 4), generator=gen))
+    got_out, got_state = hip_ops._delta_rule_definition(state, q, k, v, g, beta)
+    want_out, want_state = oracle_step(state, q, k, v, g, beta)
+    torch.testing.assert_close(got_state, want_state, atol=1e-5, rtol=0)
+    torch.testing.assert_close(got_out, want_out, atol=1e-5, rtol=0)
+    # a wrong sign on the recall term moves the state far past the bar
+    bad = hip_ops._delta_rule_definition(state, q, -k, v, g, beta)[1]
+    assert (bad - want_state).abs().max() > 1e-2
+
+    qa = torch.randn((2, 16, 256), generator=gen).to(BF16)
+    ka = torch.randn((2, 4, 33, 256), generator=gen).to(BF16)
+    va = torch.randn((2, 4, 33, 256), generator=gen).to(BF16)
+    torch.testing.assert_close(hip_ops._attention_definition(qa, ka, va, 0.0625),
+                               decode_attention(qa, ka, va, 0.0625), atol=2e-2, rtol=1e-2)
+
+
+def test_product_package_never_imports_the_oracle():
+    pkg = ROOT / "deltaforge_amd"
+    offenders = [str(p.relative_to(ROOT)) for p in pkg.rglob("*.py")
+                 if re.search(r"^\s*(from|import)\s+oracle\b", p.read_text(), flags=re.M)]
+    assert not offenders, offenders
+
+
 def test_registry_index_detects_an_entry_changed_behind_its_back():
     import dataclasses
 
