@@ -186,15 +186,30 @@ def attention_prefill(q: Tensor, k_cache: Tensor, v_cache: Tensor, gate: Tensor,
     hkv, max_len, _ = k_cache.shape
     if d != 256 or hq != 4 * hkv or not q.is_contiguous():
         raise ValueError("q must be a contiguous [P, 4 Hkv, 256]")
+    if v_cache.shape != k_cache.shape or not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous [Hkv, max_len, 256] of one shape")
+    if pos0 < 0 or pos0 + tokens > max_len:
+        raise ValueError(f"positions {pos0} .. {pos0 + tokens - 1} do not fit a cache of {max_len}")
     op = "attention_prefill"
     for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("gate", gate)):
         ops._check_dtype(op, name, t, BF16)
+    # The kernel sees only pointers and row strides: every extent it reads or writes is
+    # checked here, so a short gate or output becomes an error, not an access out of bounds.
+    ld_gate = _row_view(gate, "gate")
+    gate_cols = (hq - 1) * gate_head_stride + d
+    if gate_head_stride < 0 or gate.shape[0] != tokens or gate.shape[1] < gate_cols:
+        raise ValueError(f"gate must be [{tokens}, >= {gate_cols}] for {hq} heads at column stride "
+                         f"{gate_head_stride}, got {tuple(gate.shape)}")
     if out is None:
         out = torch.empty((tokens, hq * d), dtype=BF16, device=q.device)
+    ops._check_dtype(op, "out", out, BF16)
+    ld_out = _row_view(out, "out")
+    if out.shape[0] != tokens or out.shape[1] < hq * d:
+        raise ValueError(f"out must be [{tokens}, >= {hq * d}], got {tuple(out.shape)}")
     ops.require_gpus(op, q, k_cache, v_cache, gate, out)
     args = N.AttnPrefillArgs(q=q.data_ptr(), k_cache=k_cache.data_ptr(), v_cache=v_cache.data_ptr(),
-                             gate=gate.data_ptr(), out=out.data_ptr(), ld_gate=_row_view(gate, "gate"),
-                             gate_head_stride=gate_head_stride, ld_out=_row_view(out, "out"), tokens=tokens,
+                             gate=gate.data_ptr(), out=out.data_ptr(), ld_gate=ld_gate,
+                             gate_head_stride=gate_head_stride, ld_out=ld_out, tokens=tokens,
                              pos0=pos0, max_len=max_len, num_q_heads=hq, num_kv_heads=hkv, gate_kind=gate_kind,
                              scale=scale)
     N.check(N.lib().df_attention_prefill(C.byref(args), ops._stream(q)), op)
@@ -298,8 +313,16 @@ class Prefiller:
         if chunk < 64 or chunk % 64 or chunk > 65535:
             raise ValueError("chunk must be a multiple of 64 below 65536")
         plen = prompt.shape[1]
+        if plen < 1:
+            raise ValueError("prompt must hold at least one token")
         if plen + decoder.max_new_tokens > decoder.max_seq_len:
             raise ValueError("prompt + max_new_tokens exceeds the cache")
+        # The embedding kernels skip an id outside the table and leave its row unwritten, so
+        # the ids are checked here, once, before anything runs (an index error, as the
+        # reference's embedding lookup raises).
+        lo, hi = int(prompt.min()), int(prompt.max())
+        if lo < 0 or hi >= self.config.vocab_size:
+            raise ValueError(f"token ids must lie in [0, {self.config.vocab_size}), got {lo} .. {hi}")
         decoder.reset()
         ids = prompt[0].to(self.device, torch.int64).contiguous()
         decoder.prompt[:plen].copy_(ids)

@@ -432,3 +432,59 @@ def test_persistent_refuses_norm_weights_beyond_the_fp16_staging_range():
     w[7] = bound  # 1 + w just above the bound
     with pytest.raises(ValueError, match="post_attention_layernorm"):
         check_norm_range(cfg, {**params, "layers.2.post_attention_layernorm.weight": w})
+
+
+# -- prefill host checks --------------------------------------------------------------------
+
+
+def _attention_prefill_args(tokens=3, hkv=1, max_len=8):
+    q = torch.zeros((tokens, 4 * hkv, 256), dtype=BF16)
+    kc = torch.zeros((hkv, max_len, 256), dtype=BF16)
+    gate = torch.zeros((tokens, 2 * 256 * 4 * hkv), dtype=BF16)
+    return q, kc, kc.clone(), gate
+
+
+def test_attention_prefill_checks_gate_and_out_extents_before_the_device():
+    from deltaforge_amd.prefill import attention_prefill
+
+    q, kc, vc, gate = _attention_prefill_args()
+    # gate one column short of head 3's last element at stride 512
+    with pytest.raises(ValueError, match="gate must be"):
+        attention_prefill(q, kc, vc, gate[:, :3 * 512 + 255], gate_head_stride=512)
+    with pytest.raises(ValueError, match="gate must be"):
+        attention_prefill(q, kc, vc, gate[:2], gate_head_stride=512)
+    with pytest.raises(ValueError, match="gate must be"):
+        attention_prefill(q, kc, vc, gate, gate_head_stride=-1)
+    with pytest.raises(ValueError, match="contiguous rows"):
+        attention_prefill(q, kc, vc, gate[:, ::2], gate_head_stride=256)
+    with pytest.raises(ValueError, match="out must be"):
+        attention_prefill(q, kc, vc, gate, gate_head_stride=512, out=torch.empty((3, 1023), dtype=BF16))
+    with pytest.raises(ValueError, match="out must be"):
+        attention_prefill(q, kc, vc, gate, gate_head_stride=512, out=torch.empty((2, 1024), dtype=BF16))
+    with pytest.raises(ValueError, match="out must be"):
+        attention_prefill(q, kc, vc, gate, gate_head_stride=512, out=torch.empty((3, 1024), dtype=torch.float32))
+    with pytest.raises(ValueError, match="contiguous rows"):
+        attention_prefill(q, kc, vc, gate, gate_head_stride=512, out=torch.empty((1024, 3), dtype=BF16).t())
+    with pytest.raises(ValueError, match="do not fit"):
+        attention_prefill(q, kc, vc, gate, gate_head_stride=512, pos0=6)
+    # every extent in range: the next stop is the device check
+    with pytest.raises(RuntimeError):
+        attention_prefill(q, kc, vc, gate, gate_head_stride=512, out=torch.empty((3, 1024), dtype=BF16))
+
+
+def test_prefiller_fill_rejects_token_ids_outside_the_vocabulary():
+    from types import SimpleNamespace
+
+    from deltaforge_amd.prefill import Prefiller
+
+    pre = Prefiller.__new__(Prefiller)  # the checks run before any weight or device use
+    pre.config = mid_config()
+    pre.device = torch.device("cpu")
+    decoder = SimpleNamespace(max_new_tokens=4, max_seq_len=64,
+                              reset=lambda: pytest.fail("reset ran before the id check"))
+    vocab = pre.config.vocab_size
+    for bad in (torch.tensor([[1, vocab, 2]]), torch.tensor([[-1, 0]])):
+        with pytest.raises(ValueError, match="token ids"):
+            pre.fill(decoder, bad)
+    with pytest.raises(ValueError, match="at least one token"):
+        pre.fill(decoder, torch.zeros((1, 0), dtype=torch.int64))
