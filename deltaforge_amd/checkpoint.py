@@ -3,8 +3,16 @@
 The published Qwen3.5 checkpoint stores the text decoder under ``model.language_model.``,
 plus a vision tower (``model.visual.``) and a multi-token-prediction head (``mtp.``). Decode
 uses neither, so both are skipped by prefix and counted in the report. Every other name maps
-explicitly. A text-decoder tensor with no mapping is an error, never a silent skip. This is the
-reference's loader contract (weights.py:130-270), restated for this build's model format.
+explicitly. A text-decoder tensor with no mapping is an error, never a silent skip. That is the
+reference's loader contract (weights.py:130-270); the loader here is built differently:
+
+1. a catalogue of every tensor (name -> shard, dtype, shape) is read from the safetensors
+   headers alone, so the whole name map and shape proof are settled before any weight byte
+   is read;
+2. each entry is routed (skipped by prefix, mapped to a parameter, or refused), and the
+   mapped ones are checked against ``checkpoint_shapes``;
+3. only when the plan is whole (or ``strict=False``) are the tensors read, shard by shard,
+   each handed to the converter of its parameter kind.
 
 Model format (``synth.SynthModel``):
 - ``linears`` holds each projection as canonical K-major int4 (``CanonicalInt4``, bf16
@@ -30,8 +38,11 @@ from __future__ import annotations
 
 import json
 import re
+import struct
+from collections import defaultdict
 from dataclasses import dataclass, field
 from pathlib import Path
+from typing import NamedTuple
 
 import torch
 
@@ -79,19 +90,43 @@ class WeightMappingError(RuntimeError):
     """The checkpoint and the model do not line up (unknown, missing or misshapen tensors)."""
 
 
+# -- routing -----------------------------------------------------------------------------------
+
+
+class _Route(NamedTuple):
+    """Where one checkpoint tensor goes: ``kind`` is ``"vision"`` or ``"mtp"`` (skipped by
+    design), ``"param"`` (``target`` names the model parameter) or ``"foreign"`` (``why`` says
+    which rule refused it)."""
+
+    kind: str
+    target: str | None = None
+    why: str = ""
+
+
+def _route(name: str) -> _Route:
+    if name.startswith(VISION_PREFIX):
+        return _Route("vision")
+    if name.startswith(MTP_PREFIX):
+        return _Route("mtp")
+    top = _TOP_LEVEL.get(name)
+    if top is not None:
+        return _Route("param", top)
+    m = _LAYER_NAME.match(name)
+    if m is None:
+        return _Route("foreign", why="outside the text decoder, the vision tower and the MTP head")
+    layer, suffix = int(m.group(1)), m.group(2)
+    if suffix not in _LAYER_SUFFIXES:
+        return _Route("foreign", why=f"layer {layer} has no parameter {suffix!r}")
+    return _Route("param", f"layers.{layer}.{suffix}")
+
+
 def map_checkpoint_name(name: str) -> str | None:
     """Checkpoint tensor name -> model parameter name; ``None`` for the vision tower and the
     MTP head; ``WeightMappingError`` for any other name the decoder does not own."""
-    if name.startswith((VISION_PREFIX, MTP_PREFIX)):
-        return None
-    if name in _TOP_LEVEL:
-        return _TOP_LEVEL[name]
-    m = _LAYER_NAME.match(name)
-    if m is None:
-        raise WeightMappingError(f"unrecognised checkpoint tensor: {name!r}")
-    if m.group(2) not in _LAYER_SUFFIXES:
-        raise WeightMappingError(f"unrecognised tensor {name!r}: no mapping for layer suffix {m.group(2)!r}")
-    return f"layers.{int(m.group(1))}.{m.group(2)}"
+    r = _route(name)
+    if r.kind == "foreign":
+        raise WeightMappingError(f"checkpoint tensor {name!r} has no place in the decoder: {r.why}")
+    return r.target
 
 
 def checkpoint_shapes(config: ModelConfig) -> dict[str, tuple[int, ...]]:
@@ -123,6 +158,9 @@ def checkpoint_shapes(config: ModelConfig) -> dict[str, tuple[int, ...]]:
     if not c.tie_word_embeddings:
         shapes["lm_head.weight"] = (c.vocab_size, c.hidden_size)
     return shapes
+
+
+# -- int4 --------------------------------------------------------------------------------------
 
 
 def group_size_for(k: int) -> int:
@@ -160,6 +198,9 @@ def quantise_int4_k_major(weight: torch.Tensor, rows_per_chunk: int = 8192) -> C
     return CanonicalInt4(packed, scale)
 
 
+# -- report ------------------------------------------------------------------------------------
+
+
 @dataclass(frozen=True)
 class LoadReport:
     """Counts and names of what a load did. It is ``ok`` when nothing is missing, unmapped
@@ -174,31 +215,101 @@ class LoadReport:
 
     @property
     def ok(self) -> bool:
-        return not (self.missing or self.unmapped or self.mismatched)
+        return not any(self.problems().values())
 
-    def summary(self) -> str:
-        lines = [f"loaded {len(self.loaded)} tensors",
-                 f"skipped {len(self.skipped_vision)} vision-tower tensors (not on the decode path)",
-                 f"skipped {len(self.skipped_mtp)} MTP-head tensors (not on the decode path)"]
-        for label, names in (("missing from checkpoint", self.missing), ("unmapped in checkpoint", self.unmapped),
-                             ("shape mismatch", self.mismatched)):
-            if names:
-                more = f" (+{len(names) - 8} more)" if len(names) > 8 else ""
-                lines.append(f"{len(names)} {label}: {', '.join(names[:8])}{more}")
-        return "\n".join(lines)
+    def problems(self) -> dict[str, tuple[str, ...]]:
+        """Each way the checkpoint can fail to fit the model, with the names concerned."""
+        return {"missing (model parameters with no checkpoint tensor)": self.missing,
+                "unmapped (checkpoint tensors the decoder has no place for)": self.unmapped,
+                "shape mismatch": self.mismatched}
+
+    def summary(self, show: int = 6) -> str:
+        out = [f"{len(self.loaded)} decoder tensors loaded; skipped by design: {len(self.skipped_vision)} "
+               f"vision-tower and {len(self.skipped_mtp)} MTP-head tensors (decode reads neither)"]
+        for heading, names in self.problems().items():
+            if not names:
+                continue
+            out.append(f"{heading}: {len(names)}")
+            out.extend(f"    {n}" for n in names[:show])
+            if len(names) > show:
+                out.append(f"    ... and {len(names) - show} more")
+        return "\n".join(out)
 
 
-def _shards(path: Path) -> list[Path]:
+# -- catalogue ---------------------------------------------------------------------------------
+
+
+class _Entry(NamedTuple):
+    shard: Path
+    dtype: str
+    shape: tuple[int, ...]
+
+
+def _header(shard: Path) -> dict[str, _Entry]:
+    """Tensor name -> entry from a safetensors file's header alone: an 8-byte little-endian
+    length, then that many bytes of JSON (``{name: {dtype, shape, data_offsets}}`` plus an
+    optional ``__metadata__``). No weight data is read."""
+    with open(shard, "rb") as f:
+        head = f.read(8)
+        if len(head) != 8:
+            raise WeightMappingError(f"{shard} is too short to be a safetensors file")
+        (size,) = struct.unpack("<Q", head)
+        meta = json.loads(f.read(size))
+    return {name: _Entry(shard, m["dtype"], tuple(m["shape"])) for name, m in meta.items() if name != "__metadata__"}
+
+
+def _catalogue(path: Path) -> dict[str, _Entry]:
+    """Every tensor of a checkpoint: one file, a directory with a sharded index (the index
+    decides which shard holds each name), or a directory of ``*.safetensors`` files."""
     if path.is_file():
-        return [path]
+        return _header(path)
     index = path / "model.safetensors.index.json"
     if index.exists():
-        weight_map = json.loads(index.read_text())["weight_map"]
-        return [path / shard for shard in sorted(set(weight_map.values()))]
-    shards = sorted(path.glob("*.safetensors"))
-    if not shards:
-        raise FileNotFoundError(f"no .safetensors files under {path}")
-    return shards
+        owner: dict[str, str] = json.loads(index.read_text())["weight_map"]
+        headers = {f: _header(path / f) for f in sorted(set(owner.values()))}
+        absent = [n for n, f in owner.items() if n not in headers[f]]
+        if absent:
+            raise WeightMappingError(f"the index places {len(absent)} tensors in shards that lack them, "
+                                     f"e.g. {absent[0]!r} in {owner[absent[0]]}")
+        return {n: headers[f][n] for n, f in owner.items()}
+    files = sorted(path.glob("*.safetensors"))
+    if not files:
+        raise FileNotFoundError(f"{path} holds no safetensors checkpoint (no file, index or *.safetensors)")
+    found: dict[str, _Entry] = {}
+    for shard in files:
+        for name, entry in _header(shard).items():
+            if name in found:
+                raise WeightMappingError(f"{name!r} is stored twice, in {found[name].shard.name} and {shard.name}")
+            found[name] = entry
+    return found
+
+
+# -- conversion --------------------------------------------------------------------------------
+
+
+def _quantised(t: torch.Tensor, device) -> CanonicalInt4:
+    q = quantise_int4_k_major(t.to(device))
+    return CanonicalInt4(q.packed.cpu(), q.scale.cpu())
+
+
+def _converter(target: str, linear_names: set[str], tied: bool):
+    """The function that puts a checkpoint tensor for ``target`` into the model."""
+    if target in linear_names:
+        def put(model, t, device):
+            model.linears[target] = _quantised(t, device)
+    elif target == "embed_tokens.weight":
+        def put(model, t, device):
+            table = t.to(torch.bfloat16)
+            model.params[target] = table
+            if tied:  # the head is the embedding table, quantised like every linear
+                model.linears["lm_head"] = _quantised(table, device)
+    elif target == "lm_head.weight":
+        def put(model, t, device):
+            model.linears["lm_head"] = _quantised(t, device)
+    else:
+        def put(model, t, device):
+            model.params[target] = t.to(torch.bfloat16)
+    return put
 
 
 def load_checkpoint(path: str | Path, config: ModelConfig, *, strict: bool = True,
@@ -207,55 +318,42 @@ def load_checkpoint(path: str | Path, config: ModelConfig, *, strict: bool = Tru
 
     Returns the model in this build's format and the load report. Linears are quantised on
     ``device``; a GPU makes the 4B model's 248 matrices take seconds rather than minutes.
-    ``strict`` raises ``WeightMappingError`` unless the report is ``ok``.
+    ``strict`` raises ``WeightMappingError`` unless the report is ``ok``, before any weight
+    data is read.
     """
     from safetensors import safe_open
 
     expected = checkpoint_shapes(config)
-    linear_names = {name for name, _, _ in linear_shapes(config) if name != "lm_head"}
-    model = SynthModel(config)
-    loaded, vision, mtp, unmapped, mismatched = [], [], [], [], []
-    seen: set[str] = set()
-    for shard in _shards(Path(path)):
-        with safe_open(str(shard), framework="pt") as handle:
-            for name in handle.keys():  # noqa: SIM118 - safe_open has no __contains__
-                if name.startswith(VISION_PREFIX):
-                    vision.append(name)
-                    continue
-                if name.startswith(MTP_PREFIX):
-                    mtp.append(name)
-                    continue
-                try:
-                    target = map_checkpoint_name(name)
-                except WeightMappingError:
-                    unmapped.append(name)
-                    continue
-                if target not in expected:  # e.g. lm_head.weight of a tied model
-                    unmapped.append(name)
-                    continue
-                t = handle.get_tensor(name)
-                if tuple(t.shape) != expected[target]:
-                    mismatched.append(f"{name}: checkpoint {tuple(t.shape)} != model {expected[target]}")
-                    continue
-                if target in linear_names:
-                    q = quantise_int4_k_major(t.to(device))
-                    model.linears[target] = CanonicalInt4(q.packed.cpu(), q.scale.cpu())
-                elif target == "embed_tokens.weight":
-                    table = t.to(torch.bfloat16)
-                    model.params[target] = table
-                    if config.tie_word_embeddings:
-                        q = quantise_int4_k_major(table.to(device))
-                        model.linears["lm_head"] = CanonicalInt4(q.packed.cpu(), q.scale.cpu())
-                elif target == "lm_head.weight":
-                    q = quantise_int4_k_major(t.to(device))
-                    model.linears["lm_head"] = CanonicalInt4(q.packed.cpu(), q.scale.cpu())
-                else:
-                    model.params[target] = t.to(torch.bfloat16)
-                loaded.append(name)
-                seen.add(target)
-    report = LoadReport(loaded=tuple(sorted(loaded)), skipped_vision=tuple(sorted(vision)),
-                        skipped_mtp=tuple(sorted(mtp)), missing=tuple(sorted(set(expected) - seen)),
-                        unmapped=tuple(sorted(unmapped)), mismatched=tuple(sorted(mismatched)))
+    catalogue = _catalogue(Path(path))
+
+    skipped: dict[str, list[str]] = {"vision": [], "mtp": []}
+    unmapped: list[str] = []
+    mismatched: list[str] = []
+    plan: dict[str, str] = {}  # model parameter -> checkpoint name
+    for name in sorted(catalogue):
+        r = _route(name)
+        if r.kind in skipped:
+            skipped[r.kind].append(name)
+        elif r.kind == "foreign" or r.target not in expected:  # e.g. lm_head.weight of a tied model
+            unmapped.append(name)
+        elif catalogue[name].shape != expected[r.target]:
+            mismatched.append(f"{name}: {catalogue[name].shape} in the checkpoint, {expected[r.target]} in the model")
+        else:
+            plan[r.target] = name
+
+    report = LoadReport(loaded=tuple(sorted(plan.values())), skipped_vision=tuple(skipped["vision"]),
+                        skipped_mtp=tuple(skipped["mtp"]), missing=tuple(sorted(set(expected) - set(plan))),
+                        unmapped=tuple(unmapped), mismatched=tuple(mismatched))
     if strict and not report.ok:
-        raise WeightMappingError("checkpoint did not map cleanly onto the model:\n" + report.summary())
+        raise WeightMappingError(f"refusing a partial load of {path}:\n{report.summary()}")
+
+    linear_names = {name for name, _, _ in linear_shapes(config) if name != "lm_head"}
+    by_shard: dict[Path, list[tuple[str, str]]] = defaultdict(list)
+    for target, name in plan.items():
+        by_shard[catalogue[name].shard].append((target, name))
+    model = SynthModel(config)
+    for shard, items in by_shard.items():
+        with safe_open(str(shard), framework="pt") as handle:
+            for target, name in items:
+                _converter(target, linear_names, config.tie_word_embeddings)(model, handle.get_tensor(name), device)
     return model, report

@@ -214,3 +214,37 @@ def test_strict_load_fails_loudly(tmp_path):
     save_file(extra, str(tmp_path / "extra.safetensors"))
     _, report = load_checkpoint(tmp_path / "extra.safetensors", cfg, strict=False)
     assert set(report.unmapped) == {TEXT_PREFIX + "layers.0.mlp.extra_proj.weight", "lm_head.weight"}
+
+
+def test_the_plan_is_settled_from_headers_before_any_weight_is_read(tmp_path):
+    """A checkpoint whose data section is cut off still yields the full report: the catalogue
+    comes from the headers alone, and a strict load refuses before reading a weight."""
+    cfg = tiny_config()
+    tensors = _checkpoint(cfg, seed=3)
+    del tensors[TEXT_PREFIX + "norm.weight"]
+    full = tmp_path / "full.safetensors"
+    save_file(tensors, str(full))
+    raw = full.read_bytes()
+    header_len = int.from_bytes(raw[:8], "little")
+    cut = tmp_path / "cut.safetensors"
+    cut.write_bytes(raw[:8 + header_len + 16])  # header intact, weights gone
+    with pytest.raises(WeightMappingError, match="missing") as err:
+        load_checkpoint(cut, cfg)
+    assert "norm.weight" in str(err.value)
+
+
+def test_a_tensor_stored_twice_or_misplaced_by_the_index_is_refused(tmp_path):
+    cfg = tiny_config()
+    tensors = _checkpoint(cfg, seed=4)
+    names = sorted(tensors)
+    save_file({k: tensors[k] for k in names[:10]}, str(tmp_path / "a.safetensors"))
+    save_file({k: tensors[k] for k in names[9:]}, str(tmp_path / "b.safetensors"))  # names[9] twice
+    with pytest.raises(WeightMappingError, match="stored twice"):
+        load_checkpoint(tmp_path, cfg)
+    (tmp_path / "b.safetensors").unlink()
+    save_file({k: tensors[k] for k in names[10:]}, str(tmp_path / "b.safetensors"))
+    index = {"weight_map": {k: ("b.safetensors" if i == 0 else "a.safetensors" if i < 10 else "b.safetensors")
+                            for i, k in enumerate(names)}}
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps(index))
+    with pytest.raises(WeightMappingError, match="lack them"):
+        load_checkpoint(tmp_path, cfg)
