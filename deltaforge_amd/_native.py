@@ -52,6 +52,16 @@ class DeltaRuleArgs(C.Structure):
     ]
 
 
+class DeltaInputsArgs(C.Structure):
+    _fields_ = [
+        ("mixed", _vp), ("a", _vp), ("b", _vp), ("A_log", _vp), ("dt_bias", _vp),
+        ("query", _vp), ("key", _vp), ("value", _vp), ("g", _vp), ("beta", _vp),
+        ("ld_mixed", _i), ("ld_ab", _i),
+        ("batch", _i), ("num_k_heads", _i), ("num_v_heads", _i), ("head_k_dim", _i), ("head_v_dim", _i),
+        ("eps", _f),
+    ]
+
+
 class AttnDecodeArgs(C.Structure):
     _fields_ = [
         ("q", _vp), ("k", _vp), ("v", _vp), ("q_norm_w", _vp), ("k_norm_w", _vp), ("inv_freq", _vp),
@@ -118,6 +128,7 @@ SIGNATURES = {
     "df_int4_dequant": (_i, [_vp, _vp, _i, _i, _vp, _vp]),
     "df_gated_delta_step": (_i, [C.POINTER(GatedDeltaArgs), _vp]),
     "df_delta_rule_step": (_i, [C.POINTER(DeltaRuleArgs), _vp]),
+    "df_delta_step_inputs": (_i, [C.POINTER(DeltaInputsArgs), _vp]),
     "df_split_kv_decode_attention": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _sz, _vp]),
     "df_attention_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "df_attention_decode_splits": (_i, [_i, _i, _i]),

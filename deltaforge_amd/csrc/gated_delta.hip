@@ -247,7 +247,58 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_rule_step_kernel(DfDeltaR
                    [&](int col, float o) { p.out[(size_t)bh * p.value_dim + vs * kVSlice + col] = o; });
 }
 
+// The inputs of delta_rule_step_kernel from one token of Gated DeltaNet, as the reference
+// prepares them around its standalone step (kernels/gated_delta_step.py:189-213, 245-256):
+// per workgroup (batch b, value head h; key head h / groups), wave 0 L2-normalises q and
+// scales it by Dk^-1/2, wave 1 L2-normalises k, both in fp32 from the bf16 conv output; v is
+// widened to fp32; beta = fp32(bf16(sigmoid(b))); g = -exp(A_log) softplus(a + dt_bias).
+__global__ __launch_bounds__(2 * 64) void delta_step_inputs_kernel(DfDeltaInputsArgs p) {
+#pragma clang fp contract(off)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.x % p.num_v_heads, b = blockIdx.x / p.num_v_heads;
+  const int kh = h / (p.num_v_heads / p.num_k_heads);
+  const int key_dim = p.num_k_heads * kDk;
+  const uint16_t* row = p.mixed + (size_t)b * p.ld_mixed;
+  const size_t bh = (size_t)b * p.num_v_heads + h;
+
+  const uint16_t* src = row + wave * key_dim + kh * kDk;  // wave 0: q, wave 1: k
+  const float x0 = bf2f(src[2 * lane]), x1 = bf2f(src[2 * lane + 1]);
+  const float r = 1.0f / sqrtf(wave_sum(x0 * x0 + x1 * x1) + p.eps);
+  float y0 = x0 * r, y1 = x1 * r;
+  float* dst = (wave == 0 ? p.query : p.key) + bh * kDk;
+  if (wave == 0) {
+    const float scale = sqrtf(static_cast<float>(kDk));
+    y0 = y0 / scale;
+    y1 = y1 / scale;
+  }
+  dst[2 * lane] = y0;
+  dst[2 * lane + 1] = y1;
+
+  const uint16_t* vsrc = row + 2 * key_dim + (size_t)h * p.head_v_dim;
+  for (int e = tid; e < p.head_v_dim; e += 2 * 64) p.value[bh * p.head_v_dim + e] = bf2f(vsrc[e]);
+  if (tid == 0) {
+    const float a = bf2f(p.a[(size_t)b * p.ld_ab + h]);
+    const float bb = bf2f(p.b[(size_t)b * p.ld_ab + h]);
+    p.beta[bh] = round_bf(sigmoid(bb));
+    p.g[bh] = -expf(bf2f(p.A_log[h])) * softplus(a + bf2f(p.dt_bias[h]));
+  }
+}
+
 }  // namespace df
+
+extern "C" int df_delta_step_inputs(const DfDeltaInputsArgs* args, hipStream_t stream) {
+  using namespace df;
+  if (!args) return DF_BAD_ARGUMENT;
+  const DfDeltaInputsArgs& a = *args;
+  if (a.batch < 1 || a.head_k_dim != kDk || a.head_v_dim < 1 || a.num_k_heads < 1 || a.num_v_heads < 1 ||
+      a.num_v_heads % a.num_k_heads || !a.mixed || !a.a || !a.b || !a.A_log || !a.dt_bias || !a.query ||
+      !a.key || !a.value || !a.g || !a.beta)
+    return DF_BAD_ARGUMENT;
+  if (a.ld_mixed < 2 * a.num_k_heads * kDk + a.num_v_heads * a.head_v_dim || a.ld_ab < a.num_v_heads)
+    return DF_BAD_ARGUMENT;
+  hipLaunchKernelGGL(delta_step_inputs_kernel, dim3(a.batch * a.num_v_heads), dim3(2 * 64), 0, stream, a);
+  DF_RETURN_LAUNCH_STATUS();
+}
 
 extern "C" int df_gated_delta_step(const DfGatedDeltaArgs* args, hipStream_t stream) {
   using namespace df;

@@ -32,7 +32,17 @@ from .synth import SynthModel, inv_freq
 
 BF16 = torch.bfloat16
 
-__all__ = ["DecodeEngine"]
+__all__ = ["DecodeEngine", "STANDALONE_SLOTS"]
+
+#: Slots whose champion may be a standalone op instead of the fused kernel, and the other
+#: slots the standalone composition calls at its sites (their champions' impls go along).
+STANDALONE_SLOTS = {
+    "gated_delta_rule": ("causal_conv",),
+    "gqa_attention": ("rms_norm", "qkv_projection_rope"),
+    "causal_conv": (),
+    "rms_norm": (),
+    "qkv_projection_rope": (),
+}
 
 
 @dataclass
@@ -62,10 +72,20 @@ class DecodeEngine:
     """Greedy decode of a ``SynthModel`` (or any canonical int4 checkpoint) on one GPU."""
 
     def __init__(self, model: SynthModel, *, batch: int = 1, max_seq_len: int = 4096 + 256 + 64,
-                 device: str | torch.device = "cuda", max_new_tokens: int = 256) -> None:
+                 device: str | torch.device = "cuda", max_new_tokens: int = 256,
+                 standalone: dict | None = None) -> None:
         c: ModelConfig = model.config
         if c.output_gate_type != SIGMOID_GATE and c.output_gate_type != "swish":
             raise ValueError(f"unknown gate {c.output_gate_type}")
+        self.standalone = dict(standalone or {})
+        unknown = set(self.standalone) - set(STANDALONE_SLOTS)
+        if unknown:
+            raise ValueError(f"no standalone composition for {sorted(unknown)}; known: {sorted(STANDALONE_SLOTS)}")
+        for slot, needs in STANDALONE_SLOTS.items():
+            if slot in self.standalone:
+                absent = [n for n in needs if n not in self.standalone]
+                if absent:
+                    raise ValueError(f"the standalone {slot} step also calls {absent}; pass their kernels too")
         self.config = c
         self.batch = batch
         self.max_seq_len = max_seq_len
@@ -109,6 +129,8 @@ class DecodeEngine:
                     "state": torch.zeros((batch, c.linear_num_value_heads, c.linear_key_head_dim,
                                           c.linear_value_head_dim), dtype=torch.float32, device=dev),
                 }
+                if "gated_delta_rule" in self.standalone:  # the conv op keeps a shifting 3-tap history
+                    extra["conv_hist"] = torch.zeros((batch, c.linear_conv_dim, 3), dtype=BF16, device=dev)
             self.layers.append(_Layer(kind, p[pre + "input_layernorm.weight"], p[pre + "post_attention_layernorm.weight"],
                                       proj, out, mlp_gu, mlp_down, extra))
         self.head = gemv(lin["lm_head"].packed, lin["lm_head"].scale)
@@ -140,6 +162,9 @@ class DecodeEngine:
         self.token_log = torch.zeros((batch, max_new_tokens), dtype=torch.int64, device=dev)
         self.position = torch.zeros(1, dtype=torch.int32, device=dev)
         self.step_index = torch.zeros(1, dtype=torch.int32, device=dev)
+        # A standalone attention op takes the cache up to the current key as a tensor, so its
+        # length is read on the host: such steps run eagerly and keep this mirror in step.
+        self.host_position = 0
         self.prompt: torch.Tensor | None = None
         self._graphs: dict[str, torch.cuda.CUDAGraph] = {}
 
@@ -148,8 +173,53 @@ class DecodeEngine:
     def _gemv(self, g: _Gemv, x, **kw):
         return ops.int4_gemv(x, g.weight, plan=g.plan, ws=g.ws, eps=self.config.rms_norm_eps, **kw)
 
+    def _standalone_delta(self, layer: _Layer, core: torch.Tensor) -> None:
+        """The Gated DeltaNet middle through the standalone ops at their call sites, composed
+        as the reference composes them when its ``delta_rule_step`` is installed
+        (kernels/gated_delta_step.py:231-300): the causal conv op over a 3-tap history, the
+        step's inputs (L2 norms, q scale, gates), the delta-rule op on the fp32 state, and
+        the output cast to bf16 for the gated norm."""
+        c, e = self.config, layer.extra
+        conv_c, vd, hv = c.linear_conv_dim, c.linear_value_dim, c.linear_num_value_heads
+        conv = self.standalone["causal_conv"](self.proj[:, :conv_c].unsqueeze(-1), e["conv_hist"], e["conv_w"])
+        q, k, v, g, beta = ops.delta_step_inputs(conv.squeeze(-1), self.proj[:, conv_c + vd:conv_c + vd + hv],
+                                                 self.proj[:, conv_c + vd + hv:conv_c + vd + 2 * hv], e["A_log"],
+                                                 e["dt_bias"], num_k_heads=c.linear_num_key_heads,
+                                                 head_v_dim=c.linear_value_head_dim)
+        out, state = self.standalone["gated_delta_rule"](e["state"], q, k, v, g, beta)
+        e["state"].copy_(state)
+        core.copy_(out)
+
+    def _standalone_attention(self, layer: _Layer) -> None:
+        """Gated attention through the standalone ops at their call sites, composed as the
+        reference composes them when its split-KV op is installed
+        (kernels/flash_decode_splitkv.py:289-334): q/k RMSNorm, partial RoPE, the key and
+        value written at the position, the split-KV op over the cache so far, the output gate."""
+        c, e = self.config, layer.extra
+        b, hq, hkv, d = self.batch, c.num_attention_heads, c.num_key_value_heads, c.head_dim
+        qd, kd, pos, eps = 2 * hq * d, hkv * d, self.host_position, c.rms_norm_eps
+        if pos >= self.max_seq_len:
+            raise ValueError(f"position {pos} is past the cache ({self.max_seq_len})")
+        q_gate = self.proj[:, :qd].view(b, hq, 2, d)
+        norm, rope = self.standalone["rms_norm"], self.standalone["qkv_projection_rope"]
+        query = norm(q_gate[:, :, 0].contiguous(), e["q_norm"], eps)
+        key = norm(self.proj[:, qd:qd + kd].reshape(b, hkv, d).contiguous(), e["k_norm"], eps)
+        angles = float(pos) * self.inv_freq
+        emb = torch.cat((angles, angles)).view(1, 1, -1).expand(b, 1, -1)
+        cos, sin = emb.cos().to(BF16), emb.sin().to(BF16)
+        query = rope(query.unsqueeze(2), cos, sin)[:, :, 0]
+        key = rope(key.unsqueeze(2), cos, sin)[:, :, 0]
+        e["k_cache"][:, :, pos] = key
+        e["v_cache"][:, :, pos] = self.proj[:, qd + kd:qd + 2 * kd].reshape(b, hkv, d)
+        attn = self.standalone["gqa_attention"](query.contiguous(), e["k_cache"][:, :, :pos + 1].contiguous(),
+                                                e["v_cache"][:, :, :pos + 1].contiguous(), d ** -0.5, self.splits)
+        gate = q_gate[:, :, 1].reshape(b, hq * d).float()
+        gate = (torch.sigmoid(gate) if c.output_gate_type == SIGMOID_GATE else torch.nn.functional.silu(gate)).to(BF16)
+        torch.mul(attn.reshape(b, hq * d), gate, out=self.core[:, :hq * d])
+
     def enqueue_step(self, *, from_prompt: bool = False, log_token: bool = True) -> None:
-        """Launch one decode step on the current stream (no host sync, no allocation)."""
+        """Launch one decode step on the current stream (no host sync, no allocation; with a
+        standalone slot the step allocates its op outputs and must run eagerly)."""
         c = self.config
         if self.embed_table is not None:
             ops.embed_bf16(self.tokens, self.embed_table, self.h, prompt=self.prompt if from_prompt else None,
@@ -163,7 +233,11 @@ class DecodeEngine:
             e = layer.extra
             self._gemv(layer.proj, self.h, prologue=N.PRO_RMSNORM, norm_w=layer.in_norm,
                        out=self.proj[:, :layer.proj.weight.N])
-            if layer.kind == FULL_ATTENTION:
+            if layer.kind == FULL_ATTENTION and "gqa_attention" in self.standalone:
+                self._standalone_attention(layer)
+                self._gemv(layer.out, self.core[:, :c.num_attention_heads * c.head_dim],
+                           epilogue=N.EPI_RESIDUAL, res=self.h, out=self.h)
+            elif layer.kind == FULL_ATTENTION:
                 ops.attention_decode(self.proj[:, :qd], self.proj[:, qd:qd + kd], self.proj[:, qd + kd:qd + 2 * kd],
                                      e["q_norm"], e["k_norm"], self.inv_freq, e["k_cache"], e["v_cache"],
                                      self.position, num_q_heads=c.num_attention_heads, splits=self.splits,
@@ -173,10 +247,13 @@ class DecodeEngine:
                            epilogue=N.EPI_RESIDUAL, res=self.h, out=self.h)
             else:
                 core = self.core[:, :vd].view(self.batch, hv, c.linear_value_head_dim)
-                ops.gated_delta_step(self.proj[:, :conv_c], self.proj[:, conv_c + vd:conv_c + vd + hv],
-                                     self.proj[:, conv_c + vd + hv:conv_c + vd + 2 * hv], e["A_log"], e["dt_bias"],
-                                     e["conv_w"], e["state"], num_k_heads=c.linear_num_key_heads,
-                                     conv_ring=e["conv_ring"], position=self.position, out=core)
+                if "gated_delta_rule" in self.standalone:
+                    self._standalone_delta(layer, core)
+                else:
+                    ops.gated_delta_step(self.proj[:, :conv_c], self.proj[:, conv_c + vd:conv_c + vd + hv],
+                                         self.proj[:, conv_c + vd + hv:conv_c + vd + 2 * hv], e["A_log"],
+                                         e["dt_bias"], e["conv_w"], e["state"], num_k_heads=c.linear_num_key_heads,
+                                         conv_ring=e["conv_ring"], position=self.position, out=core)
                 self._gemv(layer.out, self.core[:, :vd], prologue=N.PRO_GATED_RMSNORM,
                            x2=self.proj[:, conv_c:conv_c + vd], norm_w=e["gnorm"],
                            epilogue=N.EPI_RESIDUAL, res=self.h, out=self.h)
@@ -190,8 +267,16 @@ class DecodeEngine:
 
     # -- graphs ---------------------------------------------------------------------------
 
+    @property
+    def capturable(self) -> bool:
+        """Whether the step can be captured: not with a standalone slot, whose ops take the
+        cache length from the host and allocate their outputs."""
+        return not self.standalone
+
     def graph(self, kind: str) -> torch.cuda.CUDAGraph:
         """The captured step: ``"decode"`` (token from the last argmax) or ``"prefill"``."""
+        if not self.capturable:
+            raise RuntimeError(f"a step with standalone {sorted(self.standalone)} cannot be captured")
         if kind not in self._graphs:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
@@ -208,6 +293,7 @@ class DecodeEngine:
                     t.zero_()
         self.position.zero_()
         self.step_index.zero_()
+        self.host_position = 0
 
     def set_prompt(self, prompt: torch.Tensor) -> None:
         prompt = prompt.to(self.device, torch.int64).contiguous()
@@ -226,24 +312,48 @@ class DecodeEngine:
         self.set_prompt(prompt)
         if prompt.shape[1] + self.max_new_tokens > self.max_seq_len:
             raise ValueError("prompt + max_new_tokens exceeds the cache")
-        if graph:
+        if graph and self.capturable:
             g = self.graph("prefill")
             for _ in range(prompt.shape[1]):
                 g.replay()
+            self.host_position += prompt.shape[1]
         else:
             for _ in range(prompt.shape[1]):
                 self.enqueue_step(from_prompt=True, log_token=False)
+                self.host_position += 1
         self.step_index.zero_()
 
     def decode(self, steps: int, *, graph: bool = True) -> None:
         """Greedy steps from ``self.tokens``; tokens land in ``token_log[:, step]``."""
-        if graph:
+        if graph and self.capturable:
             g = self.graph("decode")
             for _ in range(steps):
                 g.replay()
+            self.host_position += steps
         else:
             for _ in range(steps):
                 self.enqueue_step()
+                self.host_position += 1
+
+    def row_caches(self, row: int) -> list[dict]:
+        """Row ``row``'s caches per layer, as the prefill kernels take them: ``conv_ring``
+        ``[C, 4]`` and ``state`` ``[Hv, 128, 128]``, or ``k_cache``/``v_cache``
+        ``[Hkv, max_len, 256]`` (views, so a prefill writes the engine's own caches)."""
+        keys = ("k_cache", "v_cache", "conv_ring", "state")
+        return [{k: layer.extra[k][row] for k in keys if k in layer.extra} for layer in self.layers]
+
+    def finish_fill(self, prompt_len: int) -> None:
+        """After an external prefill of ``prompt_len`` tokens: the position, and the 3-tap
+        histories a standalone conv step reads, taken from the rings (the last three inputs,
+        oldest first, sit in slots ``prompt_len + 1 .. + 3`` mod 4)."""
+        for layer in self.layers:
+            hist = layer.extra.get("conv_hist")
+            if hist is not None:
+                slots = [(prompt_len + 1 + j) % 4 for j in range(3)]
+                hist.copy_(layer.extra["conv_ring"][:, :, slots])
+        self.position.fill_(prompt_len)
+        self.step_index.zero_()
+        self.host_position = prompt_len
 
     def state_tensors(self) -> list[torch.Tensor]:
         out = []
@@ -258,6 +368,7 @@ class DecodeEngine:
         """Copy a snapshot back in place (addresses, and so the captured graphs, stay valid)."""
         for t, s in zip(self.state_tensors(), snap):
             t.copy_(s)
+        self.host_position = int(self.position.item())
 
     # -- accounting -------------------------------------------------------------------------
 

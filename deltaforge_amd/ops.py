@@ -357,6 +357,48 @@ def delta_rule_step(state: Tensor, query: Tensor, key: Tensor, value: Tensor, g:
     return out, state_out
 
 
+def delta_step_inputs(mixed: Tensor, a: Tensor, b: Tensor, A_log: Tensor, dt_bias: Tensor, *, num_k_heads: int,
+                      head_v_dim: int, eps: float = 1e-6) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """``delta_rule_step``'s ``(query, key, value, g, beta)`` from one token of Gated DeltaNet.
+
+    ``mixed [B, C]`` is the conv + SiLU output (q | k | v, bf16), ``a``/``b`` ``[B, Hv]`` the
+    gate projections (bf16 rows), ``A_log``/``dt_bias`` ``[Hv]`` bf16. The reference's
+    prologue around its standalone step (kernels/gated_delta_step.py:189-213, 245-256): q and k
+    L2-normed in fp32 and repeated from key heads to value heads, q scaled by ``Dk**-0.5``,
+    ``beta = bf16(sigmoid(b))``, ``g = -exp(A_log) softplus(a + dt_bias)``; all fp32."""
+    if mixed.dim() != 2 or a.dim() != 2 or b.dim() != 2:
+        raise ValueError("mixed, a and b must be 2-D [B, ...] rows")
+    batch = mixed.shape[0]
+    hv = A_log.numel()
+    if hv < 1 or hv % num_k_heads or dt_bias.numel() != hv:
+        raise ValueError(f"{hv} value heads do not split over {num_k_heads} key heads (dt_bias {dt_bias.numel()})")
+    channels = 2 * num_k_heads * 128 + hv * head_v_dim
+    if mixed.shape[1] != channels:
+        raise ValueError(f"mixed must be [B, {channels}] for 128-wide key heads, got {tuple(mixed.shape)}")
+    for name, t in (("a", a), ("b", b)):
+        if t.shape[0] != batch or t.shape[1] < hv:
+            raise ValueError(f"{name} must be [{batch}, >= {hv}], got {tuple(t.shape)}")
+    for name, t in (("mixed", mixed), ("a", a), ("b", b), ("A_log", A_log), ("dt_bias", dt_bias)):
+        _check_dtype("delta_step_inputs", name, t, BF16)
+    if a.stride(0) != b.stride(0) or a.stride(1) != 1 or b.stride(1) != 1 or mixed.stride(1) != 1:
+        raise ValueError("a and b must be rows of one stride, and every row contiguous")
+    require_gpus("delta_step_inputs", mixed, a, b, A_log, dt_bias)
+    f32 = dict(dtype=torch.float32, device=mixed.device)
+    query = torch.empty((batch, hv, 128), **f32)
+    key = torch.empty((batch, hv, 128), **f32)
+    value = torch.empty((batch, hv, head_v_dim), **f32)
+    g = torch.empty((batch, hv), **f32)
+    beta = torch.empty((batch, hv), **f32)
+    args = N.DeltaInputsArgs(
+        mixed=mixed.data_ptr(), a=a.data_ptr(), b=b.data_ptr(), A_log=A_log.contiguous().data_ptr(),
+        dt_bias=dt_bias.contiguous().data_ptr(), query=query.data_ptr(), key=key.data_ptr(), value=value.data_ptr(),
+        g=g.data_ptr(), beta=beta.data_ptr(), ld_mixed=mixed.stride(0), ld_ab=a.stride(0), batch=batch,
+        num_k_heads=num_k_heads, num_v_heads=hv, head_k_dim=128, head_v_dim=head_v_dim, eps=eps,
+    )
+    N.check(N.lib().df_delta_step_inputs(C.byref(args), _stream(mixed)), "delta_step_inputs")
+    return query, key, value, g, beta
+
+
 # ---------------------------------------------------------------------------------------
 # Attention decode
 # ---------------------------------------------------------------------------------------

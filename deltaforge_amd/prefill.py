@@ -14,10 +14,10 @@ the HIP kernels of ``csrc/prefill.hip``:
 
 Then RMSNorm, the tied head and the argmax of the last position.
 
-``Prefiller.fill(decoder, prompt)`` leaves a ``PersistentDecoder`` in the state its own
-token-by-token prefill would: the conv rings, recurrent states and KV caches of every layer,
-the position, the last logits and the first generated token. Summation order is the only
-difference. ``Prefiller`` keeps its own copy of the weights, in natural column order (the
+``Prefiller.fill(decoder, prompt)`` leaves a ``PersistentDecoder`` (``fill_engine`` a
+``DecodeEngine``, one sequence per row) in the state its own token-by-token prefill would:
+the conv rings, recurrent states and KV caches of every layer, the position, the last logits
+and the first generated token. Summation order is the only difference. ``Prefiller`` keeps its own copy of the weights, in natural column order (the
 persistent kernel's copy is permuted XCD-major).
 """
 
@@ -216,6 +216,27 @@ def attention_prefill(q: Tensor, k_cache: Tensor, v_cache: Tensor, gate: Tensor,
     return out
 
 
+def unsupported_geometry(c: ModelConfig) -> str | None:
+    """Why the prefill kernels cannot run model ``c``, or ``None`` when they can: 256-wide
+    attention heads, four query heads per KV head, 128-wide Gated DeltaNet heads with a 4-tap
+    conv, every projection's K a multiple of 256 and N of 16, a power-of-two rotary half."""
+    half = c.rotary_dim // 2
+    if c.head_dim != 256 or c.num_attention_heads != 4 * c.num_key_value_heads:
+        return "attention needs head_dim 256 and four query heads per KV head"
+    if c.linear_key_head_dim != 128 or c.linear_value_head_dim != 128 or c.linear_conv_kernel_dim != 4:
+        return "Gated DeltaNet needs 128-wide heads and a 4-tap conv"
+    if c.linear_num_value_heads % c.linear_num_key_heads:
+        return "value heads must be a multiple of key heads"
+    if half < 4 or half & (half - 1) or c.rotary_dim > c.head_dim:
+        return f"rotary dim {c.rotary_dim} is not twice a power of two of at least 4"
+    for k in (c.hidden_size, c.intermediate_size, c.linear_value_dim, c.num_attention_heads * c.head_dim):
+        if k % 256:
+            return f"a projection has K = {k}, not a multiple of 256"
+    if c.vocab_size % 16 or c.intermediate_size % 16:
+        return "a projection's N is not a multiple of 16"
+    return None
+
+
 class Prefiller:
     """The model's weights in natural column order, and the forward over a prompt."""
 
@@ -308,8 +329,32 @@ class Prefiller:
         the caches), which bounds the activations and the conv kernel's grid (at most 65 535
         rows). ``chunk`` is a multiple of the delta rule's 64-token chunk, so the chunks are the
         ones a single pass would form and the result is the same."""
-        if prompt.dim() != 2 or prompt.shape[0] != 1:
-            raise ValueError(f"prompt must be [1, P], got {tuple(prompt.shape)}")
+        plen = self._check_prompt(decoder, prompt, chunk, rows=1)
+        decoder.reset()
+        ids = prompt[0].to(self.device, torch.int64).contiguous()
+        decoder.prompt[:plen].copy_(ids)
+        decoder.prompt_len = plen
+        decoder.logits.copy_(self._run(ids, decoder.layer_state, chunk))
+        ops.argmax_tokens(decoder.logits, decoder.tokens)
+        decoder.position.fill_(plen)
+        decoder.step_index.zero_()
+
+    def fill_engine(self, engine, prompt: Tensor, *, chunk: int = 16384) -> None:
+        """Prefill a ``DecodeEngine`` with ``prompt`` ``[B, P]``, one sequence per engine row:
+        every layer's caches, the position, the last logits and the first generated token, as
+        the engine's teacher-forced ``prefill`` leaves them (summation order aside)."""
+        plen = self._check_prompt(engine, prompt, chunk, rows=engine.batch)
+        engine.reset()
+        engine.set_prompt(prompt)
+        for row in range(engine.batch):
+            ids = engine.prompt[row].contiguous()
+            engine.logits[row:row + 1].copy_(self._run(ids, engine.row_caches(row), chunk))
+        engine.finish_fill(plen)
+        ops.argmax_tokens(engine.logits, engine.tokens)
+
+    def _check_prompt(self, decoder, prompt: Tensor, chunk: int, *, rows: int) -> int:
+        if prompt.dim() != 2 or prompt.shape[0] != rows:
+            raise ValueError(f"prompt must be [{rows}, P], got {tuple(prompt.shape)}")
         if chunk < 64 or chunk % 64 or chunk > 65535:
             raise ValueError("chunk must be a multiple of 64 below 65536")
         plen = prompt.shape[1]
@@ -323,13 +368,10 @@ class Prefiller:
         lo, hi = int(prompt.min()), int(prompt.max())
         if lo < 0 or hi >= self.config.vocab_size:
             raise ValueError(f"token ids must lie in [0, {self.config.vocab_size}), got {lo} .. {hi}")
-        decoder.reset()
-        ids = prompt[0].to(self.device, torch.int64).contiguous()
-        decoder.prompt[:plen].copy_(ids)
-        decoder.prompt_len = plen
-        for s in range(0, plen, chunk):
-            logits = self.forward(ids[s:s + chunk], decoder.layer_state, pos0=s)
-        decoder.logits.copy_(logits)
-        ops.argmax_tokens(decoder.logits, decoder.tokens)
-        decoder.position.fill_(plen)
-        decoder.step_index.zero_()
+        return plen
+
+    def _run(self, ids: Tensor, caches: list[dict], chunk: int) -> Tensor:
+        """``ids`` through ``forward`` ``chunk`` tokens at a time; the last position's logits."""
+        for s in range(0, ids.numel(), chunk):
+            logits = self.forward(ids[s:s + chunk], caches, pos0=s)
+        return logits

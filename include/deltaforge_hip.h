@@ -126,6 +126,28 @@ typedef struct DfDeltaRuleArgs {
  * Replaces deltaforge::delta_rule_step (kernels/gated_delta_step.py:109-186). */
 int df_delta_rule_step(const DfDeltaRuleArgs* args, hipStream_t stream);
 
+typedef struct DfDeltaInputsArgs {
+  const uint16_t* mixed;     /* [B][ld_mixed] bf16 conv + SiLU output (q | k | v)       */
+  const uint16_t* a;         /* [B][ld_ab] bf16 in_proj_a output                        */
+  const uint16_t* b;         /* [B][ld_ab] bf16 in_proj_b output                        */
+  const uint16_t* A_log;     /* [Hv] bf16                                               */
+  const uint16_t* dt_bias;   /* [Hv] bf16                                               */
+  float* query;              /* [B][Hv][Dk] fp32 out: L2-normed, scaled by Dk^-1/2      */
+  float* key;                /* [B][Hv][Dk] fp32 out: L2-normed                         */
+  float* value;              /* [B][Hv][Dv] fp32 out                                    */
+  float* g;                  /* [B][Hv] fp32 out: -exp(A_log) softplus(a + dt_bias)     */
+  float* beta;               /* [B][Hv] fp32 out: bf16(sigmoid(b)) widened              */
+  int ld_mixed, ld_ab;
+  int batch, num_k_heads, num_v_heads, head_k_dim, head_v_dim;  /* Dk == 128          */
+  float eps;                 /* L2-norm epsilon (1e-6 in the reference)                 */
+} DfDeltaInputsArgs;
+
+/* df_delta_rule_step's inputs from one token of Gated DeltaNet: the q/k L2 norms (key heads
+ * repeated over their value heads), the q scale, v in fp32 and the two gates. Replaces the
+ * torch prologue the reference runs around deltaforge::delta_rule_step when that op is
+ * installed (kernels/gated_delta_step.py:189-213, 245-256). */
+int df_delta_step_inputs(const DfDeltaInputsArgs* args, hipStream_t stream);
+
 /* ---- GQA attention decode (split-KV) -------------------------------------------- */
 
 typedef struct DfAttnDecodeArgs {

@@ -488,3 +488,72 @@ def test_prefiller_fill_rejects_token_ids_outside_the_vocabulary():
             pre.fill(decoder, bad)
     with pytest.raises(ValueError, match="at least one token"):
         pre.fill(decoder, torch.zeros((1, 0), dtype=torch.int64))
+
+
+# -- slots: the decode step calls what the registry's champions say ---------------------------
+
+
+def _registry_with(*promoted: str) -> KernelRegistry:
+    reg = KernelRegistry()
+    for e in REGISTRY:
+        reg.register(e.name, impl=e.impl, replaces=e.replaces, status=e.status, notes=e.notes)
+    for name in promoted:
+        reg.promote(name)
+    return reg
+
+
+def test_shipped_champions_plan_the_fused_step():
+    from deltaforge_amd.model import STEP_SLOTS, installed_slots, step_plan
+    from deltaforge_amd.synth import synth_model
+
+    model = synth_model(mid_config(num_layers=4), seed=0)
+    apply_champions(model)
+    slots = installed_slots(model)
+    assert {op: e.name for op, e in slots.items() if op in STEP_SLOTS} == {op: n[0] for op, n in STEP_SLOTS.items()}
+    assert step_plan(model) == {}
+
+
+@pytest.mark.parametrize("standalone,composed", [
+    ("hip_delta_rule_step", {"gated_delta_rule": "hip_delta_rule_step", "causal_conv": "hip_causal_conv_step"}),
+    ("hip_split_kv_decode_attention", {"gqa_attention": "hip_split_kv_decode_attention", "rms_norm": "hip_rms_norm",
+                                       "qkv_projection_rope": "hip_partial_rope"}),
+])
+def test_promoting_a_standalone_op_composes_its_slot_from_installed_entries(standalone, composed):
+    from deltaforge_amd.model import PersistentDecodeLoop, step_plan
+    from deltaforge_amd.synth import synth_model
+
+    model = synth_model(mid_config(num_layers=4), seed=0)
+    applied = apply_champions(model, _registry_with(standalone))
+    assert standalone in applied
+    plan = step_plan(model)
+    assert {op: model.kernel_slots[op].name for op in plan} == composed
+    # the impls are the registry entries' own callables
+    for op, impl in plan.items():
+        assert impl is REGISTRY.get(composed[op]).impl
+    # the persistent kernel fuses every slot itself, so it refuses such a registry
+    with pytest.raises(InstallerMissing, match="standalone"):
+        PersistentDecodeLoop()(model, torch.zeros((1, 4), dtype=torch.int64), 2)
+
+
+def test_a_slot_kernel_without_a_call_site_is_refused():
+    from deltaforge_amd.model import step_plan
+    from deltaforge_amd.synth import synth_model
+
+    reg = _registry_with()
+    reg.register("third_party_delta", impl=lambda *a: None, replaces="gated_delta_rule")
+    reg.promote("third_party_delta")
+    model = synth_model(mid_config(num_layers=4), seed=0)
+    apply_champions(model, reg, installers={**INSTALLERS, "third_party_delta": INSTALLERS["hip_delta_rule_step"]})
+    with pytest.raises(InstallerMissing, match="no call site"):
+        step_plan(model)
+    with pytest.raises(InstallerMissing):
+        greedy_decode(model, torch.zeros((1, 4), dtype=torch.int64), 2)
+
+
+def test_prefill_geometry_rule():
+    from deltaforge_amd.config import qwen3_5_4b_config, tiny_config
+    from deltaforge_amd.prefill import unsupported_geometry
+
+    assert unsupported_geometry(qwen3_5_4b_config()) is None
+    assert unsupported_geometry(mid_config(num_layers=4)) is None
+    assert unsupported_geometry(tiny_config()) is not None

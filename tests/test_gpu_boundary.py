@@ -177,3 +177,31 @@ def test_split_kv_workspace_reused_across_shapes():
         want = oracle_ops.decode_attention(q, k, v, scale)
         got = hip_ops.split_kv_decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), scale, splits)
         close(got, want, what=f"split_kv B={batch} L={key_len} S={splits}")
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_delta_step_inputs_match_the_reference_prologue(batch):
+    """The inputs the standalone step is composed with, against the oracle's expressions of
+    the reference's prologue (l2norm, the Dk^-1/2 scale, key heads repeated over value
+    heads, beta = bf16(sigmoid(b)), g = -exp(A_log) softplus(a + dt_bias))."""
+    import torch.nn.functional as F
+
+    from deltaforge_amd import ops
+    from oracle.model import l2norm
+
+    gen = torch.Generator().manual_seed(40 + batch)
+    hk, hv, dk, dv = 16, 32, 128, 128
+    mixed = torch.randn((batch, 2 * hk * dk + hv * dv), generator=gen).to(BF16)
+    ab = torch.randn((batch, 2 * hv + 5), generator=gen).to(BF16)  # a | b | padding: strided rows
+    a, b = ab[:, :hv], ab[:, hv:2 * hv]
+    A_log = torch.randn(hv, generator=gen).to(BF16)
+    dt_bias = torch.randn(hv, generator=gen).to(BF16)
+    got = ops.delta_step_inputs(mixed.to(DEV), ab.to(DEV)[:, :hv], ab.to(DEV)[:, hv:2 * hv], A_log.to(DEV),
+                                dt_bias.to(DEV), num_k_heads=hk, head_v_dim=dv)
+    q = mixed[:, :hk * dk].float().view(batch, hk, dk).repeat_interleave(hv // hk, dim=1)
+    k = mixed[:, hk * dk:2 * hk * dk].float().view(batch, hk, dk).repeat_interleave(hv // hk, dim=1)
+    want = (l2norm(q) / dk ** 0.5, l2norm(k), mixed[:, 2 * hk * dk:].float().view(batch, hv, dv),
+            -A_log.float().exp() * F.softplus(a.float() + dt_bias.float()), b.sigmoid().float())
+    for name, g_, w_ in zip(("query", "key", "value", "g", "beta"), got, want):
+        assert g_.dtype == torch.float32 and g_.shape == w_.shape, name
+        torch.testing.assert_close(g_.cpu(), w_, atol=2e-6, rtol=2e-6, msg=name)
