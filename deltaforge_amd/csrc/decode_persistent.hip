@@ -31,20 +31,11 @@
 // ds_read so the compiler does not insert a vmcnt(0) before them (it cannot tell which
 // slot a DMA targets); the kernel waits explicitly for exactly the block it consumes.
 //
-// GEMV arithmetic (fp16 MFMA). A block's B operand holds each nibble as an fp16 subnormal: one
-// shift and four v_and per dword leave nibble n in bits 0..3 of a half (the value n * 2^-24) or
-// in bits 4..7 (16 n * 2^-24), 5 VALU ops per 8 weights and no offset to cancel. The input row
-// is staged in fp16 as x' = x, or x / 16 where the weight carries the extra 16 (k % 8 in 2, 3,
-// 6, 7). Per 128-group the MFMA gives D = 2^-24 sum x_k n_k, a sum of exact products in fp32, and
-// with the group's c = 8 * 2^-24 sum x_k, y += (s 2^24) (D - c) = s sum x_k (n_k - 8). That is
-// the reference's sum x_k * bf16((n_k - 8) s) without the per-weight bf16 rounding (relative
-// 2^-9), i.e. the exact-weight product; D and c differ by about the ratio of the group's mean to
-// its spread, so the subtraction costs a few of fp32's 24 bits.
-// Range: fp16 holds every bf16 value below 2^15 = 32768 exactly in its normal range (values
-// under 2^-14 become subnormals, an absolute error under 2^-25). RMSNorm outputs are bounded by
-// sqrt(hidden) * max |1 + w| (the host refuses norm weights that could reach 2^15); the other
-// GEMV inputs (SwiGLU, GatedRMSNorm, attention outputs) are checked as they are staged, and a
-// value at or above 2^15 aborts the launch (kErrRange) rather than overflow to inf.
+// GEMV arithmetic (bf16 MFMA). Each lane dequantises the 32 weights it holds of a block with
+// dequant8 (int4_block.h): bf16((n - 8) s), the reference's expression bit for bit, 19 VALU ops
+// per 8 weights. The input row is staged in bf16 as it is, so any bf16 activation is taken as
+// it comes, and v_mfma_f32_16x16x32_bf16 sums the exact products in fp32 (row 0 of the
+// 16-row product; rows 1..15 are don't-cares).
 //
 // Other arithmetic is the per-op kernels' (gated_delta.hip, attention.hip, small_ops.hip),
 // with the reference's rounding points; only fp32 summation orders differ.
@@ -89,25 +80,15 @@ constexpr int kTileKeys = kCompute * 16;            // 128 keys per attention ti
 constexpr int kSplits = 2 * kPerXcd;                // key splits of a KV head over its XCD pair
 constexpr int kPairHeads = 4;                       // query heads of a KV head (2 per XCD of the pair);
                                                     // an XCD's own two are its slots 0, 1
-// int4 dot product: B = the nibbles as fp16 subnormals, the input row staged as fp16 (see the
-// file comment)
-typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 df_f16x8;
-constexpr float kStageMax = 32768.0f;               // staged inputs must lie below 2^15
-constexpr float kTwo24 = 16777216.0f;                // 2^24, the subnormal weights' scale
-
-// The fp16 GEMV input x' of element k (x / 16 where the weight carries the factor 16), and its
-// term of the group sum c = 8 * 2^-24 sum x.
-DF_DEVICE _Float16 xh_of(float x, int k) { return static_cast<_Float16>((k & 2) ? x * 0.0625f : x); }
-DF_DEVICE float c_of(float sum_x) { return sum_x * (8.0f / kTwo24); }
-DF_DEVICE uint32_t pack_h2(_Float16 a, _Float16 b) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) | (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
-}
+// int4 dot product: B = the reference's dequantised weights bf16((n - 8) s) (dequant8), the
+// input row staged in bf16 as it is (see the file comment).
+// Two bf16 values (already bf16-rounded floats) as one packed dword, k order.
+DF_DEVICE uint32_t pack_x2(float a, float b) { return (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xFFFF0000u); }
 
 constexpr uint64_t kTimeout = 50000000ull;          // 0.5 s of s_memrealtime (100 MHz)
 constexpr int kRegBase = 4;                         // ctl[4..11]: per-XCD registration tickets
 
-enum Err : int { kErrNone = 0, kErrTimeout = 1, kErrXcd = 2, kErrPosition = 3, kErrToken = 4, kErrSchedule = 5,
-                 kErrRange = 6 };
+enum Err : int { kErrNone = 0, kErrTimeout = 1, kErrXcd = 2, kErrPosition = 3, kErrToken = 4, kErrSchedule = 5 };
 
 struct Ws {
   int* ctl;          // [16]: epoch, abort, error, -, 8 registration tickets, -
@@ -259,14 +240,13 @@ DF_DEVICE float row_sum_mod4(float v) {
 __shared__ __align__(16) uint4 g_ring_w[kCompute][kRing][64];     // 1 KB blocks
 __shared__ __align__(16) uint32_t g_ring_s[kCompute][kRing][16];  // scale dword of lane i < 16: columns (i & 14), +1
 __shared__ __align__(16) uint16_t g_x[kMaxHidden + 8];            // the staged core (bf16), GatedRMSNorm's input
-__shared__ __align__(16) uint16_t g_xh[kMaxHidden + 8];           // GEMV input row x' (fp16)
+__shared__ __align__(16) uint16_t g_xh[kMaxHidden + 8];           // GEMV input row (bf16)
 
 struct Lds {
   __align__(16) uint16_t h[kMaxHidden];          // the hidden vector (bf16)
   __align__(16) uint16_t nw[kMaxHidden];         // the next RMSNorm's weight (LDS DMA, a phase ahead)
   __align__(16) uint16_t gnw[kDk];               // GatedRMSNorm weight (LDS DMA, a phase ahead)
   __align__(16) float zs[512];                   // out_proj: SiLU inputs of the GatedRMSNorm (staged during delta)
-  float xs[kMaxGroups];                          // each 128-group's c = 8 * 2^-24 sum x
   float ss;                                      // sum of squares of h (for the next RMSNorm)
   __align__(16) float part[kMaxWgTiles][16][kCompute];  // per-wave tile partials (a column's 8 adjacent)
   float red[64];
@@ -511,8 +491,7 @@ DF_DEVICE bool poll_tagged(const Ctx& c, F&& load) {
 // ---------------------------------------------------------------------------------------
 
 // Compute waves (1 barrier; the control wave passes 1): x = bf16(RMSNorm(h) * (1 + w)) over
-// `hidden` (w staged in L.nw) as the fp16 row g_xh, and the group sums L.xs. Every wave sums the squares of
-// all of h itself (identical code and order in every wave, so all agree on the factor), which
+// `hidden` (w staged in L.nw) as the bf16 row g_xh. Every wave sums the squares of all of h itself (identical code and order in every wave, so all agree on the factor), which
 // saves the cross-wave exchange and its barrier; a wave then produces whole 128-groups
 // (2 elements per lane).
 constexpr int kNormBars = 1;
@@ -525,9 +504,7 @@ DF_DEVICE void norm_w(Lds& L, Ctx& c, int hidden, float eps) {
     const uint32_t wv = *reinterpret_cast<const uint32_t*>(&L.nw[k]);
     const float x0 = round_bf(__uint_as_float(hv << 16) * r * (1.0f + __uint_as_float(wv << 16)));
     const float x1 = round_bf(__uint_as_float(hv & 0xFFFF0000u) * r * (1.0f + __uint_as_float(wv & 0xFFFF0000u)));
-    *reinterpret_cast<uint32_t*>(&g_xh[k]) = pack_h2(xh_of(x0, k), xh_of(x1, k + 1));
-    const float sg = c_of(dsum(x0 + x1));
-    if (c.lane == 0) L.xs[g] = sg;
+    *reinterpret_cast<uint32_t*>(&g_xh[k]) = pack_x2(x0, x1);
   }
   sync(c);
 }
@@ -849,56 +826,49 @@ DF_DEVICE void ring_read1(int slot, const Ctx& c, uint4& wv, uint32_t& sd) {
 }
 
 // Everything a pair of blocks needs from LDS, with one wait: both ring slots (weights,
-// scale dword), the two groups' input chunks of this lane's k slot and their group sums.
-// Only row 0 of each product is used: its A operand comes from lanes 0, 16, 32 and 48, and
-// its scales, group sums and results live in lanes 0..15. The input chunks are read by
-// those four lanes only (exec masked inside the asm and restored before it ends), which
-// cuts the LDS traffic of a pair from 11 KB to under 4 KB; the other lanes' copies hold
-// stale values that only feed rows 1..15. The scale dwords (16 distinct per slot) and the
-// group sums (one address) are read by every lane: broadcasts, cheaper than two more exec
-// switches.
+// scale dword) and the two groups' input chunks of this lane's k slot. Only row 0 of each
+// product is used: its A operand comes from lanes 0, 16, 32 and 48, and its results live in
+// lanes 0..15. The input chunks are read by those four lanes only (exec masked inside the
+// asm and restored before it ends), which cuts the LDS traffic of a pair from 11 KB to under
+// 4 KB; the other lanes' copies hold stale values that only feed rows 1..15. Every lane reads
+// its column's scale dword (16 distinct per slot, broadcasts): the B operand of every lane is
+// dequantised with it.
 struct PairIn {
   uint4 w0, w1;
   uint32_t s0, s1;
   uint4 x0[4], x1[4];
-  float xs0, xs1;
 };
-DF_DEVICE void pair_read(int slot, const Ctx& c, const uint16_t* xg0, const uint16_t* xg1, const float* xsp0,
-                         const float* xsp1, PairIn& in) {
+DF_DEVICE void pair_read(int slot, const Ctx& c, const uint16_t* xg0, const uint16_t* xg1, PairIn& in) {
   const int slot1 = next_slot(slot);
   const uint32_t wa0 = lds_addr(&g_ring_w[c.wave][slot][c.lane]);
   const uint32_t sa0 = lds_addr(&g_ring_s[c.wave][slot][c.lane & 15]);
   const uint32_t wa1 = lds_addr(&g_ring_w[c.wave][slot1][c.lane]);
   const uint32_t sa1 = lds_addr(&g_ring_s[c.wave][slot1][c.lane & 15]);
   const uint32_t xa0 = lds_addr(xg0), xa1 = lds_addr(xg1);
-  const uint32_t ya0 = lds_addr(xsp0), ya1 = lds_addr(xsp1);
   uint64_t saved;
   asm volatile(
-      "ds_read_b128 %0, %15\n\t"
-      "ds_read_b128 %1, %17\n\t"
-      "ds_read_b32 %2, %16\n\t"
-      "ds_read_b32 %3, %18\n\t"
-      "ds_read_b32 %12, %21\n\t"
-      "ds_read_b32 %13, %22\n\t"
-      "s_mov_b64 %14, exec\n\t"
+      "ds_read_b128 %0, %13\n\t"
+      "ds_read_b128 %1, %15\n\t"
+      "ds_read_b32 %2, %14\n\t"
+      "ds_read_b32 %3, %16\n\t"
+      "s_mov_b64 %12, exec\n\t"
       "s_mov_b32 exec_lo, 0x10001\n\t"
       "s_mov_b32 exec_hi, 0x10001\n\t"
       "s_nop 0\n\t"
-      "ds_read_b128 %4, %19\n\t"
-      "ds_read_b128 %5, %19 offset:16\n\t"
-      "ds_read_b128 %6, %19 offset:32\n\t"
-      "ds_read_b128 %7, %19 offset:48\n\t"
-      "ds_read_b128 %8, %20\n\t"
-      "ds_read_b128 %9, %20 offset:16\n\t"
-      "ds_read_b128 %10, %20 offset:32\n\t"
-      "ds_read_b128 %11, %20 offset:48\n\t"
-      "s_mov_b64 exec, %14\n\t"
+      "ds_read_b128 %4, %17\n\t"
+      "ds_read_b128 %5, %17 offset:16\n\t"
+      "ds_read_b128 %6, %17 offset:32\n\t"
+      "ds_read_b128 %7, %17 offset:48\n\t"
+      "ds_read_b128 %8, %18\n\t"
+      "ds_read_b128 %9, %18 offset:16\n\t"
+      "ds_read_b128 %10, %18 offset:32\n\t"
+      "ds_read_b128 %11, %18 offset:48\n\t"
+      "s_mov_b64 exec, %12\n\t"
       "s_nop 0\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&v"(in.w0), "=&v"(in.w1), "=&v"(in.s0), "=&v"(in.s1), "=&v"(in.x0[0]), "=&v"(in.x0[1]), "=&v"(in.x0[2]),
-        "=&v"(in.x0[3]), "=&v"(in.x1[0]), "=&v"(in.x1[1]), "=&v"(in.x1[2]), "=&v"(in.x1[3]), "=&v"(in.xs0),
-        "=&v"(in.xs1), "=&s"(saved)
-      : "v"(wa0), "v"(sa0), "v"(wa1), "v"(sa1), "v"(xa0), "v"(xa1), "v"(ya0), "v"(ya1)
+        "=&v"(in.x0[3]), "=&v"(in.x1[0]), "=&v"(in.x1[1]), "=&v"(in.x1[2]), "=&v"(in.x1[3]), "=&s"(saved)
+      : "v"(wa0), "v"(sa0), "v"(wa1), "v"(sa1), "v"(xa0), "v"(xa1)
       : "memory");
 }
 
@@ -910,55 +880,41 @@ DF_DEVICE void take_block(Stream& st, const Ctx& c, uint4& wv, uint32_t& sd) {
   st.rslot = next_slot(st.rslot);
 }
 
-DF_DEVICE void take_pair(Stream& st, const Ctx& c, const uint16_t* xg0, const uint16_t* xg1, const float* xsp0,
-                          const float* xsp1, PairIn& in) {
+DF_DEVICE void take_pair(Stream& st, const Ctx& c, const uint16_t* xg0, const uint16_t* xg1, PairIn& in) {
   wait_oldest<2>(st);
-  pair_read(st.rslot, c, xg0, xg1, xsp0, xsp1, in);
+  pair_read(st.rslot, c, xg0, xg1, in);
   st.consumed += 2;
   st.rslot = next_slot(next_slot(st.rslot));
 }
 
-// Row 0 of one block's product: lanes 0..15 return s_col * sum_k x_k (n_k - 8) over the
-// block's 128 k (x = the group's fp16 input chunks x' at this lane's k slot, xs = the group's
-// c, sh = 16 * (lane & 1) selects this lane's scale in the dword). A dword's nibble pairs
-// (bits 4j, 16 + 4j) become the fp16 pairs w & m_lo, w & m_hi, (w >> 8) & m_lo, (w >> 8) & m_hi:
-// subnormals n * 2^-24 for k % 8 in 0, 1, 4, 5 and 16 n * 2^-24 for k % 8 in 2, 3, 6, 7. The
-// masks arrive as opaque SGPR values, so the compiler emits one v_and_b32 each (gfx9 VOP3
-// encodes no literal) and its hazard checks still cover the results, which feed an MFMA.
-struct DotK {
-  uint32_t mlo, mhi;
-};
-// Made once per loop, outside it: opaque to the compiler, so they stay in registers.
-DF_DEVICE DotK dot_consts() {
-  DotK k{0x000F000Fu, 0x00F000F0u};
-  asm volatile("" : "+s"(k.mlo), "+s"(k.mhi));
-  return k;
-}
-DF_DEVICE float block_dot_r(const uint4& wv, uint32_t sd, const uint4 (&x)[4], float xs, uint32_t sh, const DotK& K) {
-  const float s = __uint_as_float((sd >> sh) << 16);
+// Row 0 of one block's product: lanes 0..15 return sum_k x_k bf16((n_k - 8) s_col) over the
+// block's 128 k (x = the group's bf16 input chunks at this lane's k slot, sh = 16 * (lane & 1)
+// selects this lane's column scale in the dword). Each lane dequantises its own 32 weights
+// with dequant8, the reference's expression bit for bit, and the four bf16 MFMAs sum the
+// products in fp32.
+DF_DEVICE float block_dot_r(const uint4& wv, uint32_t sd, const uint4 (&x)[4], uint32_t sh) {
+  const GroupScale gs = group_scale(static_cast<uint16_t>(sd >> sh));
   const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
-  const uint32_t mlo = K.mlo, mhi = K.mhi;
   df_f32x4 d4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    const uint32_t w = words[d], t = w >> 8;
-    const uint4 bw = make_uint4(w & mlo, w & mhi, t & mlo, t & mhi);
-    d4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(df_f16x8, x[d]), __builtin_bit_cast(df_f16x8, bw),
-                                                d4, 0, 0, 0);
+    const uint4 bw = dequant8(words[d], gs);
+    d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, x[d]), __builtin_bit_cast(df_bf16x8, bw),
+                                                 d4, 0, 0, 0);
   }
-  return (s * kTwo24) * (d4[0] - xs);
+  return d4[0];
 }
 
 // Single-block form reading its input from LDS.
-DF_DEVICE float block_dot(const uint4& wv, uint32_t sd, const uint16_t* x, float xs, int lane) {
+DF_DEVICE float block_dot(const uint4& wv, uint32_t sd, const uint16_t* x, int lane) {
   uint4 xv[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) xv[d] = *reinterpret_cast<const uint4*>(x + d * 8);
-  return block_dot_r(wv, sd, xv, xs, 16u * (lane & 1), dot_consts());
+  return block_dot_r(wv, sd, xv, 16u * (lane & 1));
 }
 
-// Compute waves: consume this wave's blocks of GEMV phase g (input row g_x, group sums
-// L.xs); per-tile partials of row 0 go to L.part[tile - first tile of the workgroup][wave].
+// Compute waves: consume this wave's blocks of GEMV phase g (input row g_xh); per-tile
+// partials of row 0 go to L.part[tile - first tile of the workgroup][wave].
 // Blocks are taken two at a time (two independent MFMA chains per iteration).
 DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPersistModel& M, const Geo& q,
                             int steps, Lds& L) {
@@ -982,15 +938,14 @@ DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPer
     }
   };
   const uint32_t sh = 16u * (c.lane & 1);
-  const DotK K = dot_consts();
   int i = 0;
 #pragma unroll 1
   for (; i + 1 < n; i += 2) {
     const int gl1 = gl + 1 == g.ng ? 0 : gl + 1;
     PairIn in;
-    take_pair(st, c, xb + gl * kGroup, xb + gl1 * kGroup, &L.xs[gl], &L.xs[gl1], in);
-    const float v0 = block_dot_r(in.w0, in.s0, in.x0, in.xs0, sh, K);
-    const float v1 = block_dot_r(in.w1, in.s1, in.x1, in.xs1, sh, K);
+    take_pair(st, c, xb + gl * kGroup, xb + gl1 * kGroup, in);
+    const float v0 = block_dot_r(in.w0, in.s0, in.x0, sh);
+    const float v1 = block_dot_r(in.w1, in.s1, in.x1, sh);
     refill2(st, steps, c);
     add(v0);
     add(v1);
@@ -999,7 +954,7 @@ DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPer
     uint4 w0;
     uint32_t s0;
     take_block(st, c, w0, s0);
-    add(block_dot(w0, s0, xb + gl * kGroup, L.xs[gl], c.lane));
+    add(block_dot(w0, s0, xb + gl * kGroup, c.lane));
     fill(st, steps, c);
   }
   if (n > 0 && gl != 0 && c.lane < 16) L.part[tr][c.lane][c.wave] = acc;
@@ -1207,7 +1162,7 @@ DF_DEVICE void stage_gu(const Ctx& c, int inter_x, float* gu) {
 }
 
 // Compute waves (1 barrier; the control wave passes 1): the down projection's input
-// act = bf16(bf16(silu(g)) * u) as the fp16 row g_xh, and its group sums L.xs. The gate|up columns come
+// act = bf16(bf16(silu(g)) * u) as the bf16 row g_xh. The gate|up columns come
 // in 32-column pairs (16 gate columns, then their 16 up columns), so act j reads gate
 // column 32 (j / 16) + j % 16 and the up column 16 further. A wave produces whole
 // 128-groups (2 elements per lane).
@@ -1221,18 +1176,14 @@ DF_DEVICE void swiglu_act(Lds& L, Ctx& c, int inter_x) {
     const float2 uv = *reinterpret_cast<const float2*>(gu + col + 16);
     const float x0 = round_bf(round_bf(silu(round_bf(gv.x))) * round_bf(uv.x));
     const float x1 = round_bf(round_bf(silu(round_bf(gv.y))) * round_bf(uv.y));
-    if (!__all(fmaxf(fabsf(x0), fabsf(x1)) < kStageMax)) raise_abort(c, kErrRange);
-    *reinterpret_cast<uint32_t*>(&g_xh[j]) = pack_h2(xh_of(x0, j), xh_of(x1, j + 1));
-    const float sg = c_of(dsum(x0 + x1));
-    if (c.lane == 0) L.xs[g] = sg;
+    *reinterpret_cast<uint32_t*>(&g_xh[j]) = pack_x2(x0, x1);
   }
   sync(c);
 }
 
 // Control wave: the XCD's 512 merged attention / delta outputs (tagged bf16, published by the
 // workgroups of the XCD at epoch `want`) into g_x (the GatedRMSNorm's input) or, as the GEMV
-// input itself (`direct`), into g_xh with the group sums L.xs of its four 128-groups
-// (a group is one 16-lane row of 8 values per lane).
+// input itself (`direct`), into g_xh.
 DF_DEVICE bool stage_core(Lds& L, const Ctx& c, uint32_t want, bool direct) {
   const auto r = rsrc(c.w.core + (size_t)c.xcd * 512);
   uint4 v0, v1;
@@ -1244,24 +1195,7 @@ DF_DEVICE bool stage_core(Lds& L, const Ctx& c, uint32_t want, bool direct) {
     return false;
   const uint4 v = make_uint4((v0.x & 0xFFFFu) | (v0.y << 16), (v0.z & 0xFFFFu) | (v0.w << 16),
                              (v1.x & 0xFFFFu) | (v1.y << 16), (v1.z & 0xFFFFu) | (v1.w << 16));
-  if (!direct) {
-    *reinterpret_cast<uint4*>(&g_x[c.lane * 8]) = v;
-  } else {
-    float s = 0.0f, amax = 0.0f;
-    uint32_t hw[4];
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {  // elements 8 lane + 2 e, + 1
-      const float x0 = __uint_as_float(w[e] << 16), x1 = __uint_as_float(w[e] & 0xFFFF0000u);
-      hw[e] = pack_h2(xh_of(x0, 2 * e), xh_of(x1, 2 * e + 1));
-      s += x0 + x1;
-      amax = fmaxf(amax, fmaxf(fabsf(x0), fabsf(x1)));
-    }
-    if (!__all(amax < kStageMax)) raise_abort(c, kErrRange);
-    *reinterpret_cast<uint4*>(&g_xh[c.lane * 8]) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    s = c_of(row_sum(s));
-    if ((c.lane & 15) == 0) L.xs[c.lane >> 4] = s;
-  }
+  *reinterpret_cast<uint4*>(direct ? &g_xh[c.lane * 8] : &g_x[c.lane * 8]) = v;
   return true;
 }
 
@@ -1977,11 +1911,8 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
             const float t1 = round_bf(bf2f(L.gnw[64 + c.lane]) * round_bf(v1 * rr));
             const float xv0 = round_bf(t0 * silu(L.zs[i0]));
             const float xv1 = round_bf(t1 * silu(L.zs[i1]));
-            if (!__all(fmaxf(fabsf(xv0), fabsf(xv1)) < kStageMax)) raise_abort(c, kErrRange);
-            g_xh[i0] = __builtin_bit_cast(uint16_t, xh_of(xv0, i0));
-            g_xh[i1] = __builtin_bit_cast(uint16_t, xh_of(xv1, i1));
-            const float gs = c_of(dsum(xv0 + xv1));
-            if (c.lane == 0) L.xs[c.wave] = gs;
+            g_xh[i0] = f2bf(xv0);
+            g_xh[i1] = f2bf(xv1);
           }
           sync(c);
           gemv_consume(g, c, st, M, q, steps, L);
@@ -2197,7 +2128,6 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       const int t0 = head_tile(q, c.wave), ntw = head_tile(q, c.wave + 1) - t0;
       const uint16_t* xb = g_xh + (c.lane >> 4) * 32;
       const uint32_t sh = 16u * (c.lane & 1);
-      const DotK K = dot_consts();
       float bv = -INFINITY;
       int bi = 0x7FFFFFFF;
       float acc = 0.0f;
@@ -2206,9 +2136,9 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
 #pragma unroll 1
       for (int i = 0; i < ntw * G; i += 2) {
         PairIn in;
-        take_pair(st, c, xb + gl * kGroup, xb + (gl + 1) * kGroup, &L.xs[gl], &L.xs[gl + 1], in);
-        const float v0 = block_dot_r(in.w0, in.s0, in.x0, in.xs0, sh, K);
-        const float v1 = block_dot_r(in.w1, in.s1, in.x1, in.xs1, sh, K);
+        take_pair(st, c, xb + gl * kGroup, xb + (gl + 1) * kGroup, in);
+        const float v0 = block_dot_r(in.w0, in.s0, in.x0, sh);
+        const float v1 = block_dot_r(in.w1, in.s1, in.x1, sh);
         refill2(st, steps, c);
         acc += v0;
         acc += v1;

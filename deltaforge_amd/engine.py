@@ -34,6 +34,10 @@ BF16 = torch.bfloat16
 
 __all__ = ["DecodeEngine", "STANDALONE_SLOTS"]
 
+#: Split count the standalone attention op is called with (the reference's DEFAULT_SPLITS at
+#: the call site its installer swaps in, kernels/flash_decode_splitkv.py:46, 322-324).
+STANDALONE_SPLITS = 8
+
 #: Slots whose champion may be a standalone op instead of the fused kernel, and the other
 #: slots the standalone composition calls at its sites (their champions' impls go along).
 STANDALONE_SLOTS = {
@@ -212,7 +216,7 @@ class DecodeEngine:
         e["k_cache"][:, :, pos] = key
         e["v_cache"][:, :, pos] = self.proj[:, qd + kd:qd + 2 * kd].reshape(b, hkv, d)
         attn = self.standalone["gqa_attention"](query.contiguous(), e["k_cache"][:, :, :pos + 1].contiguous(),
-                                                e["v_cache"][:, :, :pos + 1].contiguous(), d ** -0.5, self.splits)
+                                                e["v_cache"][:, :, :pos + 1].contiguous(), d ** -0.5, STANDALONE_SPLITS)
         gate = q_gate[:, :, 1].reshape(b, hq * d).float()
         gate = (torch.sigmoid(gate) if c.output_gate_type == SIGMOID_GATE else torch.nn.functional.silu(gate)).to(BF16)
         torch.mul(attn.reshape(b, hq * d), gate, out=self.core[:, :hq * d])

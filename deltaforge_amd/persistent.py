@@ -22,7 +22,7 @@ from . import ops
 from .config import FULL_ATTENTION, SIGMOID_GATE, ModelConfig
 from .synth import SynthModel, inv_freq
 
-__all__ = ["PersistentDecoder", "attention_proj_columns", "check_geometry", "check_norm_range", "linear_proj_columns", "rope_table"]
+__all__ = ["PersistentDecoder", "attention_proj_columns", "check_geometry", "linear_proj_columns", "rope_table"]
 
 BF16 = torch.bfloat16
 XCD = 8
@@ -30,8 +30,7 @@ LIN_COLS = 1552  # per XCD: q 256, k 256, v 512, z 512, a 4, b 4, 8 zero columns
 ATTN_COLS = 1536  # per XCD: 2 x (query 256 | gate 256), k 256, v 256
 ERRORS = {1: "a cross-workgroup hand-off timed out", 2: "a workgroup ran on an unexpected XCD",
           3: "position, prompt or token log out of range", 4: "token id out of range",
-          5: "control/compute barrier schedules disagree",
-          6: "a GEMV input reached 2^15, beyond the kernel's fp16 staging range"}
+          5: "control/compute barrier schedules disagree"}
 
 
 def linear_proj_columns(c: ModelConfig) -> torch.Tensor:
@@ -89,19 +88,6 @@ def rope_table(c: ModelConfig, max_len: int) -> torch.Tensor:
     return (cs | (sn << 16)).contiguous()
 
 
-def check_norm_range(config: ModelConfig, params: dict) -> None:
-    """The persistent kernel stages RMSNorm outputs in fp16 unchecked: x = h r (1 + w) with
-    sum (h r)^2 <= hidden, so |x| <= sqrt(hidden) * max |1 + w|, which must stay below 2^15 for
-    every RMSNorm weight (the layers' input and post-attention norms and the final norm)."""
-    bound = 32768.0 / config.hidden_size ** 0.5
-    for name, w in params.items():
-        if name == "norm.weight" or name.endswith("input_layernorm.weight") or name.endswith("post_attention_layernorm.weight"):
-            peak = float((1.0 + w.float()).abs().max())
-            if peak >= bound:
-                raise ValueError(f"{name}: max |1 + w| = {peak:.4g} reaches {bound:.4g}, where the persistent "
-                                 f"kernel's fp16 staging of the normed row could overflow")
-
-
 def check_geometry(c: ModelConfig) -> None:
     ok = (c.linear_num_key_heads == 16 and c.linear_num_value_heads == 32 and c.linear_key_head_dim == 128
           and c.linear_value_head_dim == 128 and c.num_attention_heads == 16 and c.num_key_value_heads == 4
@@ -128,7 +114,6 @@ class PersistentDecoder:
         self.max_new_tokens = max_new_tokens
         self.device = dev = torch.device(device)
         ops.require_gpu(torch.empty(0, device=dev), "decode_persistent")
-        check_norm_range(c, model.params)
         p = {k: v.to(dev) for k, v in model.params.items()}
         lin = model.linears
 

@@ -182,13 +182,11 @@ def test_greedy_decode_through_the_promoted_persistent_candidate(mid):
     assert torch.equal(again, got)
 
 
-def test_persistent_aborts_when_a_gemv_input_leaves_the_fp16_range(mid):
-    """The persistent kernel stages GEMV inputs in fp16, exact below 2^15. A SwiGLU output at or
-    above 2^15 (one layer's up_proj scales raised 10^5-fold, so act = silu(g) * u reaches ~10^5)
-    must abort the launch with the range error instead of computing with inf; the per-op engine,
-    whose bf16 dequant has no such limit, decodes the same model to finite logits."""
-    from deltaforge_amd._native import NativeError
-
+def test_persistent_takes_gemv_inputs_beyond_the_fp16_range(mid):
+    """GEMV inputs are staged in bf16 and weights dequantised to bf16, so activations far
+    beyond fp16's 65504 go through as the per-op engine takes them: one layer's up_proj scales
+    raised 10^5-fold (act = silu(g) * u reaches ~10^5) give both decoders finite logits, the
+    same argmax and a KL at the level of summation-order noise."""
     cfg, model, prompt, _, _ = mid
     big = synth.SynthModel(config=model.config, params=dict(model.params), linears=dict(model.linears))
     up = big.linears["layers.1.mlp.up_proj.weight"]
@@ -196,10 +194,11 @@ def test_persistent_aborts_when_a_gemv_input_leaves_the_fp16_range(mid):
         up, scale=(up.scale.float() * 1e5).to(up.scale.dtype))
     eng = DecodeEngine(big, max_seq_len=64, max_new_tokens=16)
     eng.prefill(prompt[:, :4].cuda())
-    torch.cuda.synchronize()
-    assert bool(torch.isfinite(eng.logits.float()).all())
     dec = PersistentDecoder(big, max_seq_len=64, max_new_tokens=16)
-    for _ in range(2):  # the abort leaves the decoder usable after reset (prefill resets)
-        dec.prefill(prompt[:, :4].cuda())
-        with pytest.raises(NativeError, match="fp16 staging range"):
-            dec.check()
+    dec.prefill(prompt[:, :4].cuda())
+    dec.check()
+    want, got = eng.logits.float().cpu(), dec.logits.float().cpu()
+    assert bool(torch.isfinite(want).all()) and bool(torch.isfinite(got).all())
+    kl, agree = kl_and_agreement(want, got)
+    print(f"act ~1e5: persistent vs engine KL {float(kl.mean()):.3e}, argmax agree {bool(agree.all())}", flush=True)
+    assert bool(agree.all()) and float(kl.mean()) < 1e-3

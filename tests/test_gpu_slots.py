@@ -6,7 +6,9 @@ reference-signature standalone op promoted, both promoted) a fresh mid-config mo
 prefills the prompt in one parallel pass and then steps through the slot's installed
 kernels. The engine is then teacher-forced over the oracle's greedy continuation and scored
 as the reference's layer-2 gate scores (harness/correctness.py:383-464): mean KL < 1e-3 and
-top-1 agreement, with the free-running tokens' first divergence reported.
+top-1 agreement, with the free-running tokens' first divergence allowed only at a near tie
+of the oracle's top two logits (correctness.py:508-553). The model draws the symmetric
+int4 range, so its logits follow the input.
 
 The persistent loop is checked the same way, and both loops' prefill path is shown to be the
 parallel one on a long prompt.
@@ -50,7 +52,7 @@ def registry_with(*promoted: str) -> KernelRegistry:
 @pytest.fixture(scope="module")
 def ref():
     cfg = mid_config(4)
-    model = synth.synth_model(cfg, seed=5)
+    model = synth.synth_model(cfg, seed=5, symmetric=True)
     prompt = synth.prompt_ids(cfg.vocab_size, 24, seed=6)
     with torch.no_grad():
         tokens, logits = oracle_for(model).greedy(prompt, NEW)
@@ -78,7 +80,7 @@ def teacher_forced(loop, prompt, ref_tokens):
 @pytest.mark.parametrize("variant", list(VARIANTS))
 def test_greedy_decode_through_the_installed_slots_matches_the_oracle(ref, variant):
     cfg, prompt, ref_tokens, ref_logits = ref
-    model = synth.synth_model(cfg, seed=5)
+    model = synth.synth_model(cfg, seed=5, symmetric=True)
     applied = apply_champions(model, registry_with(*VARIANTS[variant]))
     for name in VARIANTS[variant]:
         assert name in applied
@@ -97,7 +99,10 @@ def test_greedy_decode_through_the_installed_slots_matches_the_oracle(ref, varia
           f"teacher-forced mean KL {float(kl.mean()):.3e}, top-1 {float(agree.float().mean()):.3f}", flush=True)
     assert float(kl.mean()) < 1e-3
     assert float(agree.float().mean()) >= 7 / 8
-    assert diverge is None or diverge >= 4
+    if diverge is not None:  # a free-run split is allowed only where the oracle's top two nearly tie
+        top2 = ref_logits[0, diverge].float().topk(2).values
+        print(f"[{variant}] oracle top-2 gap at the divergence: {float(top2[0] - top2[1]):.4f}", flush=True)
+        assert float(top2[0] - top2[1]) <= 0.125
 
 
 @pytest.mark.parametrize("variant", ["fused", "both", "persistent"])
@@ -106,7 +111,7 @@ def test_greedy_decode_prefills_a_long_prompt_in_one_parallel_pass(variant):
     oracle's argmax (or within 0.125 of its top logit, a near tie), and its time is printed
     beside the teacher-forced prefill of the same decoder."""
     cfg = mid_config(4)
-    model = synth.synth_model(cfg, seed=9)
+    model = synth.synth_model(cfg, seed=9, symmetric=True)
     prompt = synth.prompt_ids(cfg.vocab_size, 2048, seed=10)
     apply_champions(model, registry_with(*VARIANTS[variant]))
     greedy_decode(model, prompt, 2)  # builds the loop's decoder and prefiller at this size
