@@ -374,11 +374,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DfAttnDecodeArgs p, At
 }
 
 // The splits' merge, after attn_decode_kernel: workgroup (chunk, query head, batch row), 64
-// output dims each. Wave 0 turns the S (m, l) pairs into split weights w_s = exp(m_s - m*) (0
-// for an empty split) and the denominator; wave w then sums splits w, w + 4, ... of each dim
-// with 16 independent loads in flight per lane, and the 4 wave sums are added in wave order.
-// The partials were written through to memory by workgroups on any XCD; they are read at
-// system scope (a plain load could hit a line this XCD's L2 kept from an earlier call).
+// output dims each; wave w sums splits w, w + 4, ... of each dim and the 4 wave sums are added
+// in wave order. Every wave issues its first 16 partial loads and wave 0 the (m, l) pairs of
+// up to 256 splits before any of them is used, so for S <= 64 the merge is one memory round
+// trip: wave 0 then turns the pairs into split weights w_s = exp(m_s - m*) (0 for an empty
+// split) and the denominator, and later batches (S > 64) follow. The partials were written
+// through to memory by workgroups on any XCD; they are read at system scope (a plain load
+// could hit a line this XCD's L2 kept from an earlier call).
 constexpr int kMergeBatch = 16;
 template <bool PLAIN>
 __global__ __launch_bounds__(256) void attn_merge_kernel(DfAttnDecodeArgs p, AttnWs ws) {
@@ -393,29 +395,46 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(DfAttnDecodeArgs p, Att
     if (pos < 0 || pos >= p.max_len) return;  // the split kernel refused too
   }
   const size_t row0 = ((size_t)b * p.num_q_heads + hq) * S;
+  const int d = chunk * 64 + lane;
+  const float* accp = ws.acc + row0 * kHd + d;
+  float a[kMergeBatch];
+#pragma unroll
+  for (int i = 0; i < kMergeBatch; ++i) {
+    const int sp = wave + kQPerKv * i;
+    a[i] = sp < S ? load_through(accp + (size_t)sp * kHd) : 0.0f;
+  }
   if (wave == 0) {
-    float mstar = -INFINITY;
-    for (int sp = lane; sp < S; sp += 64) {
-      const float m = load_through(ws.ml + (row0 + sp) * 2), l = load_through(ws.ml + (row0 + sp) * 2 + 1);
-      mstar = fmaxf(mstar, l > 0.0f ? m : -INFINITY);
+    constexpr int kPer = kMaxSplits / 64;
+    float m[kPer], l[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int sp = lane + 64 * j;
+      m[j] = sp < S ? load_through(ws.ml + (row0 + sp) * 2) : -INFINITY;
+      l[j] = sp < S ? load_through(ws.ml + (row0 + sp) * 2 + 1) : 0.0f;
     }
+    float mstar = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) mstar = fmaxf(mstar, l[j] > 0.0f ? m[j] : -INFINITY);
     mstar = wave_max(mstar);
     float den = 0.0f;
-    for (int sp = lane; sp < S; sp += 64) {
-      const float m = load_through(ws.ml + (row0 + sp) * 2), l = load_through(ws.ml + (row0 + sp) * 2 + 1);
-      const float w = (l > 0.0f && m != -INFINITY) ? expf(m - mstar) : 0.0f;
-      den += w * l;
-      w_s[sp] = w;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int sp = lane + 64 * j;
+      const float w = (l[j] > 0.0f && m[j] != -INFINITY) ? expf(m[j] - mstar) : 0.0f;
+      den += w * l[j];
+      if (sp < S) w_s[sp] = w;
     }
     den = wave_sum(den);
     if (lane == 0) den_s = den;
   }
   __syncthreads();
-  const int d = chunk * 64 + lane;
-  const float* accp = ws.acc + row0 * kHd + d;
   float num = 0.0f;
-  for (int s0 = wave; s0 < S; s0 += kQPerKv * kMergeBatch) {
-    float a[kMergeBatch];
+#pragma unroll
+  for (int i = 0; i < kMergeBatch; ++i) {
+    const int sp = wave + kQPerKv * i;
+    if (sp < S) num += w_s[sp] * a[i];
+  }
+  for (int s0 = wave + kQPerKv * kMergeBatch; s0 < S; s0 += kQPerKv * kMergeBatch) {
 #pragma unroll
     for (int i = 0; i < kMergeBatch; ++i) {
       const int sp = s0 + kQPerKv * i;
@@ -490,9 +509,11 @@ size_t df_attention_decode_workspace_bytes(int batch, int num_q_heads, int num_k
 }
 
 int df_attention_decode_splits(int batch, int num_kv_heads, int max_keys) {
-  // Aim for ~1024 workgroups, at least one 64-key tile per split, at most 256 splits.
+  // Aim for ~512 workgroups (two resident per CU: 216 VGPRs, 21 KB of LDS), at least one
+  // 64-key tile per split, at most 256 splits. Measured against ~1024: B=1 at 32k keys 40.7
+  // against 48.9 us, B=8 at 4k keys 38.6 against 44.5 us; the same at B=1, 4k keys.
   if (batch < 1 || num_kv_heads < 1 || max_keys < 1) return 1;
-  int s = 1024 / (batch * num_kv_heads);
+  int s = 512 / (batch * num_kv_heads);
   const int tiles = (max_keys + kTile - 1) / kTile;
   if (s > tiles) s = tiles;
   if (s > 256) s = 256;
