@@ -1,21 +1,27 @@
 """Config 5 benchmark: bs=1 greedy decode of the int4 Qwen3.5-4B-shaped hybrid on one MI355X.
 
     python bench.py [--steps 256] [--warmup 8] [--prompt-len 4096] [--no-cpu-baseline]
+                    [--engine persistent|graph]
 
-A step is one greedy decode token (one replay of the captured decode graph). The prompt
-(4096 random ids, seed 1) is prefilled untimed, the cache is snapshotted, ``warmup`` steps
-run and the snapshot is restored, then exactly ``steps`` tokens are timed with HIP events
-between device synchronisations. Weights are random-init in the model's real shapes
+A step is one greedy decode token. By default (``--engine persistent``) all ``steps`` tokens
+run inside one launch of the persistent kernel ``df::pd::decode_kernel`` (every layer of every
+token in one cooperative launch); ``--engine graph`` replays the per-op kernels as one captured
+HIP graph per token instead. The prompt (4096 random ids, seed 1) is prefilled untimed by the
+parallel prefill, the caches are snapshotted, ``warmup`` tokens run and the snapshot is
+restored, then exactly ``steps`` tokens are timed with HIP events on the stream the decode runs
+on, between device synchronisations. Weights are random-init in the model's real shapes
 (synthetic data: there is no checkpoint here). One JSON line is printed.
 
-``roofline`` is for the kernel with the largest share of decode time, the fused
-RMSNorm + gate/up int4 GEMV + SwiGLU (one launch = 2560 x 18432 int4 + bf16 scales + h + norm
-weight + the 9216 bf16 activations it writes). It is timed with HIP events around a captured
-graph of the 32 layers' launches (so the weights stream from HBM, as in decode) on the stream
-the graph runs on. ``--roofline-only`` runs just that graph plus a plain 256 MiB device copy,
-for the ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` passes that calibrate HBM traffic.
+``roofline`` is for the dominant kernel. With the persistent engine that is the decode launch
+itself: achieved = the reference bytes model's weight + state + KV bytes per token
+(``harness/bytes_model.py``) x tokens per launch / launch time; traffic = the HBM bytes per
+launch from calibrated ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` passes
+(``PERSISTENT_TRAFFIC_BYTES_PER_TOKEN``). With the graph engine it is the fused RMSNorm +
+gate/up int4 GEMV + SwiGLU, timed around a captured graph of the 32 layers' launches;
+``--roofline-only`` runs just that graph plus a plain 256 MiB device copy for its PMC passes.
 ``cpu_baseline`` times the CPU oracle (``oracle/``, plain PyTorch, fp32 dequant as the
-reference does) on one decode step of the same model at the same context on the host cores.
+reference does) on decode steps of the same model at the same context on the host cores: the
+median of ``--cpu-steps`` steps, with the thread count and the CPU model.
 """
 
 from __future__ import annotations
@@ -42,6 +48,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--prompt-len", type=int, default=4096)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=3, help="CPU oracle decode steps timed (median reported)")
     ap.add_argument("--roofline-reps", type=int, default=10)
     ap.add_argument("--roofline-only", action="store_true")
     ap.add_argument("--calibration-copy", action="store_true",
@@ -67,9 +74,9 @@ GATE_UP_KERNEL = "w4_gemv_kernel<RMSNORM, SWIGLU> (post-attention norm + gate/up
 # WRITE_SIZE). Re-measure when the kernel changes.
 GATE_UP_TRAFFIC_BYTES = 12049 * 1024 * 2 + 18 * 1024
 # HBM bytes per decode token of the persistent kernel from the calibrated PMC passes over the
-# timed 256-token launch (332,334,028 KiB fetched x 1.9998, 17,707,377 KiB written, / 256),
+# timed 256-token launch (334,344,530.5 KiB fetched x 1.99982, 17,625,739.0 KiB written, / 256),
 # recorded with their commands in PERSISTENT_TRAFFIC_SOURCE. Re-measure when the kernel changes.
-PERSISTENT_TRAFFIC_BYTES_PER_TOKEN = 2729268486
+PERSISTENT_TRAFFIC_BYTES_PER_TOKEN = 2745024542
 PERSISTENT_TRAFFIC_SOURCE = ("profiles/decode_persistent_config5.md: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
                              "over bench.py --steps 256, scaled by a 256 MiB copy in the same process")
 
@@ -124,13 +131,33 @@ def copy_calibration(mib: int = 256) -> None:
     log(f"calibration copy: {mib} MiB read + {mib} MiB written per launch (3 launches)")
 
 
-def cpu_baseline(model, position: int) -> dict:
-    """One decode step of the CPU oracle at ``position`` (bounded sample of the same workload)."""
+def cpu_model_name() -> str:
+    """The host CPU's model name as ``lscpu`` prints it (``/proc/cpuinfo`` if lscpu is absent)."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        name = next((ln.split(":", 1)[1].strip() for ln in out.splitlines() if ln.startswith("Model name")), None)
+        if name:
+            return name
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            return next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "unknown CPU")
+    except OSError:
+        return "unknown CPU"
+
+
+def cpu_baseline(model, position: int, steps: int = 3) -> dict:
+    """``steps`` decode steps of the CPU oracle at ``position`` (a bounded sample of the same
+    workload), median reported. Threads are torch's default for this process (the box sets
+    ``OMP_NUM_THREADS``); the count reported is ``torch.get_num_threads()``."""
+    import statistics
+
     from oracle.int4 import dequantise_int4_k_major
     from oracle.model import OracleModel
 
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
     params = dict(model.params)
     head = model.linears["lm_head"]
     params["embed_tokens.weight"] = dequantise_int4_k_major(head.packed, head.scale, 128).to(torch.bfloat16).t().contiguous()
@@ -144,23 +171,20 @@ def cpu_baseline(model, position: int) -> dict:
     token = torch.tensor([[17]])
     times = []
     with torch.no_grad():
-        for _ in range(2):
+        for _ in range(max(steps, 3)):
             t0 = time.perf_counter()
             oracle.forward(token, cache, num_logits_to_keep=1)
             times.append(time.perf_counter() - t0)
             cache.seq_len = position
-    best = min(times)
-    cpu = "unknown CPU"
-    try:
-        with open("/proc/cpuinfo") as f:
-            cpu = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), cpu)
-    except OSError:
-        pass
-    return {"value": 1.0 / best, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"1 decode step (best of 2) of the same 32-layer int4 model at context {position}, "
-                      f"CPU oracle (plain PyTorch, fp32 dequant per linear), {threads} threads "
-                      f"(os.cpu_count() = {os.cpu_count()}) on {cpu}",
-            "seconds_per_token": best}
+    med = statistics.median(times)
+    threads = torch.get_num_threads()
+    cpu = cpu_model_name()
+    return {"value": 1.0 / med, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"median of {len(times)} decode steps (each {', '.join(f'{t:.2f}' for t in times)} s) of the "
+                      f"same 32-layer int4 model at context {position}, CPU oracle (plain PyTorch, fp32 dequant per "
+                      f"linear); torch.get_num_threads() = {threads} (os.cpu_count() = {os.cpu_count()}); "
+                      f"lscpu model name: {cpu}",
+            "threads": threads, "cpu_model": cpu, "seconds_per_token": med}
 
 
 def run_prefill(engine, model, args, persistent: bool) -> dict:
@@ -307,7 +331,7 @@ def main() -> int:
     baseline = None
     if not args.no_cpu_baseline:
         t0 = time.perf_counter()
-        baseline = cpu_baseline(model, args.prompt_len)
+        baseline = cpu_baseline(model, args.prompt_len, args.cpu_steps)
         log(f"cpu baseline: {baseline['seconds_per_token']:.2f} s/token on {baseline['cores']} threads "
             f"(sample took {time.perf_counter() - t0:.1f}s)")
         baseline.pop("seconds_per_token")

@@ -28,6 +28,10 @@ BF16 = torch.bfloat16
 XCD = 8
 LIN_COLS = 1552  # per XCD: q 256, k 256, v 512, z 512, a 4, b 4, 8 zero columns
 ATTN_COLS = 1536  # per XCD: 2 x (query 256 | gate 256), k 256, v 256
+#: Trace buffer layout of the traced build: the control wave's row, then 8 compute-wave rows.
+TRACE_CONTROL, TRACE_WAVE = 2048, 240
+TRACE_ROWS = 4096
+
 ERRORS = {1: "a cross-workgroup hand-off timed out", 2: "a workgroup ran on an unexpected XCD",
           3: "position, prompt or token log out of range", 4: "token id out of range",
           5: "control/compute barrier schedules disagree"}
@@ -226,13 +230,15 @@ class PersistentDecoder:
             m.trace, m.trace_step, m.trace_capacity = self._trace.data_ptr(), self._trace_step, self._trace.numel()
         return m
 
-    def trace_decode(self, steps: int, trace_step: int) -> list[int]:
-        """Greedy ``steps`` with the phase trace of step ``trace_step``: the s_memrealtime
-        (100 MHz) stamps workgroup (XCD 0, rank 0) takes at each phase's start, after its
-        hand-off, and at its signal. Only the traced build of the library stamps
+    def trace_decode(self, steps: int, trace_step: int) -> dict:
+        """Greedy ``steps`` with the phase trace of step ``trace_step`` from workgroup (XCD 0,
+        rank 0): ``{"control": [...], "waves": [[...] x 8]}``, each stamp s_memrealtime (100 MHz)
+        << 8 | tag. The control wave stamps each phase's start, its hand-off landing and its
+        signal (trace rows 0..2047); each compute wave stamps its GEMV consume and attention
+        split points in a row of 240 after them. Only the traced build of the library stamps
         (``python -m deltaforge_amd.build --trace``, loaded with ``lib=``); the product build
-        compiles the stamps out and returns an empty list."""
-        self._trace = torch.zeros(4096, dtype=torch.int64, device=self.device)
+        compiles the stamps out and returns empty lists. ``harness.phase_trace`` reads it."""
+        self._trace = torch.zeros(TRACE_ROWS, dtype=torch.int64, device=self.device)
         self._trace_step = trace_step
         try:
             self.decode(steps)
@@ -240,7 +246,10 @@ class PersistentDecoder:
         finally:
             stamps = self._trace.cpu().tolist()
             self._trace = None
-        return [t for t in stamps if t]
+        ctl = [t for t in stamps[:TRACE_CONTROL] if t]
+        waves = [[t for t in stamps[TRACE_CONTROL + TRACE_WAVE * w:TRACE_CONTROL + TRACE_WAVE * (w + 1)] if t]
+                 for w in range(8)]
+        return {"control": ctl, "waves": waves}
 
     def launch(self, steps: int, *, teacher_forced: bool) -> None:
         """Enqueue ``steps`` decode steps on the current stream (no host synchronisation)."""

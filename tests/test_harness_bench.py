@@ -118,3 +118,27 @@ def test_result_record_serialises_and_rejects_unknown_outcomes(tmp_path):
         ResultRecord(kind="ab", outcome="great", config_name="x")
     with pytest.raises(ValueError):
         ResultRecord(kind="other", outcome="win", config_name="x")
+
+
+def test_phase_trace_report_attributes_time_to_phases():
+    from deltaforge_amd.harness.phase_trace import layer_windows, phase_totals, decode_stamps, report
+
+    def st(us, tag):
+        return (int(round(us * 100)) << 8) | tag
+
+    ctl = [st(0, 10)]
+    t = 1.0
+    for layer in range(4):
+        kinds = ((1, 5), (4, 12), (6, 3), (11, 3), (7, 7), (8, 6), (11, 3)) if layer == 3 else \
+            ((1, 5), (2, 4), (3, 3), (11, 3), (7, 7), (8, 6), (11, 3))
+        for tag, d in kinds:
+            ctl.append(st(t, tag))
+            t += d
+    ctl.append(st(t, 9))
+    dec = decode_stamps(ctl)
+    totals = {n: (tot, c) for n, tot, c in phase_totals(dec)}
+    assert totals["reduce"] == (24.0, 8) and totals["attn"] == (12.0, 1) and totals["embed"] == (1.0, 1)
+    layers = layer_windows(dec)
+    assert [round(e - s, 2) for s, e, _ in layers] == [31.0, 31.0, 31.0, 39.0]
+    assert [a for _, _, a in layers] == [False, False, False, True]
+    assert "no stamps" in report({"control": [], "waves": [[]] * 8})
