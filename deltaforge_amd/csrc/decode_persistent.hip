@@ -872,6 +872,33 @@ DF_DEVICE void pair_read(int slot, const Ctx& c, const uint16_t* xg0, const uint
       : "memory");
 }
 
+// The two groups' input chunks of this lane's k slot alone (the pair_read layout): lanes 0,
+// 16, 32 and 48 read, the others keep stale values that only feed rows 1..15.
+DF_DEVICE void x_read(const uint16_t* xg0, const uint16_t* xg1, uint4 (&x0)[4], uint4 (&x1)[4]) {
+  const uint32_t xa0 = lds_addr(xg0), xa1 = lds_addr(xg1);
+  uint64_t saved;
+  asm volatile(
+      "s_mov_b64 %8, exec\n\t"
+      "s_mov_b32 exec_lo, 0x10001\n\t"
+      "s_mov_b32 exec_hi, 0x10001\n\t"
+      "s_nop 0\n\t"
+      "ds_read_b128 %0, %9\n\t"
+      "ds_read_b128 %1, %9 offset:16\n\t"
+      "ds_read_b128 %2, %9 offset:32\n\t"
+      "ds_read_b128 %3, %9 offset:48\n\t"
+      "ds_read_b128 %4, %10\n\t"
+      "ds_read_b128 %5, %10 offset:16\n\t"
+      "ds_read_b128 %6, %10 offset:32\n\t"
+      "ds_read_b128 %7, %10 offset:48\n\t"
+      "s_mov_b64 exec, %8\n\t"
+      "s_nop 0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x0[0]), "=&v"(x0[1]), "=&v"(x0[2]), "=&v"(x0[3]), "=&v"(x1[0]), "=&v"(x1[1]), "=&v"(x1[2]),
+        "=&v"(x1[3]), "=&s"(saved)
+      : "v"(xa0), "v"(xa1)
+      : "memory");
+}
+
 // Wait for the oldest pending block and read it.
 DF_DEVICE void take_block(Stream& st, const Ctx& c, uint4& wv, uint32_t& sd) {
   wait_oldest<1>(st);
@@ -887,22 +914,34 @@ DF_DEVICE void take_pair(Stream& st, const Ctx& c, const uint16_t* xg0, const ui
   st.rslot = next_slot(next_slot(st.rslot));
 }
 
-// Row 0 of one block's product: lanes 0..15 return sum_k x_k bf16((n_k - 8) s_col) over the
-// block's 128 k (x = the group's bf16 input chunks at this lane's k slot, sh = 16 * (lane & 1)
-// selects this lane's column scale in the dword). Each lane dequantises its own 32 weights
-// with dequant8, the reference's expression bit for bit, and the four bf16 MFMAs sum the
-// products in fp32.
-DF_DEVICE float block_dot_r(const uint4& wv, uint32_t sd, const uint4 (&x)[4], uint32_t sh) {
+// One block's B operands: this lane's 32 weights dequantised with dequant8, the reference's
+// bf16((n - 8) s) bit for bit (sh = 16 * (lane & 1) selects the lane's column scale in the
+// scale dword).
+DF_DEVICE void dequant_block(const uint4& wv, uint32_t sd, uint32_t sh, uint4 (&b)[4]) {
   const GroupScale gs = group_scale(static_cast<uint16_t>(sd >> sh));
-  const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+  b[0] = dequant8(wv.x, gs);
+  b[1] = dequant8(wv.y, gs);
+  b[2] = dequant8(wv.z, gs);
+  b[3] = dequant8(wv.w, gs);
+}
+
+// Row 0 of one block's product from its dequantised weights: lanes 0..15 return
+// sum_k x_k w_k over the block's 128 k (x = the group's bf16 input chunks at this lane's k
+// slot), the four bf16 MFMAs summing the products in fp32.
+DF_DEVICE float block_dot_b(const uint4 (&b)[4], const uint4 (&x)[4]) {
   df_f32x4 d4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const uint4 bw = dequant8(words[d], gs);
-    d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, x[d]), __builtin_bit_cast(df_bf16x8, bw),
+  for (int d = 0; d < 4; ++d)
+    d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, x[d]), __builtin_bit_cast(df_bf16x8, b[d]),
                                                  d4, 0, 0, 0);
-  }
   return d4[0];
+}
+
+// Both steps for a block whose weights were just read from the ring.
+DF_DEVICE float block_dot_r(const uint4& wv, uint32_t sd, const uint4 (&x)[4], uint32_t sh) {
+  uint4 b[4];
+  dequant_block(wv, sd, sh, b);
+  return block_dot_b(b, x);
 }
 
 // Single-block form reading its input from LDS.
@@ -916,8 +955,37 @@ DF_DEVICE float block_dot(const uint4& wv, uint32_t sd, const uint16_t* x, int l
 // Compute waves: consume this wave's blocks of GEMV phase g (input row g_xh); per-tile
 // partials of row 0 go to L.part[tile - first tile of the workgroup][wave].
 // Blocks are taken two at a time (two independent MFMA chains per iteration).
+// A phase's first block pair, taken from the ring and dequantised while the workgroup waited
+// for the phase's input (predequant), and whether it holds them.
+struct PreDq {
+  uint4 b0[4], b1[4];
+  bool ok;
+};
+
+// Compute waves, while the control wave runs a hand-off (the stream does not hold there): take
+// this wave's first two blocks of GEMV phase g from the ring, refill their slots and
+// dequantise them, so the phase starts at its MFMAs. Skipped when the wave has fewer than two
+// blocks in the phase or fewer than two are in flight.
+DF_DEVICE void predequant(const Gemv& g, const Ctx& c, Stream& st, int steps, PreDq& pre) {
+  int lo, n;
+  wave_range(g, c.wave, lo, n);
+  pre.ok = n >= 2 && st.issued - st.consumed >= 2;
+  if (!pre.ok) return;
+  wait_oldest<2>(st);
+  uint4 w0, w1;
+  uint32_t s0, s1;
+  ring_read1(st.rslot, c, w0, s0);
+  ring_read1(next_slot(st.rslot), c, w1, s1);
+  st.consumed += 2;
+  st.rslot = next_slot(next_slot(st.rslot));
+  refill2(st, steps, c);
+  const uint32_t sh = 16u * (c.lane & 1);
+  dequant_block(w0, s0, sh, pre.b0);
+  dequant_block(w1, s1, sh, pre.b1);
+}
+
 DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPersistModel& M, const Geo& q,
-                            int steps, Lds& L) {
+                            int steps, Lds& L, PreDq& pre) {
   stamp(const_cast<Ctx&>(c), kTConsume);
   int lo, n;
   wave_range(g, c.wave, lo, n);
@@ -939,6 +1007,17 @@ DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPer
   };
   const uint32_t sh = 16u * (c.lane & 1);
   int i = 0;
+  if (pre.ok) {  // the first two blocks, dequantised ahead (n >= 2)
+    const int gl1 = gl + 1 == g.ng ? 0 : gl + 1;
+    uint4 x0[4], x1[4];
+    x_read(xb + gl * kGroup, xb + gl1 * kGroup, x0, x1);
+    const float v0 = block_dot_b(pre.b0, x0);
+    const float v1 = block_dot_b(pre.b1, x1);
+    add(v0);
+    add(v1);
+    pre.ok = false;
+    i = 2;
+  }
 #pragma unroll 1
   for (; i + 1 < n; i += 2) {
     const int gl1 = gl + 1 == g.ng ? 0 : gl + 1;
@@ -1875,6 +1954,11 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
     fence(c);
     sync(c);  // embed
     if (!L.ok) return stop();
+    // a GEMV phase's first block pair, dequantised while the control wave runs the hand-off
+    // before it (after out_proj / o_proj for gate|up, after gate|up for down, after down for the
+    // next input projection, after the delta step for out_proj)
+    PreDq pre;
+    pre.ok = false;
     for (int li = 0; li < M.num_layers; ++li) {
       LayerPtr Lp = layer_at(M, li);
       const int kind = LKIND(Lp);
@@ -1882,7 +1966,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         fence(c);
         const Gemv g = gemv_of(Lp, q, 0, c.xcd, c.r);
         norm_w(L, c, hidden, M.eps);
-        gemv_consume(g, c, st, M, q, steps, L);
+        gemv_consume(g, c, st, M, q, steps, L, pre);
         sync(c);
       }
       if (kind == 0) {
@@ -1898,7 +1982,8 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         {  // gated norm + out_proj
           fence(c);
           const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
-            sync(c);
+          predequant(g, c, st, steps, pre);
+          sync(c);
           if (!L.ok) return stop();
           // GatedRMSNorm: wave h < 4 takes head h whole (elements 128 h + lane and + 64), so
           // no partial crosses waves; each sum is the two 64-lane halves added in order
@@ -1915,8 +2000,9 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
             g_xh[i1] = f2bf(xv1);
           }
           sync(c);
-          gemv_consume(g, c, st, M, q, steps, L);
+          gemv_consume(g, c, st, M, q, steps, L, pre);
           sync(c);
+          predequant(gemv_of(Lp, q, 2, c.xcd, c.r), c, st, steps, pre);
           sync(c);  // all-reduce done, h in LDS
           if (!L.ok) return stop();
         }
@@ -2011,8 +2097,9 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
             const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
               sync(c);
             if (!L.ok) return stop();
-            gemv_consume(g, c, st, M, q, steps, L);
+            gemv_consume(g, c, st, M, q, steps, L, pre);
             sync(c);
+            predequant(gemv_of(Lp, q, 2, c.xcd, c.r), c, st, steps, pre);
             sync(c);  // all-reduce done
             if (!L.ok) return stop();
           }
@@ -2094,8 +2181,9 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
             const Gemv g = gemv_of(Lp, q, 1, c.xcd, c.r);
               sync(c);
             if (!L.ok) return stop();
-            gemv_consume(g, c, st, M, q, steps, L);
+            gemv_consume(g, c, st, M, q, steps, L, pre);
             sync(c);
+            predequant(gemv_of(Lp, q, 2, c.xcd, c.r), c, st, steps, pre);
             sync(c);  // all-reduce done
             if (!L.ok) return stop();
           }
@@ -2105,17 +2193,19 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         fence(c);
         const Gemv g = gemv_of(Lp, q, 2, c.xcd, c.r);
         norm_w(L, c, hidden, M.eps);
-        gemv_consume(g, c, st, M, q, steps, L);
+        gemv_consume(g, c, st, M, q, steps, L, pre);
         sync(c);
       }
       {  // down
         fence(c);
         const Gemv g = gemv_of(Lp, q, 3, c.xcd, c.r);
+        predequant(g, c, st, steps, pre);
         sync(c);
         if (!L.ok) return stop();
         swiglu_act(L, c, q.inter_x);
-        gemv_consume(g, c, st, M, q, steps, L);
+        gemv_consume(g, c, st, M, q, steps, L, pre);
         sync(c);
+        if (li + 1 < M.num_layers) predequant(gemv_of(layer_at(M, li + 1), q, 0, c.xcd, c.r), c, st, steps, pre);
         sync(c);  // all-reduce done
         if (!L.ok) return stop();
       }
