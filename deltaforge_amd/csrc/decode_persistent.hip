@@ -914,15 +914,40 @@ DF_DEVICE void take_pair(Stream& st, const Ctx& c, const uint16_t* xg0, const ui
   st.rslot = next_slot(next_slot(st.rslot));
 }
 
-// One block's B operands: this lane's 32 weights dequantised with dequant8, the reference's
-// bf16((n - 8) s) bit for bit (sh = 16 * (lane & 1) selects the lane's column scale in the
-// scale dword).
-DF_DEVICE void dequant_block(const uint4& wv, uint32_t sd, uint32_t sh, uint4 (&b)[4]) {
-  const GroupScale gs = group_scale(static_cast<uint16_t>(sd >> sh));
-  b[0] = dequant8(wv.x, gs);
-  b[1] = dequant8(wv.y, gs);
-  b[2] = dequant8(wv.z, gs);
-  b[3] = dequant8(wv.w, gs);
+// One block's B operands: this lane's 32 weights as the reference's bf16((n - 8) s), bit for
+// bit, in 17 VALU per 8 weights. One shift and four and-or put each nibble in the mantissa of
+// an fp16 with exponent 2^10: 1024 + n (nibbles at bits 0..3 of a half) or 1024 + 16 n (bits
+// 4..7). v_fma_mix_f32 widens that fp16 exactly and forms (1024 + n) s - 1032 s, or
+// (1024 + 16 n) (s / 16) - 72 s, in one rounding of an exact value that fp32 holds: (n - 8) s
+// exactly (s has 8 significant bits, the constants at most 15); v_cvt_pk_bf16_f32 then
+// rounds each pair to nearest-even, as dequant8 (int4_block.h) does. sh = 16 * (lane & 1)
+// selects the lane's column scale in the scale dword.
+struct DqK {
+  uint32_t mlo, mhi, bias;
+};
+// Made once per loop, outside it: opaque to the compiler, so they stay in registers.
+DF_DEVICE DqK dq_consts() {
+  DqK k{0x000F000Fu, 0x00F000F0u, 0x64006400u};
+  asm volatile("" : "+v"(k.mlo), "+v"(k.mhi), "+v"(k.bias));
+  return k;
+}
+typedef _Float16 df_f16x2 __attribute__((ext_vector_type(2)));
+DF_DEVICE void dequant_block(const uint4& wv, uint32_t sd, uint32_t sh, const DqK& K, uint4 (&b)[4]) {
+  const float s = bf2f(static_cast<uint16_t>(sd >> sh));
+  const float c1 = -1032.0f * s, s16 = s * 0.0625f, c16 = -72.0f * s;
+  const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t w = words[d], t = w >> 8;
+    const df_f16x2 h0 = __builtin_bit_cast(df_f16x2, (w & K.mlo) | K.bias);  // k % 8 = 0, 1
+    const df_f16x2 h1 = __builtin_bit_cast(df_f16x2, (w & K.mhi) | K.bias);  // 2, 3
+    const df_f16x2 h2 = __builtin_bit_cast(df_f16x2, (t & K.mlo) | K.bias);  // 4, 5
+    const df_f16x2 h3 = __builtin_bit_cast(df_f16x2, (t & K.mhi) | K.bias);  // 6, 7
+    b[d] = make_uint4(pack_bf16(__builtin_fmaf(static_cast<float>(h0.x), s, c1), __builtin_fmaf(static_cast<float>(h0.y), s, c1)),
+                      pack_bf16(__builtin_fmaf(static_cast<float>(h1.x), s16, c16), __builtin_fmaf(static_cast<float>(h1.y), s16, c16)),
+                      pack_bf16(__builtin_fmaf(static_cast<float>(h2.x), s, c1), __builtin_fmaf(static_cast<float>(h2.y), s, c1)),
+                      pack_bf16(__builtin_fmaf(static_cast<float>(h3.x), s16, c16), __builtin_fmaf(static_cast<float>(h3.y), s16, c16)));
+  }
 }
 
 // Row 0 of one block's product from its dequantised weights: lanes 0..15 return
@@ -938,9 +963,9 @@ DF_DEVICE float block_dot_b(const uint4 (&b)[4], const uint4 (&x)[4]) {
 }
 
 // Both steps for a block whose weights were just read from the ring.
-DF_DEVICE float block_dot_r(const uint4& wv, uint32_t sd, const uint4 (&x)[4], uint32_t sh) {
+DF_DEVICE float block_dot_r(const uint4& wv, uint32_t sd, const uint4 (&x)[4], uint32_t sh, const DqK& K) {
   uint4 b[4];
-  dequant_block(wv, sd, sh, b);
+  dequant_block(wv, sd, sh, K, b);
   return block_dot_b(b, x);
 }
 
@@ -949,7 +974,7 @@ DF_DEVICE float block_dot(const uint4& wv, uint32_t sd, const uint16_t* x, int l
   uint4 xv[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) xv[d] = *reinterpret_cast<const uint4*>(x + d * 8);
-  return block_dot_r(wv, sd, xv, 16u * (lane & 1));
+  return block_dot_r(wv, sd, xv, 16u * (lane & 1), dq_consts());
 }
 
 // Compute waves: consume this wave's blocks of GEMV phase g (input row g_xh); per-tile
@@ -980,8 +1005,9 @@ DF_DEVICE void predequant(const Gemv& g, const Ctx& c, Stream& st, int steps, Pr
   st.rslot = next_slot(next_slot(st.rslot));
   refill2(st, steps, c);
   const uint32_t sh = 16u * (c.lane & 1);
-  dequant_block(w0, s0, sh, pre.b0);
-  dequant_block(w1, s1, sh, pre.b1);
+  const DqK K = dq_consts();
+  dequant_block(w0, s0, sh, K, pre.b0);
+  dequant_block(w1, s1, sh, K, pre.b1);
 }
 
 DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPersistModel& M, const Geo& q,
@@ -1006,6 +1032,7 @@ DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPer
     }
   };
   const uint32_t sh = 16u * (c.lane & 1);
+  const DqK K = dq_consts();
   int i = 0;
   if (pre.ok) {  // the first two blocks, dequantised ahead (n >= 2)
     const int gl1 = gl + 1 == g.ng ? 0 : gl + 1;
@@ -1023,8 +1050,8 @@ DF_DEVICE void gemv_consume(const Gemv& g, const Ctx& c, Stream& st, const DfPer
     const int gl1 = gl + 1 == g.ng ? 0 : gl + 1;
     PairIn in;
     take_pair(st, c, xb + gl * kGroup, xb + gl1 * kGroup, in);
-    const float v0 = block_dot_r(in.w0, in.s0, in.x0, sh);
-    const float v1 = block_dot_r(in.w1, in.s1, in.x1, sh);
+    const float v0 = block_dot_r(in.w0, in.s0, in.x0, sh, K);
+    const float v1 = block_dot_r(in.w1, in.s1, in.x1, sh, K);
     refill2(st, steps, c);
     add(v0);
     add(v1);
@@ -2218,6 +2245,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       const int t0 = head_tile(q, c.wave), ntw = head_tile(q, c.wave + 1) - t0;
       const uint16_t* xb = g_xh + (c.lane >> 4) * 32;
       const uint32_t sh = 16u * (c.lane & 1);
+      const DqK K = dq_consts();
       float bv = -INFINITY;
       int bi = 0x7FFFFFFF;
       float acc = 0.0f;
@@ -2227,8 +2255,8 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       for (int i = 0; i < ntw * G; i += 2) {
         PairIn in;
         take_pair(st, c, xb + gl * kGroup, xb + (gl + 1) * kGroup, in);
-        const float v0 = block_dot_r(in.w0, in.s0, in.x0, sh);
-        const float v1 = block_dot_r(in.w1, in.s1, in.x1, sh);
+        const float v0 = block_dot_r(in.w0, in.s0, in.x0, sh, K);
+        const float v1 = block_dot_r(in.w1, in.s1, in.x1, sh, K);
         refill2(st, steps, c);
         acc += v0;
         acc += v1;
