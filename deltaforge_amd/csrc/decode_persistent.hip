@@ -914,40 +914,15 @@ DF_DEVICE void take_pair(Stream& st, const Ctx& c, const uint16_t* xg0, const ui
   st.rslot = next_slot(next_slot(st.rslot));
 }
 
-// One block's B operands: this lane's 32 weights as the reference's bf16((n - 8) s), bit for
-// bit, in 17 VALU per 8 weights. One shift and four and-or put each nibble in the mantissa of
-// an fp16 with exponent 2^10: 1024 + n (nibbles at bits 0..3 of a half) or 1024 + 16 n (bits
-// 4..7). v_fma_mix_f32 widens that fp16 exactly and forms (1024 + n) s - 1032 s, or
-// (1024 + 16 n) (s / 16) - 72 s, in one rounding of an exact value that fp32 holds: (n - 8) s
-// exactly (s has 8 significant bits, the constants at most 15); v_cvt_pk_bf16_f32 then
-// rounds each pair to nearest-even, as dequant8 (int4_block.h) does. sh = 16 * (lane & 1)
-// selects the lane's column scale in the scale dword.
-struct DqK {
-  uint32_t mlo, mhi, bias;
-};
-// Made once per loop, outside it: opaque to the compiler, so they stay in registers.
-DF_DEVICE DqK dq_consts() {
-  DqK k{0x000F000Fu, 0x00F000F0u, 0x64006400u};
-  asm volatile("" : "+v"(k.mlo), "+v"(k.mhi), "+v"(k.bias));
-  return k;
-}
-typedef _Float16 df_f16x2 __attribute__((ext_vector_type(2)));
+// One block's B operands: this lane's 32 weights dequantised with dequant8 (int4_block.h), the
+// reference's bf16((n - 8) s) bit for bit (sh = 16 * (lane & 1) selects the lane's column scale
+// in the scale dword).
 DF_DEVICE void dequant_block(const uint4& wv, uint32_t sd, uint32_t sh, const DqK& K, uint4 (&b)[4]) {
-  const float s = bf2f(static_cast<uint16_t>(sd >> sh));
-  const float c1 = -1032.0f * s, s16 = s * 0.0625f, c16 = -72.0f * s;
-  const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const uint32_t w = words[d], t = w >> 8;
-    const df_f16x2 h0 = __builtin_bit_cast(df_f16x2, (w & K.mlo) | K.bias);  // k % 8 = 0, 1
-    const df_f16x2 h1 = __builtin_bit_cast(df_f16x2, (w & K.mhi) | K.bias);  // 2, 3
-    const df_f16x2 h2 = __builtin_bit_cast(df_f16x2, (t & K.mlo) | K.bias);  // 4, 5
-    const df_f16x2 h3 = __builtin_bit_cast(df_f16x2, (t & K.mhi) | K.bias);  // 6, 7
-    b[d] = make_uint4(pack_bf16(__builtin_fmaf(static_cast<float>(h0.x), s, c1), __builtin_fmaf(static_cast<float>(h0.y), s, c1)),
-                      pack_bf16(__builtin_fmaf(static_cast<float>(h1.x), s16, c16), __builtin_fmaf(static_cast<float>(h1.y), s16, c16)),
-                      pack_bf16(__builtin_fmaf(static_cast<float>(h2.x), s, c1), __builtin_fmaf(static_cast<float>(h2.y), s, c1)),
-                      pack_bf16(__builtin_fmaf(static_cast<float>(h3.x), s16, c16), __builtin_fmaf(static_cast<float>(h3.y), s16, c16)));
-  }
+  const GroupScale gs = group_scale(static_cast<uint16_t>(sd >> sh));
+  b[0] = dequant8(wv.x, gs, K);
+  b[1] = dequant8(wv.y, gs, K);
+  b[2] = dequant8(wv.z, gs, K);
+  b[3] = dequant8(wv.w, gs, K);
 }
 
 // Row 0 of one block's product from its dequantised weights: lanes 0..15 return

@@ -26,45 +26,50 @@ DF_DEVICE uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, df_bf16x2));
 }
 
-// Per-group dequant constants: 512 * scale and -8 * scale (both exact in fp32).
+// Per-group dequant constants (all exact in fp32: the scale has 8 significant bits, 1032 and
+// 72 two set bits each): the scale, -1032 s, s / 16 and -72 s.
 struct GroupScale {
-  float s512, neg8s;
+  float s, c1, s16, c16;
 };
 
 DF_DEVICE GroupScale group_scale(uint16_t sbits) {
   const float s = bf2f(sbits);
-  return GroupScale{512.0f * s, -8.0f * s};
+  return GroupScale{s, -1032.0f * s, 0.0625f * s, -72.0f * s};
 }
 
-// w & 0x0F0F0F0F as one opaque instruction, so the byte conversions below stay
-// v_cvt_f32_ubyte{0..3} of the masked word instead of one bit-field extract per nibble.
-// (Only plain ALU ops go through inline asm: the compiler cannot see the issue latency of an
-// instruction it only knows as text, so anything whose result needs wait states stays in C.)
-DF_DEVICE uint32_t low_nibbles(uint32_t w) {
-  uint32_t r;
-  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(w));
-  return r;
+// The unpack's masks and fp16 exponent: made once per loop, outside it, and opaque to the
+// compiler, so they stay in registers and each unpack is one v_and_or_b32.
+struct DqK {
+  uint32_t mlo, mhi, bias;
+};
+DF_DEVICE DqK dq_consts() {
+  DqK k{0x000F000Fu, 0x00F000F0u, 0x64006400u};
+  asm volatile("" : "+v"(k.mlo), "+v"(k.mhi), "+v"(k.bias));
+  return k;
 }
 
-// One dword of 8 nibbles -> 8 bf16 weights (4 packed pairs, k order e = 0..7).
-// A byte holding a nibble n (0..15) is the OCP E4M3 encoding of n * 2^-9 (subnormal for
-// n < 8, exponent field 1 for n >= 8, linear across the boundary), so v_cvt_pk_f32_fp8 turns
-// two nibbles into two exact floats per instruction; fma(n 2^-9, 512 s, -8 s) = (n - 8) s
-// exactly (at most 12 significant bits) and v_cvt_pk_bf16_f32 rounds each pair to
-// nearest-even bf16: the reference's bf16((nibble - 8) * scale). 19 VALU ops per 8 weights.
-DF_DEVICE uint4 dequant8(uint32_t w, const GroupScale& gs) {
-  const uint32_t lo = low_nibbles(w);       // bytes: e0, e4, e1, e5
-  const uint32_t hi = low_nibbles(w >> 4);  // bytes: e2, e6, e3, e7
-  const df_f32x2 f04 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(lo), false);
-  const df_f32x2 f15 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(lo), true);
-  const df_f32x2 f26 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(hi), false);
-  const df_f32x2 f37 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(hi), true);
-  const float s = gs.s512, c = gs.neg8s;
-  const float e0 = __builtin_fmaf(f04.x, s, c), e4 = __builtin_fmaf(f04.y, s, c);
-  const float e1 = __builtin_fmaf(f15.x, s, c), e5 = __builtin_fmaf(f15.y, s, c);
-  const float e2 = __builtin_fmaf(f26.x, s, c), e6 = __builtin_fmaf(f26.y, s, c);
-  const float e3 = __builtin_fmaf(f37.x, s, c), e7 = __builtin_fmaf(f37.y, s, c);
-  return make_uint4(pack_bf16(e0, e1), pack_bf16(e2, e3), pack_bf16(e4, e5), pack_bf16(e6, e7));
+typedef _Float16 df_f16x2 __attribute__((ext_vector_type(2)));
+
+// One dword of 8 nibbles -> 8 bf16 weights (4 packed pairs, k order e = 0..7), the reference's
+// bf16((nibble - 8) * scale) bit for bit, 17 VALU ops per 8 weights:
+//   - one shift and four and-or put each nibble in the mantissa of an fp16 with exponent 2^10:
+//     1024 + n for the nibbles at bits 0..3 of a half (e = 0, 1, 4, 5), 1024 + 16 n for those
+//     at bits 4..7 (e = 2, 3, 6, 7);
+//   - v_fma_mix_f32 widens each fp16 exactly and forms (1024 + n) s - 1032 s, or
+//     (1024 + 16 n) (s / 16) - 72 s, with one rounding of an exact value fp32 holds: (n - 8) s
+//     exactly (at most 12 significant bits);
+//   - v_cvt_pk_bf16_f32 rounds each pair to nearest-even bf16.
+DF_DEVICE uint4 dequant8(uint32_t w, const GroupScale& gs, const DqK& K) {
+  const uint32_t t = w >> 8;
+  const df_f16x2 h0 = __builtin_bit_cast(df_f16x2, (w & K.mlo) | K.bias);  // e0, e1
+  const df_f16x2 h1 = __builtin_bit_cast(df_f16x2, (w & K.mhi) | K.bias);  // e2, e3
+  const df_f16x2 h2 = __builtin_bit_cast(df_f16x2, (t & K.mlo) | K.bias);  // e4, e5
+  const df_f16x2 h3 = __builtin_bit_cast(df_f16x2, (t & K.mhi) | K.bias);  // e6, e7
+  const float s = gs.s, c1 = gs.c1, s16 = gs.s16, c16 = gs.c16;
+  return make_uint4(pack_bf16(__builtin_fmaf(static_cast<float>(h0.x), s, c1), __builtin_fmaf(static_cast<float>(h0.y), s, c1)),
+                    pack_bf16(__builtin_fmaf(static_cast<float>(h1.x), s16, c16), __builtin_fmaf(static_cast<float>(h1.y), s16, c16)),
+                    pack_bf16(__builtin_fmaf(static_cast<float>(h2.x), s, c1), __builtin_fmaf(static_cast<float>(h2.y), s, c1)),
+                    pack_bf16(__builtin_fmaf(static_cast<float>(h3.x), s16, c16), __builtin_fmaf(static_cast<float>(h3.y), s16, c16)));
 }
 
 }  // namespace df

@@ -318,13 +318,14 @@ __global__ __launch_bounds__(kThreads) void w4_gemv_kernel(DfInt4GemvArgs p) {
   const int slot = lane >> 4;  // K slot of A and B; C row block
   const uint16_t* xrow = xs + min(col, p.rows) * L.xs_ld + slot * 32;  // absent rows read zeros
   df_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const DqK K = dq_consts();
 
   auto group_mac = [&](const uint4 wv, const uint16_t sraw, const int g) {
     const GroupScale gs = group_scale(sraw);
     const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      const uint4 bw = dequant8(words[d], gs);
+      const uint4 bw = dequant8(words[d], gs, K);
       const uint4 aw = *reinterpret_cast<const uint4*>(xrow + g * kGroup + d * 8);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, aw),
                                                     __builtin_bit_cast(df_bf16x8, bw), acc, 0, 0, 0);
@@ -439,7 +440,7 @@ __global__ void w4_dequant_kernel(const uint32_t* __restrict__ wt, const uint16_
   const size_t tg = idx >> 8;
   const int g = tg % G, t = tg / G;
   const int s = lane >> 4, c = lane & 15, n = t * kTileCols + c;
-  const uint4 q = dequant8(wt[idx], group_scale(st[tg * kTileCols + c]));
+  const uint4 q = dequant8(wt[idx], group_scale(st[tg * kTileCols + c]), dq_consts());
   const uint32_t pairs[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
   for (int e = 0; e < 8; ++e) {

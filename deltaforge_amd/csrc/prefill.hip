@@ -95,6 +95,7 @@ __global__ __launch_bounds__(256, 2) void int4_gemm_kernel(DfInt4GemmArgs p) {
   load_w(0);
   store_x(0);
   if (G > 1) load_x(1);
+  const DqK K = dq_consts();
   for (int g = 0; g < G; ++g) {
     // xs[g & 1] is complete, and every wave is done with xs[(g + 1) & 1] (group g - 1)
     __syncthreads();
@@ -102,10 +103,10 @@ __global__ __launch_bounds__(256, 2) void int4_gemm_kernel(DfInt4GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const GroupScale gs = group_scale(sr[j]);  // the exact bf16((n - 8) * scale) of the per-op GEMV
-      b[j][0] = dequant8(wr[j].x, gs);
-      b[j][1] = dequant8(wr[j].y, gs);
-      b[j][2] = dequant8(wr[j].z, gs);
-      b[j][3] = dequant8(wr[j].w, gs);
+      b[j][0] = dequant8(wr[j].x, gs, K);
+      b[j][1] = dequant8(wr[j].y, gs, K);
+      b[j][2] = dequant8(wr[j].z, gs, K);
+      b[j][3] = dequant8(wr[j].w, gs, K);
     }
     if (g + 1 < G) {
       store_x((g + 1) & 1);
