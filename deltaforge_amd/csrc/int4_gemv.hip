@@ -498,15 +498,36 @@ int df_int4_gemv_plan(int rows, int K, int N, int epilogue, int target_waves, in
   // Widest workgroup (most tiles, least K splitting) that divides the tiles and still
   // reaches the wave target; SwiGLU pairs a gate tile with an up tile, so at least 2.
   const int min_nt = epilogue == DF_EPI_SWIGLU ? 2 : 1;
-  int nt = 8;
-  while (nt > min_nt && (tiles % nt || (tiles / nt) * kWaves < target_waves)) nt /= 2;
   // A workgroup's LDS (the activation rows of its K range, partial sums) must fit kGemvLds of
   // gfx950's 160 KB: 16 rows of K = 2560 fit, so that shape needs no K split, partials or
   // reduce launch.
-  int gps = G;
-  while (gps > 1 && gemv_smem(rows, gps * kGroup, nt).total > kGemvLds) --gps;
-  int ks = (G + gps - 1) / gps;
-  gps = (G + ks - 1) / ks;
+  auto split_for = [&](int nt_, int& gps_, int& ks_) {
+    gps_ = G;
+    while (gps_ > 1 && gemv_smem(rows, gps_ * kGroup, nt_).total > kGemvLds) --gps_;
+    ks_ = (G + gps_ - 1) / gps_;
+    gps_ = (G + ks_ - 1) / ks_;
+  };
+  int nt = 8;
+  while (nt > min_nt && (tiles % nt || (tiles / nt) * kWaves < target_waves)) nt /= 2;
+  if (rows > 4) {
+    // Many rows: every workgroup stages all rows of its K range, so fewer, wider workgroups
+    // stage them fewer times. Take the most workgroups up to one per CU (measured best at 8
+    // and 16 rows: gate|up 2560 x 18432 in 144 workgroups of 8 tiles, 17.7 against 23.9 us at
+    // 16 rows and 16.2 against 20.3 us at 8 rows with 288 of 4; down 9216 x 2560 in 160
+    // workgroups, 13.8 against 20.7 us at 16 rows (4 tiles x 4 K splits, not 1 tile) and 14.0
+    // against 16.1 us at 8 rows (2 tiles x 2 splits)).
+    int best = 0, best_wgs = 0;
+    for (int c = 8; c >= min_nt; c /= 2) {
+      if (tiles % c) continue;
+      int gps_, ks_;
+      split_for(c, gps_, ks_);
+      const int wgs = (tiles / c) * ks_;
+      if (wgs <= 256 && wgs > best_wgs) best = c, best_wgs = wgs;
+    }
+    if (best) nt = best;
+  }
+  int gps, ks;
+  split_for(nt, gps, ks);
   *tiles_per_workgroup = nt;
   *ksplit = ks;
   *groups_per_split = gps;
