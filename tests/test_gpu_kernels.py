@@ -68,6 +68,45 @@ def test_int4_gemv_matches_champion_expression(rows, k, n):
     close(got, dequant_gemv(x, w.packed, w.scale, 128), what=f"gemv {rows}x{k}x{n}")
 
 
+@pytest.mark.parametrize("epilogue", [N.EPI_STORE, N.EPI_RESIDUAL, N.EPI_SWIGLU])
+def test_int4_gemv_k_split_reuses_its_workspace(epilogue):
+    """A K split across workgroups (the last split of a column block sums the partials):
+    three calls in a row on one zero-filled workspace, different inputs and row counts, each
+    against the expression; the counters are back at zero after every call, and a repeat of
+    the first call is bit-identical."""
+    gen = torch.Generator().manual_seed(31 + epilogue)
+    k, n = 4608, 256
+    w = synth.draw_int4(gen, k, n)
+    weight = repack(w)
+    plans = [ops.GemvPlan(2, 6, 6, int(N.lib().df_int4_gemv_workspace_bytes(16, n, 6))),
+             ops.GemvPlan(4, 3, 12, int(N.lib().df_int4_gemv_workspace_bytes(16, n, 3)))]
+    ws = torch.zeros(max(p.workspace_bytes for p in plans), dtype=torch.uint8, device=DEV)
+    firsts = []
+    for rows, plan in ((16, plans[0]), (5, plans[1]), (1, plans[0])):
+        x = torch.randn((rows, k), generator=gen).to(torch.bfloat16)
+        res = torch.randn((rows, n), generator=gen).to(torch.bfloat16)
+        print(f"[k-split] epilogue {epilogue} rows {rows} ksplit {plan.ksplit}", flush=True)
+        got = ops.int4_gemv(x.to(DEV), weight, epilogue=epilogue, plan=plan, ws=ws,
+                            res=res.to(DEV) if epilogue == N.EPI_RESIDUAL else None)
+        y = dequant_gemv(x, w.packed, w.scale, 128)
+        if epilogue == N.EPI_RESIDUAL:
+            want = (res.float() + y.float()).to(torch.bfloat16)
+        elif epilogue == N.EPI_SWIGLU:  # 16-column gate / up tiles alternate
+            yf = y.float().reshape(rows, n // 32, 2, 16)
+            g, u = yf[:, :, 0].to(torch.bfloat16).float(), yf[:, :, 1].to(torch.bfloat16).float()
+            want = (torch.nn.functional.silu(g).to(torch.bfloat16).float() * u).to(torch.bfloat16).reshape(rows, n // 2)
+        else:
+            want = y
+        close(got, want, what=f"k-split gemv epilogue {epilogue} rows {rows}",
+              flip_frac=2e-3 if epilogue == N.EPI_SWIGLU else 0.0)
+        assert int(ws[: (n // 16) * 4].count_nonzero()) == 0, "completion counters left non-zero"
+        firsts.append((x, got.clone(), res))
+    x0, got0, res0 = firsts[0]
+    again = ops.int4_gemv(x0.to(DEV), weight, epilogue=epilogue, plan=plans[0], ws=ws,
+                          res=res0.to(DEV) if epilogue == N.EPI_RESIDUAL else None)
+    assert torch.equal(again, got0)
+
+
 def test_int4_gemv_is_deterministic_across_runs():
     gen = torch.Generator().manual_seed(5)
     w = synth.draw_int4(gen, 9216, 2560)
