@@ -301,7 +301,7 @@ struct Lds {
       __align__(16) uint16_t qn_w[kHd];
       __align__(16) uint16_t kn_w[kHd];
       uint32_t rope[kRot / 2];                   // this position's RoPE row (cos | sin << 16)
-      float sc[kPairHeads][kTileKeys];
+      float sc[kPairHeads][kTileKeys + kCompute];  // + the waves' extra keys (at_ext)
       float alpha[kPairHeads];
       float ml[kPairHeads][2];
       __align__(16) float red[kPairHeads][kHd];  // the split's PV sums (the per-wave partials
@@ -1615,6 +1615,7 @@ DF_DEVICE void norm_rope4_lds(float x[4], const uint16_t* nw, float eps, const u
 
 struct AtPre {
   uint4 kb[8];   // K rows: this lane's key (t0 + 16 wave + col), dims d*32 + slot*8 ..+7
+  uint2 ke;      // the wave's extra key t0 + 128 + wave (at_ext), K dims 4 lane ..+3
 };
 // A tile's K and V rows, loaded together (the per-XCD key split).
 struct AtPreKV {
@@ -1633,7 +1634,8 @@ DF_DEVICE void at_keys(const Ctx& c, int& j0, int& j1) {
 // Whether the tile at t0 is the split's last and runs past 128 keys by at most one key per
 // wave: wave w then takes key t0 + 128 + w besides its 16 (a lane-parallel dot product and
 // one more PV term) instead of a second, near-empty tile. A split of 4097..4352 keys over 32
-// workgroups (129..136 keys each) is one tile so.
+// workgroups (129..136 keys each) is one tile so, and one of 32769..33280 keys over the 64
+// workgroups of an XCD pair (513..520 each) four tiles instead of five.
 __host__ __device__ inline bool at_ext(int t0, int j1) {
   return j1 - t0 > kTileKeys && j1 - t0 <= kTileKeys + kCompute;
 }
@@ -1665,6 +1667,9 @@ DF_DEVICE void at_issue_k(const Ctx& c, LayerPtr Lp, int t0, int j1, AtPre& P) {
 #pragma unroll
     for (int d = 0; d < 8; ++d) P.kb[d] = gload16(kp + d * 32);
   }
+  const int ek = t0 + kTileKeys + c.wave;
+  P.ke = make_uint2(0u, 0u);
+  if (at_ext(t0, j1) && ek < j1 && ek != c.pos) P.ke = gload8((GlobalBf16)LF(Lp, k_cache) + (base + ek) * kHd + c.lane * 4);
 }
 
 // Compute waves: the K and V rows of one 128-key tile (not the new position's, which the tile
@@ -1878,8 +1883,30 @@ DF_DEVICE void at_tile4(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, flo
         if (h < nh) A.sc[h][c.wave * 16 + col] = live ? d4[h] * scale : -INFINITY;
     }
   }
-  // V rows: keys t0 + 16 wave + j, dims 4 lane ..+3
-  uint2 vb[16];
+  const bool ext = at_ext(t0, j1);
+  const int ek = t0 + kTileKeys + c.wave;
+  if (ext) {  // this wave's extra key: q . k over the 64 lanes' 4 dims each, per head
+    uint2 kr = P.ke;
+    if (ek == c.pos) kr = *reinterpret_cast<const uint2*>(A.knew + c.lane * 4);
+    const float k4[4] = {__uint_as_float(kr.x << 16), __uint_as_float(kr.x & 0xFFFF0000u),
+                         __uint_as_float(kr.y << 16), __uint_as_float(kr.y & 0xFFFF0000u)};
+#pragma unroll
+    for (int h = 0; h < kPairHeads; ++h) {
+      if (h >= nh) break;
+      float se = -INFINITY;
+      if (ek < j1) {
+        const uint2 qr = *reinterpret_cast<const uint2*>(&A.q[h][c.lane * 4]);
+        float p = __uint_as_float(qr.x << 16) * k4[0];
+        p += __uint_as_float(qr.x & 0xFFFF0000u) * k4[1];
+        p += __uint_as_float(qr.y << 16) * k4[2];
+        p += __uint_as_float(qr.y & 0xFFFF0000u) * k4[3];
+        se = dsum(p) * scale;
+      }
+      if (c.lane == 0) A.sc[h][kTileKeys + c.wave] = se;
+    }
+  }
+  // V rows: keys t0 + 16 wave + j, dims 4 lane ..+3 (and the extra key's)
+  uint2 vb[16], ve = make_uint2(0u, 0u);
   {
     const size_t base = (size_t)(c.xcd >> 1) * c.max_len;
     GlobalBf16 vc = (GlobalBf16)LF(Lp, v_cache);
@@ -1889,23 +1916,27 @@ DF_DEVICE void at_tile4(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, flo
       vb[jj] = make_uint2(0u, 0u);
       if (kk < j1 && kk != c.pos) vb[jj] = gload8(vc + (base + kk) * kHd + c.lane * 4);
     }
+    if (ext && ek < j1 && ek != c.pos) ve = gload8(vc + (base + ek) * kHd + c.lane * 4);
   }
   sync(c);
   if (c.wave < nh) {
     const int h = c.wave;
     const float s0 = A.sc[h][c.lane], s1 = A.sc[h][c.lane + 64];
-    const float tmax = dmax(fmaxf(s0, s1));
+    const float s2 = ext && c.lane < kCompute ? A.sc[h][kTileKeys + c.lane] : -INFINITY;
+    const float tmax = dmax(fmaxf(fmaxf(s0, s1), s2));
     const float mo = A.ml[h][0];
     const float m_new = fmaxf(mo, tmax);
-    float p0 = 0.f, p1 = 0.f, alpha = 1.0f;
+    float p0 = 0.f, p1 = 0.f, p2 = 0.f, alpha = 1.0f;
     if (m_new != -INFINITY) {
       p0 = s0 == -INFINITY ? 0.0f : expf(s0 - m_new);
       p1 = s1 == -INFINITY ? 0.0f : expf(s1 - m_new);
+      p2 = s2 == -INFINITY ? 0.0f : expf(s2 - m_new);
       alpha = mo == -INFINITY ? 0.0f : expf(mo - m_new);
     }
-    const float lsum = dsum(p0 + p1);
+    const float lsum = dsum((p0 + p1) + p2);
     A.sc[h][c.lane] = p0;
     A.sc[h][c.lane + 64] = p1;
+    if (ext && c.lane < kCompute) A.sc[h][kTileKeys + c.lane] = p2;
     if (c.lane == 0) {
       A.ml[h][0] = m_new;
       A.ml[h][1] = A.ml[h][1] * alpha + lsum;
@@ -1940,6 +1971,20 @@ DF_DEVICE void at_tile4(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPre& P, flo
           acc[h][2] += pr * v2;
           acc[h][3] += pr * v3;
         }
+      }
+    }
+    if (ext && ek < j1) {
+      const uint2 raw = ek == c.pos ? vn : ve;
+      const float v0 = __uint_as_float(raw.x << 16), v1 = __uint_as_float(raw.x & 0xFFFF0000u);
+      const float v2 = __uint_as_float(raw.y << 16), v3 = __uint_as_float(raw.y & 0xFFFF0000u);
+#pragma unroll
+      for (int h = 0; h < kPairHeads; ++h) {
+        if (h >= nh) break;
+        const float pr = A.sc[h][kTileKeys + c.wave];
+        acc[h][0] += pr * v0;
+        acc[h][1] += pr * v1;
+        acc[h][2] += pr * v2;
+        acc[h][3] += pr * v3;
       }
     }
   }
@@ -2113,6 +2158,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
             AtPre P;
             at_issue_k(c, Lp, t0, j1, P);
             at_tile4(c, Lp, t0, j1, P, acc, nh, L);
+            if (at_ext(t0, j1)) break;  // its extra keys were the split's last
           }
           // the split's KV loads are consumed (wait unconditionally: the compiler cannot pair
           // the first tile's prefetch with the loop, and the held stream has nothing in flight)
@@ -2487,8 +2533,10 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           sync(c);  // q/k normed and roped
           int j0, j1;
           at_keys4(c, j0, j1);
-          for (int t0 = j0; t0 < j1; t0 += kTileKeys)
+          for (int t0 = j0; t0 < j1; t0 += kTileKeys) {
             for (int i = 0; i < kTileBars; ++i) sync(c);
+            if (at_ext(t0, j1)) break;  // the compute waves' last tile took the extra keys
+          }
           sync(c);
           sync(c);  // PV partials summed into A.red
           c.epoch += 1;

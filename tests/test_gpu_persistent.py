@@ -88,12 +88,14 @@ def test_persistent_state_matches_engine(mid):
         assert int(dec.position.item()) == n
 
 
-@pytest.mark.parametrize("n", [4200, 12400])
+@pytest.mark.parametrize("n", [4200, 12400, 16440])
 def test_persistent_long_context_attention_matches_engine(n):
-    """Attention at 4 200 keys, where each workgroup's split (132 keys) spans two 128-key tiles
-    and each XCD merges 32 splits per head, and at 12 400 keys, past the length where the keys
-    are split over the XCD pair instead (64 splits of 194 keys serving all four query heads of
-    a KV head, merged across XCDs): an attention-only stack, persistent vs the per-op engine
+    """Attention at 4 200 keys, where each workgroup's split (132 keys) is one 128-key tile plus
+    one extra key per wave and each XCD merges 32 splits per head; at 12 400 keys, past the
+    length where the keys are split over the XCD pair instead (64 splits of 194 keys serving all
+    four query heads of a KV head, merged across XCDs); and at 16 440 keys, where a pair split
+    (257 keys) is two tiles plus an extra key. The prefill steps through every shorter context
+    (two-tile and extra-key splits of both kinds). An attention-only stack, persistent vs the per-op engine
     (whose split-KV attention kernel is checked against the oracle up to 131 072 keys; the CPU
     oracle itself would take minutes here). K/V caches within 3 % normwise, logits after the
     prefill and after one more step (its new key written inside a two-tile split) within a
