@@ -23,9 +23,8 @@
 // differs from the reference.
 //
 // When even that leaves too few waves, the K range is also split across workgroups
-// (blockIdx.y); those write fp32 partials, and the last split of each column block to
-// arrive (a completion counter in the workspace) sums them in split order and runs the
-// epilogue. The sum's order is fixed, so results are bit-identical run to run.
+// (blockIdx.y); those write fp32 partials and a second kernel sums them in split order and
+// runs the epilogue. Nothing uses atomics, so results are bit-identical run to run.
 #include "common.h"
 #include "deltaforge_hip.h"
 #include "int4_block.h"
@@ -44,15 +43,6 @@ struct GemvSmem {
   int xs_ld;  // bf16 elements per LDS row of x
   int ybuf_off, red_off, total;
 };
-
-// A K split's workspace: one completion counter per 16-column tile in a fixed area at its
-// start (so calls of other shapes sharing the workspace never write partials over a
-// counter), then the fp32 partials [ksplit][rows][N].
-constexpr int kCounterTiles = 16384;  // N <= 262144 when the K range is split
-constexpr size_t kCounterBytes = kCounterTiles * sizeof(int);
-DF_DEVICE int* gemv_counters(const DfInt4GemvArgs& p) {
-  return reinterpret_cast<int*>(reinterpret_cast<char*>(p.part) - kCounterBytes);
-}
 
 // LDS holds the activation rows plus, when rows < 16, one zero row that the MFMA lanes of
 // absent rows read (so the inner loop has no divergent branch).
@@ -377,33 +367,36 @@ __global__ __launch_bounds__(kThreads) void w4_gemv_kernel(DfInt4GemvArgs p) {
   const int col0 = blockIdx.x * COLS;
   if (gridDim.y == 1) {
     gemv_epilogue<EPI>(p, ybuf, col0, COLS);
-    return;
+  } else {
+    for (int e = threadIdx.x; e < p.rows * COLS; e += kThreads) {
+      const int m = e / COLS, c = e % COLS;
+      p.part[((size_t)blockIdx.y * p.rows + m) * p.N + col0 + c] = ybuf[e];
+    }
   }
-  // K split: this workgroup's partials go out write-through; the last of the column block's
-  // splits to arrive sums all of them in split order and runs the epilogue (deterministic:
-  // the order does not depend on which split arrives last), then clears the counter.
-  for (int e = threadIdx.x; e < p.rows * COLS; e += kThreads) {
-    const int m = e / COLS, c = e % COLS;
-    store_through(&p.part[((size_t)blockIdx.y * p.rows + m) * p.N + col0 + c], ybuf[e]);
-  }
-  publish_wait();
-  int* counter = gemv_counters(p) + blockIdx.x;
-  __syncthreads();
-  int* last = reinterpret_cast<int*>(red);
-  if (threadIdx.x == 0) *last = arrive(counter) == (int)gridDim.y - 1;
-  __syncthreads();
-  if (!*last) return;
-  const size_t stride = (size_t)p.rows * p.N;
-  for (int e = threadIdx.x; e < p.rows * COLS; e += kThreads) {
-    const int m = e / COLS, c = e % COLS;
+}
+
+// Sum of the cross-workgroup K splits (in split order) + the epilogue. 64 columns per block.
+template <int EPI>
+__global__ __launch_bounds__(256) void w4_reduce_kernel(DfInt4GemvArgs p) {
+  __shared__ float y[kMaxRows * 64];
+  const int col0 = blockIdx.x * 64;
+  for (int e = threadIdx.x; e < p.rows * 64; e += 256) {
+    const int m = e / 64, c = e % 64;
     const float* src = p.part + (size_t)m * p.N + col0 + c;
-    float v = 0.0f;
-    for (int s = 0; s < (int)gridDim.y; ++s) v += load_through(src + s * stride);
-    ybuf[e] = v;
+    const size_t stride = (size_t)p.rows * p.N;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    int s = 0;
+    for (; s + 4 <= p.ksplit; s += 4) {
+      const float a0 = src[(s + 0) * stride], a1 = src[(s + 1) * stride];
+      const float a2 = src[(s + 2) * stride], a3 = src[(s + 3) * stride];
+      v[0] = ((v[0] + a0) + a1) + a2;
+      v[0] = v[0] + a3;
+    }
+    for (; s < p.ksplit; ++s) v[0] += src[s * stride];
+    y[e] = v[0];
   }
   __syncthreads();
-  gemv_epilogue<EPI>(p, ybuf, col0, COLS);
-  if (threadIdx.x == 0) *counter = 0;
+  gemv_epilogue<EPI>(p, y, col0, 64);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -468,7 +461,9 @@ static hipError_t launch_gemv(const DfInt4GemvArgs& a, hipStream_t stream) {
   else
     hipLaunchKernelGGL((w4_gemv_kernel<PRO, EPI, NT, false>), grid, dim3(kThreads), L.total, stream, a);
   hipError_t e = hipGetLastError();
-  return e;
+  if (e != hipSuccess || a.ksplit == 1) return e;
+  hipLaunchKernelGGL((w4_reduce_kernel<EPI>), dim3(a.N / 64), dim3(256), 0, stream, a);
+  return hipGetLastError();
 }
 
 template <int PRO, int EPI>
@@ -489,7 +484,7 @@ using namespace df;
 extern "C" {
 
 size_t df_int4_gemv_workspace_bytes(int rows, int N, int ksplit) {
-  return ksplit > 1 ? kCounterBytes + (size_t)ksplit * rows * N * sizeof(float) : 0;
+  return ksplit > 1 ? (size_t)ksplit * rows * N * sizeof(float) : 0;
 }
 
 int df_int4_gemv_plan(int rows, int K, int N, int epilogue, int target_waves, int* tiles_per_workgroup,
@@ -571,10 +566,9 @@ int df_int4_gemv(const DfInt4GemvArgs* args, void* workspace, size_t workspace_b
     return DF_BAD_ARGUMENT;
   if (a.h_out && reinterpret_cast<uintptr_t>(a.h_out) % 16) return DF_BAD_ARGUMENT;
   if (a.ksplit > 1) {
-    if (a.N / kTileCols > kCounterTiles) return DF_BAD_ARGUMENT;
     if (!workspace || workspace_bytes < df_int4_gemv_workspace_bytes(a.rows, a.N, a.ksplit))
       return DF_WORKSPACE_TOO_SMALL;
-    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+    a.part = reinterpret_cast<float*>(workspace);
   }
   hipError_t e = hipErrorInvalidValue;
 #define DF_GEMV_CASE(PRO, EPI) \

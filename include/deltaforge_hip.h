@@ -67,11 +67,8 @@ size_t df_int4_gemv_workspace_bytes(int rows, int N, int ksplit);
  * Replaces torch_dequant_gemv_int4 (kernels/visible_int4_head.py:187-199) and
  * tiled_gemv_int4 (kernels/tiled_gemv.py:915-953); with DF_PRO_ADD_RMSNORM it is the
  * tied head with its final residual + RMSNorm (reference.py:735, 810, 764-777).
- * With ksplit > 1 (N <= 262144) the workspace holds a 64 KB area of completion counters
- * (one per 16-column tile) and then the fp32 partials: the last split of a column block to
- * arrive sums the partials in split order and runs the epilogue, so results are
- * deterministic. The workspace must be zero-filled before its first use; every call leaves
- * its counters at zero, whatever its shape. Calls sharing a workspace must not overlap. */
+ * With ksplit > 1 a second kernel sums the fp32 partials held in the workspace;
+ * calls sharing a workspace must not overlap. No atomics: results are deterministic. */
 int df_int4_gemv(const DfInt4GemvArgs* args, void* workspace, size_t workspace_bytes,
                  hipStream_t stream);
 

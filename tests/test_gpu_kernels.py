@@ -70,10 +70,10 @@ def test_int4_gemv_matches_champion_expression(rows, k, n):
 
 @pytest.mark.parametrize("epilogue", [N.EPI_STORE, N.EPI_RESIDUAL, N.EPI_SWIGLU])
 def test_int4_gemv_k_split_reuses_its_workspace(epilogue):
-    """A K split across workgroups (the last split of a column block sums the partials):
-    three calls in a row on one zero-filled workspace, different inputs and row counts, each
-    against the expression; the counters are back at zero after every call, and a repeat of
-    the first call is bit-identical."""
+    """A K split across workgroups (partials in the workspace, summed in split order by the
+    reduce kernel, which runs the epilogue): three calls in a row on one workspace, different
+    inputs, row counts and split counts, each against the expression; a repeat of the first
+    call is bit-identical."""
     gen = torch.Generator().manual_seed(31 + epilogue)
     k, n = 4608, 256
     w = synth.draw_int4(gen, k, n)
@@ -99,7 +99,6 @@ def test_int4_gemv_k_split_reuses_its_workspace(epilogue):
             want = y
         close(got, want, what=f"k-split gemv epilogue {epilogue} rows {rows}",
               flip_frac=2e-3 if epilogue == N.EPI_SWIGLU else 0.0)
-        assert int(ws[: (n // 16) * 4].count_nonzero()) == 0, "completion counters left non-zero"
         firsts.append((x, got.clone(), res))
     x0, got0, res0 = firsts[0]
     again = ops.int4_gemv(x0.to(DEV), weight, epilogue=epilogue, plan=plans[0], ws=ws,
