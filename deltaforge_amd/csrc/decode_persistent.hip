@@ -381,8 +381,8 @@ enum Tag : int { kTProj = 1, kTDelta, kTOut, kTAttn, kTMerge, kTOProj, kTGateUp,
                  kTReduce, kTStaged = 20, kTSignal = 30,
                  // finer points: control wave (delta step, all-reduce, down's hand-off)
                  kTDnLanded = 21, kTDnState = 22, kTDnDone = 23, kTArLanded = 31, kTArLocal = 32, kTGuLanded = 34,
-                 // compute waves (their own trace rows): GEMV consume, attention split
-                 kTConsume = 40, kTConsumed = 42, kTAtStaged = 60, kTAtRoped = 61, kTAtQk = 62, kTAtSoftmax = 63,
+                 // compute waves (their own trace rows): GEMV consume, delta step, attention split
+                 kTConsume = 40, kTConsumed = 42, kTDnIn = 43, kTDnConv = 44, kTDnMath = 45, kTAtStaged = 60, kTAtRoped = 61, kTAtQk = 62, kTAtSoftmax = 63,
                  kTAtPv = 64, kTAtDone = 65 };
 // Compiled in only with DF_TRACE defined (a separate build of the library): the stamps' code sits
 // between the phases of every token, in the instruction cache the decode depends on.
@@ -2077,9 +2077,12 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         {  // the Gated DeltaNet step's arithmetic (dn_conv, dn_math); the control wave stages it
           sync(c);  // inputs in LDS
           if (!L.ok) return stop();
+          stamp(c, kTDnIn);
           dn_conv(c, L);
           sync(c);
+          stamp(c, kTDnConv);
           dn_math(c, L);
+          stamp(c, kTDnMath);
           sync(c);
           static_assert(kDnBars == 3, "the control wave passes the same barriers");
         }
