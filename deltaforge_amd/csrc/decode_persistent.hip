@@ -2377,6 +2377,12 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
 // The control wave's whole launch.
 template <bool TABLE, bool PAIR>
 DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int steps, int teacher_forced, Lds& L) {
+  // The control wave shares SIMD 0 with compute waves 0 and 4, which dequantise a phase's
+  // first blocks (predequant) while it runs the hand-off: at equal priority its epilogue,
+  // polls and staging got about a third of that SIMD's issue slots. It issues little
+  // (polls sleep between tries), so letting it win the arbitration costs the compute waves
+  // little and shortens the serial chain (1.4 % per token, same-box A/B).
+  __builtin_amdgcn_s_setprio(3);
   const int hidden = M.hidden;
   const int G = q.Gh;
   const int pos0 = *M.position;
