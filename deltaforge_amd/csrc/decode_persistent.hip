@@ -268,6 +268,7 @@ struct Lds {
       float core[16];                            // the unit's 16 outputs
       float ab8[8];                              // a of the XCD's 4 value heads, then b
       float gp[2];                               // A_log, dt_bias of the unit's value head
+      float gates[2];                            // beta, exp(g) (dn_conv's spare lane)
     } dn;
     struct {                                     // attention split
       __align__(16) uint16_t q[2][kHd];
@@ -1434,9 +1435,9 @@ DF_DEVICE void dn_state_prefetch(const Ctx& c, LayerPtr Lp, Lds& L) {
 // at out_proj's first barrier otherwise) carry the arithmetic:
 //   dn_stage    control wave: the in_proj hand-off (q, k of the key head, the unit's 16 v, a/b,
 //               the XCD's z) and the unit's conv taps and history into LDS;     | barrier
-//   dn_conv     compute waves: the 4-tap conv + SiLU of the 272 channels, 34 per wave;
-//                                                                                | barrier
-//   dn_math     compute waves: q/k L2 norms and the gates (each wave, identically), then wave w
+//   dn_conv     compute waves: the 4-tap conv + SiLU of the 272 channels, 34 per wave, and
+//               the gates on a spare lane;                                       | barrier
+//   dn_math     compute waves: q/k L2 norms (each wave, identically), then wave w
 //               runs the delta rule on value columns 2 w, 2 w + 1 over all 128 state rows (two
 //               rows per lane), so each column's recall and output are one wave's sums; the
 //               updated slice goes back to the LDS copy, the outputs to LDS;   | barrier
@@ -1493,7 +1494,8 @@ DF_DEVICE bool dn_stage(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_in) {
 
 // Compute waves: conv + SiLU (fp32 sum in tap order, bf16, SiLU, bf16) of channels
 // 34 w .. 34 w + 33. History slots (pos+1)&3, (pos+2)&3, (pos+3)&3 hold positions pos-3, pos-2,
-// pos-1 (slot pos&3 is written by dn_publish).
+// pos-1 (slot pos&3 is written by dn_publish). The last wave's spare lane 63 computes the unit's
+// gates, beta = bf16(sigmoid(b)) and exp(g) = exp(-exp(A_log) softplus(a + dt_bias)), for dn_math.
 DF_DEVICE void dn_conv(const Ctx& c, Lds& L) {
 #pragma clang fp contract(off)
   auto& D = L.u.dn;
@@ -1511,6 +1513,11 @@ DF_DEVICE void dn_conv(const Ctx& c, Lds& L) {
     acc = acc + h2 * w2;
     acc = acc + D.qkv_in[ch] * w3;
     D.y[ch] = round_bf(silu(round_bf(acc)));
+  } else if (c.wave == kCompute - 1 && c.lane == 63) {  // a spare lane: the unit's gates
+    const int hvl = c.r >> 3;
+    const float a = D.ab8[hvl], b = D.ab8[4 + hvl];
+    D.gates[0] = round_bf(sigmoid(b));
+    D.gates[1] = expf(-expf(D.gp[0]) * softplus(a + D.gp[1]));
   }
 }
 
@@ -1520,7 +1527,6 @@ DF_DEVICE void dn_conv(const Ctx& c, Lds& L) {
 DF_DEVICE void dn_math(const Ctx& c, Lds& L) {
 #pragma clang fp contract(off)
   auto& D = L.u.dn;
-  const int hvl = c.r >> 3;
   // L2 norms of q (then scaled by dk^-1/2) and k, in every wave alike
   const float q0 = D.y[c.lane], q1 = D.y[c.lane + 64];
   const float k0 = D.y[kDk + c.lane], k1 = D.y[kDk + c.lane + 64];
@@ -1529,10 +1535,9 @@ DF_DEVICE void dn_math(const Ctx& c, Lds& L) {
   const float scale = sqrtf(static_cast<float>(kDk));
   const float qn0 = (q0 * rq) / scale, qn1 = (q1 * rq) / scale;
   const float kn0 = k0 * rk, kn1 = k1 * rk;
-  // gates
-  const float a = D.ab8[hvl], b = D.ab8[4 + hvl];
-  const float beta = round_bf(sigmoid(b));
-  const float eg = expf(-expf(D.gp[0]) * softplus(a + D.gp[1]));
+  // gates (dn_conv's spare lane computed them, off the reductions' path)
+  const float beta = D.gates[0];
+  const float eg = D.gates[1];
   // this wave's two columns of rows lane and lane + 64
   const int c0 = 2 * c.wave;
   float* s0 = reinterpret_cast<float*>(&D.S[c.lane / 16][(c.lane % 16) * 4 + c0 / 4]) + (c0 % 4);
