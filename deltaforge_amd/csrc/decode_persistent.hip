@@ -382,6 +382,7 @@ enum Tag : int { kTProj = 1, kTDelta, kTOut, kTAttn, kTMerge, kTOProj, kTGateUp,
                  kTReduce, kTStaged = 20, kTSignal = 30,
                  // finer points: control wave (delta step, all-reduce, down's hand-off)
                  kTDnLanded = 21, kTDnState = 22, kTDnDone = 23, kTArLanded = 31, kTArLocal = 32, kTGuLanded = 34,
+                 kTHeadConsumed = 35, kTHeadDone = 36,
                  // compute waves (their own trace rows): GEMV consume, delta step, attention split
                  kTConsume = 40, kTConsumed = 42, kTDnIn = 43, kTDnConv = 44, kTDnMath = 45, kTAtStaged = 60, kTAtRoped = 61, kTAtQk = 62, kTAtSoftmax = 63,
                  kTAtPv = 64, kTAtDone = 65 };
@@ -2790,6 +2791,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
       // final_norm is in L.nw (its DMA preceded the last all-reduce's polls)
       for (int i = 0; i < kNormBars; ++i) sync(c);
       sync(c);  // head blocks consumed, per-wave candidates in LDS
+      stamp(c, kTHeadConsumed);
       c.epoch += 1;
       // logits out (this workgroup's columns, 32 B per tile)
       if (M.logits) {
@@ -2852,6 +2854,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         raise_abort(c, kErrSchedule);
         ok = false;
       }
+      stamp(c, kTHeadDone);
       if (c.lane == 0) L.ok = ok;
       sync(c);
       if (!ok) return;

@@ -20,9 +20,9 @@ import collections
 PHASES = {1: "proj", 2: "delta", 3: "out", 4: "attn", 5: "merge", 6: "oproj", 7: "gateup", 8: "down", 9: "head",
           10: "embed", 11: "reduce"}
 POINTS = {20: "staged", 30: "signal", 21: "dn-landed", 22: "dn-state", 23: "dn-done", 31: "ar-landed",
-          32: "ar-local", 34: "gu-landed", 40: "consume", 42: "consumed", 43: "dn-in", 44: "dn-conv",
-          45: "dn-math", 60: "at-staged", 61: "at-roped", 62: "at-qk", 63: "at-softmax", 64: "at-pv",
-          65: "at-done"}
+          32: "ar-local", 34: "gu-landed", 35: "head-consumed", 36: "head-done", 40: "consume", 42: "consumed",
+          43: "dn-in", 44: "dn-conv", 45: "dn-math", 60: "at-staged", 61: "at-roped", 62: "at-qk",
+          63: "at-softmax", 64: "at-pv", 65: "at-done"}
 
 
 def decode_stamps(stamps: list[int]) -> list[tuple[float, str]]:
@@ -58,6 +58,10 @@ def report(trace: dict) -> str:
         return "no stamps: load the traced build (python -m deltaforge_amd.build --trace)"
     base = ctl[0][0]
     lines = [f"traced step: {ctl[-1][0] - base:.1f} us from the embedding to the head's last stamp"]
+    marks = {n: t for t, n in ctl if n in ("head", "head-consumed", "head-done")}
+    if len(marks) == 3:
+        lines.append(f"head: {marks['head-consumed'] - marks['head']:.1f} us of GEMV (this workgroup's tiles), "
+                     f"{marks['head-done'] - marks['head-consumed']:.1f} us to the argmax over all workgroups")
     lines.append("")
     lines.append("| phase (start to next start) | total us | count | per phase us | share |")
     lines.append("|---|---:|---:|---:|---:|")
