@@ -597,11 +597,10 @@ DF_DEVICE int head_tile(const Geo& q, int wave) {
 //
 // Run descriptor: w = weights of the first block | (blocks << 48), s = its scales | hold << 63
 // (hold: the stream stops before this run until the attention layer's KV-cache loads are
-// consumed, because they share the wave's in-order vmcnt). With the keys split per XCD the
-// hold is the first run after an attention layer's input projection (o_proj's). With the keys
-// split over the XCD pair it is a zero-block marker run of its own right after the input
-// projection: the split's PV partials then borrow the ring, which must be drained there for
-// every wave, and a flag carried by the next real run would leave a wave with no blocks
+// consumed, because they share the wave's in-order vmcnt). The hold is a zero-block marker run
+// of its own right after each attention layer's input projection: the attention borrows the
+// ring there (the per-XCD split's K rows, the pair split's PV partials), so it must be drained
+// for every wave, and a flag carried by the next real run would leave a wave with no blocks
 // between two attention layers' input projections with its ring full at the second.
 struct RunDesc {
   uint64_t w, s;
@@ -637,34 +636,29 @@ DF_DEVICE int build_runs(const DfPersistModel& M, const Geo& q, const Ctx& c) {
                                   reinterpret_cast<uint64_t>(sc) | (hold ? 1ull << 63 : 0ull)};
     n += 1;
   };
-  bool hold = false;  // pending until the next run (a wave with no o_proj blocks holds at gate|up)
   for (int li = 0; li < M.num_layers; ++li) {
     const int kind = LKIND(&g_layers[li]) & 1;
     for (int k = 0; k < 4; ++k) {
       const Gemv g = gemv_of(&g_layers[li], q, k, c.xcd, c.r);
       int lo, cnt;
       wave_range(g, c.wave, lo, cnt);
-      if constexpr (!PAIR) hold = hold || (kind == 1 && k == 1);
       // blocks lo .. lo + cnt of the slice (tile-major, ng groups per tile): a tile's run is
       // contiguous, and so are consecutive tiles when the slice spans every group
       while (cnt > 0) {
         const int t = lo / g.ng, gi = lo % g.ng;
         const int len = g.ng == g.G ? cnt : min(cnt, g.ng - gi);
         const size_t blk = (size_t)(g.tile0 + t) * g.G + g.g0 + gi;
-        put(g.w + blk * kBlockBytes, g.s + blk * kTileCols, len, hold);
-        hold = false;
+        put(g.w + blk * kBlockBytes, g.s + blk * kTileCols, len, false);
         lo += len;
         cnt -= len;
       }
-      if constexpr (PAIR) {
-        if (kind == 1 && k == 0) put(nullptr, nullptr, 0, true);
-      }
+      if (kind == 1 && k == 0) put(nullptr, nullptr, 0, true);
     }
   }
   const int t0 = head_tile(q, c.wave), ntw = head_tile(q, c.wave + 1) - t0;
   if (ntw > 0) {  // consecutive tiles are contiguous (tile-major, Gh groups per tile)
     const size_t blk = (size_t)t0 * q.Gh;
-    put(M.head_w + blk * kBlockBytes, M.head_s + blk * kTileCols, ntw * q.Gh, hold);
+    put(M.head_w + blk * kBlockBytes, M.head_s + blk * kTileCols, ntw * q.Gh, false);
   }
   // Every geometry the launcher accepts fits: per layer at most 1 run each for the
   // column-parallel phases and 2 for each row-parallel one (a wave's share of out_proj /
@@ -1623,9 +1617,8 @@ struct AtPre {
   uint4 kb[8];   // K rows: this lane's key (t0 + 16 wave + col), dims d*32 + slot*8 ..+7
   uint2 ke;      // the wave's extra key t0 + 128 + wave (at_ext), K dims 4 lane ..+3
 };
-// A tile's K and V rows, loaded together (the per-XCD key split).
+// A tile's V rows in registers (the per-XCD key split; its K rows come by DMA into the ring).
 struct AtPreKV {
-  uint4 kb[8];   // as AtPre
   uint2 vb[16];  // V rows: keys t0 + 16 wave + j, dims 4 lane ..+3
   uint2 ke, ve;  // the wave's extra key t0 + 128 + wave (at_ext), K and V dims 4 lane ..+3
 };
@@ -1678,35 +1671,37 @@ DF_DEVICE void at_issue_k(const Ctx& c, LayerPtr Lp, int t0, int j1, AtPre& P) {
   if (at_ext(t0, j1) && ek < j1 && ek != c.pos) P.ke = gload8((GlobalBf16)LF(Lp, k_cache) + (base + ek) * kHd + c.lane * 4);
 }
 
-// Compute waves: the K and V rows of one 128-key tile (not the new position's, which the tile
-// takes from LDS), issued together so the tile waits one memory round trip instead of two.
-DF_DEVICE void at_issue_kv(const Ctx& c, LayerPtr Lp, int t0, int j1, AtPreKV& P) {
+// Compute waves: the K rows of one 128-key tile by LDS DMA into the wave's weight ring, which
+// is idle through the attention (the stream holds at the marker run after the input projection
+// with every block consumed), so they go out before the q/k staging without holding registers.
+// Chunk d (16 bytes) of this lane's key lands in ring slot d at the lane's position: the QK
+// reads of one d are one contiguous 1 KB. Rows past the split clamp into it (the tile ignores
+// them; the new position's row is taken from LDS).
+constexpr int kAtVLoads = 18;  // vector loads at_issue_v issues after the K DMAs
+static_assert(kRing >= 8, "a wave's ring holds its 16 keys' K rows (8 KB)");
+DF_DEVICE void at_dma_k(const Ctx& c, LayerPtr Lp, int t0, int j1) {
   const int col = c.lane & 15, slot = c.lane >> 4;
   const size_t base = (size_t)(c.xcd >> 1) * c.max_len;
-  const int key = t0 + c.wave * 16 + col;
-  // defined on every path: a conditionally-set register array is a value the compiler carries
-  // around the whole layer loop (spilled across every other phase)
+  const int key = min(t0 + c.wave * 16 + col, j1 - 1);
+  const uint16_t* kp = LF(Lp, k_cache) + (base + key) * kHd + slot * 8;
 #pragma unroll
-  for (int d = 0; d < 8; ++d) P.kb[d] = make_uint4(0u, 0u, 0u, 0u);
-  if (key < j1 && key != c.pos) {
-    GlobalBf16 kp = (GlobalBf16)LF(Lp, k_cache) + (base + key) * kHd + slot * 8;
-#pragma unroll
-    for (int d = 0; d < 8; ++d) P.kb[d] = gload16(kp + d * 32);
-  }
+  for (int d = 0; d < 8; ++d) dma16(kp + d * 32, lds_addr(&g_ring_w[c.wave][d][0]));
+}
+
+// Compute waves: the V rows of one 128-key tile and the wave's extra key's K and V rows
+// (at_ext): kAtVLoads loads on every path (rows clamp into the split), so a wait for the older
+// K DMAs can count them.
+DF_DEVICE void at_issue_v(const Ctx& c, LayerPtr Lp, int t0, int j1, AtPreKV& P) {
+  const size_t base = (size_t)(c.xcd >> 1) * c.max_len;
   GlobalBf16 vc = (GlobalBf16)LF(Lp, v_cache);
 #pragma unroll
   for (int jj = 0; jj < 16; ++jj) {
-    const int kk = t0 + c.wave * 16 + jj;
-    P.vb[jj] = make_uint2(0u, 0u);
-    if (kk < j1 && kk != c.pos) P.vb[jj] = gload8(vc + (base + kk) * kHd + c.lane * 4);
+    const int kk = min(t0 + c.wave * 16 + jj, j1 - 1);
+    P.vb[jj] = gload8(vc + (base + kk) * kHd + c.lane * 4);
   }
-  const int ek = t0 + kTileKeys + c.wave;
-  P.ke = make_uint2(0u, 0u);
-  P.ve = make_uint2(0u, 0u);
-  if (at_ext(t0, j1) && ek < j1 && ek != c.pos) {
-    P.ke = gload8((GlobalBf16)LF(Lp, k_cache) + (base + ek) * kHd + c.lane * 4);
-    P.ve = gload8(vc + (base + ek) * kHd + c.lane * 4);
-  }
+  const int ek = min(t0 + kTileKeys + c.wave, j1 - 1);
+  P.ke = gload8((GlobalBf16)LF(Lp, k_cache) + (base + ek) * kHd + c.lane * 4);
+  P.ve = gload8(vc + (base + ek) * kHd + c.lane * 4);
 }
 
 // Compute waves (kTileBars barriers): one 128-key tile whose K and V rows are in flight in P
@@ -1717,6 +1712,9 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPreKV& P, fl
   auto& A = L.u.at;
   const int col = c.lane & 15, slot = c.lane >> 4;
   const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
+  asm volatile("" ::: "memory");  // at_issue_v's loads stay ahead of the wait
+  wait_vm<kAtVLoads>();           // the tile's K DMAs (older than at_issue_v's loads)
+  asm volatile("" ::: "memory");
   {
     const int key = t0 + c.wave * 16 + col;
     const bool live = key < j1;
@@ -1724,9 +1722,9 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPreKV& P, fl
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       uint4 kn = *reinterpret_cast<const uint4*>(A.knew + d * 32 + slot * 8);
-      asm volatile("" : "+v"(kn.x), "+v"(kn.y), "+v"(kn.z), "+v"(kn.w));  // a value, not a pointer select into P
+      asm volatile("" : "+v"(kn.x), "+v"(kn.y), "+v"(kn.z), "+v"(kn.w));  // a value, not a pointer select into the ring
       uint4 bw = make_uint4(0u, 0u, 0u, 0u);
-      if (live) bw = key == c.pos ? kn : P.kb[d];
+      if (live) bw = key == c.pos ? kn : g_ring_w[c.wave][d][c.lane];
       uint4 aw = make_uint4(0u, 0u, 0u, 0u);
       if (col < 2) aw = *reinterpret_cast<const uint4*>(&A.q[col][d * 32 + slot * 8]);
       d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, aw), __builtin_bit_cast(df_bf16x8, bw),
@@ -2222,6 +2220,7 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           int j0, j1;
           at_keys(c, j0, j1);
           auto& A = L.u.at;
+          if (j0 < j1) at_dma_k(c, Lp, j0, j1);  // the first tile's K rows, ahead of the staging
           sync(c);  // q/k/v staged
           if (!L.ok) return stop();
           stamp(c, kTAtStaged);
@@ -2252,11 +2251,12 @@ DF_DEVICE void compute_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           }
           float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
           for (int t0 = j0; t0 < j1; t0 += kTileKeys) {
-            // K and V rows are loaded here, in straight-line code with their use (loads held
-            // across the staging code raise the register pressure of the whole kernel, which then
-            // spills around the GEMV phases)
+            // V rows are loaded here, in straight-line code with their use (loads held across
+            // the staging code raise the register pressure of the whole kernel, which then
+            // spills around the GEMV phases); K rows go by DMA, the first tile's before the staging
+            if (t0 != j0) at_dma_k(c, Lp, t0, j1);  // the previous tile's QK is past its barriers
             AtPreKV P;
-            at_issue_kv(c, Lp, t0, j1, P);
+            at_issue_v(c, Lp, t0, j1, P);
             at_tile(c, Lp, t0, j1, P, acc, L);
             if (at_ext(t0, j1)) break;  // its extra keys were the split's last
           }
