@@ -1436,8 +1436,9 @@ DF_DEVICE void dn_state_prefetch(const Ctx& c, LayerPtr Lp, Lds& L) {
 //               runs the delta rule on value columns 2 w, 2 w + 1 over all 128 state rows (two
 //               rows per lane), so each column's recall and output are one wave's sums; the
 //               updated slice goes back to the LDS copy, the outputs to LDS;   | barrier
-//   dn_publish  control wave: the 16 outputs (tagged with their epoch), the new state slice and
-//               this position's conv history slots, to memory.
+//   dn_publish  control wave: the 16 outputs (tagged with their epoch), to memory; the new
+//               state slice and this position's conv history slots follow during out_proj's
+//               consume (dn_store_state).
 // The arithmetic and rounding points are the reference's (reference.py:407-461, 496-545); fp32
 // sums over the state rows run in a fixed order of their own.
 constexpr int kDnBars = 3;
@@ -1558,16 +1559,26 @@ DF_DEVICE void dn_math(const Ctx& c, Lds& L) {
   }
 }
 
-// Control wave, after the compute waves' delta rule: the 16 outputs tagged with `epoch_out`,
-// then the stores nobody waits for (a wave's memory operations leave in order): the new state
-// slice, and this position's conv history slot of the channels this unit owns (its v slice; the
-// key head's q/k for the (even value head, slice 0) unit).
+// Control wave, after the compute waves' delta rule: the 16 outputs tagged with `epoch_out`.
+// The stores nobody waits for follow in dn_store_state: the new state slice, and this
+// position's conv history slot of the channels this unit owns (its v slice; the key head's q/k
+// for the (even value head, slice 0) unit).
 DF_DEVICE void dn_publish(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_out) {
   auto& D = L.u.dn;
   const int hvl = c.r >> 3, vs = c.r & 7;
   const int hv = 4 * c.xcd + hvl;
   if (c.lane < 16) c.w.core[(size_t)c.xcd * 512 + hvl * kDk + vs * 16 + c.lane] = tag_bf16(f2bf(D.core[c.lane]), epoch_out);
   stamp(c, kTDnDone);
+}
+
+// Control wave, during out_proj's consume (off the hand-off path; the union's delta-step data
+// stays untouched until the MLP): the new state slice and this position's conv history slots
+// to memory. Read again only by the next token's same layer; the all-reduce's signal waits for
+// these stores with the rest.
+DF_DEVICE void dn_store_state(Ctx& c, LayerPtr Lp, Lds& L) {
+  auto& D = L.u.dn;
+  const int hvl = c.r >> 3, vs = c.r & 7;
+  const int hv = 4 * c.xcd + hvl;
   const int row0 = c.lane >> 2, col4 = (c.lane & 3) * 4;
   float* sbase = LF(Lp, state) + ((size_t)hv * kDk + row0) * kDk + vs * 16 + col4;
 #pragma unroll
@@ -2525,6 +2536,7 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
           stamp(c, kTStaged);
           dma_row(LF(Lp, post_norm), L.nw, hidden, c.lane);
           sync(c);  // g_x, group sums
+          dn_store_state(c, Lp, L);
           sync(c);  // blocks consumed
           rowpar_epilogue(g, c, L, hidden);
           if (!allreduce_residual(c, L, hidden)) return fail(1);
