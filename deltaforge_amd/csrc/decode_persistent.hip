@@ -1428,8 +1428,9 @@ DF_DEVICE void dn_state_prefetch(const Ctx& c, LayerPtr Lp, Lds& L) {
 // The Gated DeltaNet step of this workgroup's unit (value head hv = 4 x + r / 8, value columns
 // 16 (r % 8) .. + 15), in three parts around two barriers, so that the eight compute waves (idle
 // at out_proj's first barrier otherwise) carry the arithmetic:
-//   dn_stage    control wave: the in_proj hand-off (q, k of the key head, the unit's 16 v, a/b,
-//               the XCD's z) and the unit's conv taps and history into LDS;     | barrier
+//   dn_stage    control wave: the in_proj hand-off (q, k of the key head, the unit's 16 v, a/b)
+//               and the unit's conv taps and history into LDS (the XCD's z follows while the
+//               compute waves run the conv);                                     | barrier
 //   dn_conv     compute waves: the 4-tap conv + SiLU of the 272 channels, 34 per wave, and
 //               the gates on a spare lane;                                       | barrier
 //   dn_math     compute waves: q/k L2 norms (each wave, identically), then wave w
@@ -1465,13 +1466,14 @@ DF_DEVICE bool dn_stage(Ctx& c, LayerPtr Lp, Lds& L, uint32_t epoch_in) {
   }
   const float alog = bf2f(LF(Lp, A_log)[hv]), dtb = bf2f(LF(Lp, dt_bias)[hv]);
   const int khl = hvl >> 1;
-  const Seg seg[5] = {{kLinQ + khl * 128, 128, D.qkv_in},
+  // (z, the out_proj GatedRMSNorm's gate, is gathered while the compute waves run the conv:
+  // the delta step's own poll stays 6 loads per lane instead of 14)
+  const Seg seg[4] = {{kLinQ + khl * 128, 128, D.qkv_in},
                       {kLinK + khl * 128, 128, D.qkv_in + 128},
                       {kLinV + hvl * 128 + vs * 16, 16, D.qkv_in + 256},
-                      {kLinA, 8, D.ab8},
-                      {kLinZ, 512, L.zs}};
+                      {kLinA, 8, D.ab8}};
   // the state slice is in LDS: its DMA (dn_state_prefetch) preceded this poll
-  if (!gather_colpar<5, 7>(c, seg, epoch_in)) return false;
+  if (!gather_colpar<4, 3>(c, seg, epoch_in)) return false;
   stamp(c, kTDnLanded);
 #pragma unroll
   for (int i = 0; i < kCh; ++i) {
@@ -2524,7 +2526,13 @@ DF_DEVICE void control_main(const DfPersistModel& M, const Geo& q, Ctx& c, int s
         c.epoch += 1;
         // the compute waves run the conv and the delta rule between these barriers
         if (!dn_stage(c, Lp, L, c.epoch - 1)) return fail(1);
-        for (int i = 0; i < kDnBars; ++i) sync(c);
+        sync(c);  // the step's inputs in LDS: the compute waves run the conv
+        // meanwhile z (the out_proj GatedRMSNorm's gate, from the same input projection); a
+        // failed poll passes the step's barriers and stops where the compute waves next check
+        const Seg zseg[1] = {{kLinZ, 512, L.zs}};
+        const bool zok = gather_colpar<1, 4>(c, zseg, c.epoch - 1);
+        for (int i = 1; i < kDnBars; ++i) sync(c);
+        if (!zok) return fail(1);
         dn_publish(c, Lp, L, c.epoch);
         // ================= gated norm + out_proj (row-parallel) ======================
         {
