@@ -12,8 +12,8 @@
 //
 // Work split: a workgroup of 8 waves owns NT 16-column tiles; the 8/NT waves that share a
 // tile split its K range, and their fp32 partials are summed in LDS in a fixed order. Each
-// wave keeps 8 groups (8 KB of weights per wave) in flight. Each group is one fully
-// coalesced 1 KB load (64 lanes x 16 B).
+// wave keeps 12 groups (8 for the logits epilogue) in flight, 1 KB of weights each. Each group
+// is one fully coalesced 1 KB load (64 lanes x 16 B).
 //
 // Arithmetic is the reference's (kernels/visible_int4_head.py:187-199): every weight is
 // dequantised to bf16((nibble - 8) * scale) -- (nibble - 8) * scale is exact in fp32 and
@@ -34,7 +34,13 @@ namespace df {
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxRows = 16;
-constexpr int kDepth = 8;  // groups in flight per wave
+// Groups in flight per wave. 12 puts a whole K range of the decode's MLP shapes (9 to 10
+// groups per wave at 1 row, 9 to 20 at 16) in flight at once or nearly: MLP block 23.5 ->
+// 22.3 us at 1 row and 35.4 -> 33.8 us at 16 rows, against 8. The head's 20-group ranges ran
+// 1.6 to 2.7 % slower with 12 than with 8 (and 16 or 20 were slower everywhere), so the logits
+// epilogue keeps 8.
+template <int EPI>
+constexpr int depth_of() { return EPI == DF_EPI_LOGITS ? 8 : 12; }
 constexpr int kNormChunks = 3;  // RMSNorm prologue: K <= kNormChunks * kThreads * 8 = 12288
 constexpr int kRowChunks = 5;   // ... one wave per row when K <= kRowChunks * 64 * 8 = 2560
 constexpr int kGemvLds = 100 * 1024;  // LDS bytes a workgroup may take
@@ -279,6 +285,7 @@ template <int PRO, int EPI, int NT, bool WROWS>
 __global__ __launch_bounds__(kThreads) void w4_gemv_kernel(DfInt4GemvArgs p) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int KS = kWaves / NT;
+  constexpr int kDepth = depth_of<EPI>();
   constexpr int COLS = NT * kTileCols;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int tsub = wave % NT, kpart = wave / NT;
