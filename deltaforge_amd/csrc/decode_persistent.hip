@@ -346,6 +346,12 @@ DF_DEVICE int uniform_int(int v) { return __builtin_amdgcn_readfirstlane(v); }
 DF_DEVICE uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
 }
+// 16 bytes from LDS through an LDS pointer (a ds_read whatever the compiler knows of p).
+DF_DEVICE uint4 lds_ld16(const void* p) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((const __attribute__((address_space(3))) char*)p);
+  return __builtin_bit_cast(uint4, v);
+}
 
 // Workgroup barrier that orders LDS only. __syncthreads() is a workgroup-scope release
 // fence, which on gfx950 waits for every outstanding vector memory operation of the wave
@@ -1734,10 +1740,12 @@ DF_DEVICE void at_tile(Ctx& c, LayerPtr Lp, int t0, int j1, const AtPreKV& P, fl
     df_f32x4 d4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
-      uint4 kn = *reinterpret_cast<const uint4*>(A.knew + d * 32 + slot * 8);
-      asm volatile("" : "+v"(kn.x), "+v"(kn.y), "+v"(kn.z), "+v"(kn.w));  // a value, not a pointer select into the ring
+      // both rows by LDS loads (a generic pointer on one side would make the select a flat load
+      // that waits for every outstanding vector memory operation, the tile's V rows included)
+      const uint4 kn = lds_ld16(A.knew + d * 32 + slot * 8);
+      const uint4 kr = lds_ld16(&g_ring_w[c.wave][d][c.lane]);
       uint4 bw = make_uint4(0u, 0u, 0u, 0u);
-      if (live) bw = key == c.pos ? kn : g_ring_w[c.wave][d][c.lane];
+      if (live) bw = key == c.pos ? kn : kr;
       uint4 aw = make_uint4(0u, 0u, 0u, 0u);
       if (col < 2) aw = *reinterpret_cast<const uint4*>(&A.q[col][d * 32 + slot * 8]);
       d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(df_bf16x8, aw), __builtin_bit_cast(df_bf16x8, bw),
