@@ -1588,15 +1588,20 @@ DF_DEVICE void dn_store_state(Ctx& c, LayerPtr Lp, Lds& L) {
   const int hvl = c.r >> 3, vs = c.r & 7;
   const int hv = 4 * c.xcd + hvl;
   const int row0 = c.lane >> 2, col4 = (c.lane & 3) * 4;
-  float* sbase = LF(Lp, state) + ((size_t)hv * kDk + row0) * kDk + vs * 16 + col4;
+  // global-address stores: a flat store (the layer table's pointers are generic) would count
+  // on the LDS counter too, and the next barrier's lgkmcnt(0) would wait for its write
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  auto* sbase = (__attribute__((address_space(1))) float*)(LF(Lp, state) + ((size_t)hv * kDk + row0) * kDk + vs * 16 + col4);
 #pragma unroll
-  for (int i = 0; i < kDk / 16; ++i) *reinterpret_cast<float4*>(sbase + (size_t)16 * i * kDk) = D.S[i][c.lane];
+  for (int i = 0; i < kDk / 16; ++i)
+    *(__attribute__((address_space(1))) f32x4*)(sbase + (size_t)16 * i * kDk) = __builtin_bit_cast(f32x4, D.S[i][c.lane]);
+  auto* ring = (__attribute__((address_space(1))) uint16_t*)LF(Lp, conv_ring);
   constexpr int kCh = (kDnCh + 63) / 64;
 #pragma unroll
   for (int i = 0; i < kCh; ++i) {
     const int ch = c.lane + 64 * i;
     const bool owner = ch >= 2 * kDk || ((hvl & 1) == 0 && vs == 0);
-    if (ch < kDnCh && owner) LF(Lp, conv_ring)[(size_t)dn_channel(c, ch) * 4 + (c.pos & 3)] = f2bf(D.qkv_in[ch]);
+    if (ch < kDnCh && owner) ring[(size_t)dn_channel(c, ch) * 4 + (c.pos & 3)] = f2bf(D.qkv_in[ch]);
   }
 }
 
