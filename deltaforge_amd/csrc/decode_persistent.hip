@@ -528,6 +528,7 @@ struct Gemv {
   int tile0;       // first tile of the XCD slice
   int g0, ng;      // group slice
   int b_lo, b_hi;  // this workgroup's block range (relative to the slice, tile-major)
+  int k;           // phase: 0 input projection, 1 out_proj / o_proj, 2 gate|up, 3 down
 };
 
 // Phase k of a layer of kind `kind` (phases: 0 input projection, 1 out_proj / o_proj,
@@ -537,14 +538,14 @@ DF_DEVICE Gemv gemv_geom(int kind, const Geo& q, int k, int xcd, int r) {
   if (k == 0) {
     const int nt = (kind == 0 ? kLinCols : kAttnCols) / kTileCols;
     const int B = nt * q.Gh;
-    g = Gemv{nullptr, nullptr, q.Gh, xcd * nt, 0, q.Gh, (r * B) / kPerXcd, ((r + 1) * B) / kPerXcd};
+    g = Gemv{nullptr, nullptr, q.Gh, xcd * nt, 0, q.Gh, (r * B) / kPerXcd, ((r + 1) * B) / kPerXcd, 0};
   } else if (k == 1) {
-    g = Gemv{nullptr, nullptr, 4096 / kGroup, 0, xcd * 4, 4, q.rp_lo * 4, q.rp_hi * 4};
+    g = Gemv{nullptr, nullptr, 4096 / kGroup, 0, xcd * 4, 4, q.rp_lo * 4, q.rp_hi * 4, 1};
   } else if (k == 2) {
     const int B = q.gu_tiles * q.Gh;
-    g = Gemv{nullptr, nullptr, q.Gh, xcd * q.gu_tiles, 0, q.Gh, (r * B) / kPerXcd, ((r + 1) * B) / kPerXcd};
+    g = Gemv{nullptr, nullptr, q.Gh, xcd * q.gu_tiles, 0, q.Gh, (r * B) / kPerXcd, ((r + 1) * B) / kPerXcd, 2};
   } else {
-    g = Gemv{nullptr, nullptr, q.inter / kGroup, 0, xcd * q.ngx, q.ngx, q.rp_lo * q.ngx, q.rp_hi * q.ngx};
+    g = Gemv{nullptr, nullptr, q.inter / kGroup, 0, xcd * q.ngx, q.ngx, q.rp_lo * q.ngx, q.rp_hi * q.ngx, 3};
   }
   return g;
 }
@@ -578,23 +579,29 @@ DF_DEVICE Gemv gemv_of(LayerPtr Lp, const Geo& q, int k, int xcd, int r) {
 // A compute wave's share of a workgroup's blocks. Wave w runs on SIMD w % 4, so waves 4..7
 // share their SIMD with the older waves 0..3, which win the issue arbitration: with equal
 // shares the younger waves finished 15-25 % later and the phase waited for them while each
-// SIMD ran one wave. Shares of 3 : 2 (waves 0..3 : 4..7) decode fastest of 1 : 1, 6 : 5,
-// 5 : 4, 3 : 2, 7 : 4 and 2 : 1 (same-box A/B).
-constexpr int kShareOld = 3, kShareYoung = 2, kShares = 4 * (kShareOld + kShareYoung);
+// SIMD ran one wave. One ratio for every phase, 3 : 2 (waves 0..3 : 4..7), decoded fastest of
+// 1 : 1, 6 : 5, 5 : 4, 3 : 2, 7 : 4 and 2 : 1; the traced finish stamps then showed the older
+// waves last in the input projection and the younger ones last in down, so the older wave's
+// share of its SIMD pair is set per phase, in 40ths: input projection 22 (11 : 9), out_proj /
+// o_proj 24 (3 : 2), gate|up 25 (5 : 3), down 26 (13 : 7); 0.6 % per token over one ratio
+// (same-box A/Bs of 12 settings). The head keeps 3 : 2.
+constexpr int kSharePair = 40, kShares = 4 * kSharePair, kShareHead = 24;
 static_assert(kCompute == 8, "two waves per SIMD");
-DF_DEVICE int share_before(int wave) {
-  return wave <= 4 ? kShareOld * wave : 4 * kShareOld + kShareYoung * (wave - 4);
+DF_DEVICE int share_old(int k) { return k == 0 ? 22 : k == 1 ? 24 : k == 2 ? 25 : 26; }
+DF_DEVICE int share_before(int a, int wave) {
+  return wave <= 4 ? a * wave : 4 * a + (kSharePair - a) * (wave - 4);
 }
 DF_DEVICE void wave_range(const Gemv& g, int wave, int& lo, int& n) {
   const int len = g.b_hi - g.b_lo;
-  lo = g.b_lo + (len * share_before(wave)) / kShares;
-  n = g.b_lo + (len * share_before(wave + 1)) / kShares - lo;
+  const int a = share_old(g.k);
+  lo = g.b_lo + (len * share_before(a, wave)) / kShares;
+  n = g.b_lo + (len * share_before(a, wave + 1)) / kShares - lo;
 }
 
-// The head's vocabulary tiles t_lo .. t_hi of the workgroup, in the same weighted shares: wave
-// w takes the contiguous tiles head_tile(w) .. head_tile(w + 1), one run of its stream.
+// The head's vocabulary tiles t_lo .. t_hi of the workgroup, in weighted shares: wave w takes
+// the contiguous tiles head_tile(w) .. head_tile(w + 1), one run of its stream.
 DF_DEVICE int head_tile(const Geo& q, int wave) {
-  return q.t_lo + ((q.t_hi - q.t_lo) * share_before(wave)) / kShares;
+  return q.t_lo + ((q.t_hi - q.t_lo) * share_before(kShareHead, wave)) / kShares;
 }
 
 // A compute wave's weight stream: the wave's 1 KB blocks of every GEMV phase of every layer
