@@ -584,8 +584,9 @@ DF_DEVICE Gemv gemv_of(LayerPtr Lp, const Geo& q, int k, int xcd, int r) {
 // waves last in the input projection and the younger ones last in down, so the older wave's
 // share of its SIMD pair is set per phase, in 40ths: input projection 22 (11 : 9), out_proj /
 // o_proj 24 (3 : 2), gate|up 25 (5 : 3), down 26 (13 : 7); 0.6 % per token over one ratio
-// (same-box A/Bs of 12 settings). The head keeps 3 : 2.
-constexpr int kSharePair = 40, kShares = 4 * kSharePair, kShareHead = 24;
+// (same-box A/Bs of 12 settings). The head's tiles go 7 : 3 (28; 0.3 % over 3 : 2, and 3 : 1
+// or 4 : 1 lost 1.1 %).
+constexpr int kSharePair = 40, kShares = 4 * kSharePair, kShareHead = 28;
 static_assert(kCompute == 8, "two waves per SIMD");
 DF_DEVICE int share_old(int k) { return k == 0 ? 22 : k == 1 ? 24 : k == 2 ? 25 : 26; }
 DF_DEVICE int share_before(int a, int wave) {
