@@ -76,7 +76,7 @@ GATE_UP_TRAFFIC_BYTES = 12049 * 1024 * 2 + 18 * 1024
 # HBM bytes per decode token of the persistent kernel from the calibrated PMC passes over the
 # timed 256-token launch (334,344,530.5 KiB fetched x 1.99982, 17,625,739.0 KiB written, / 256),
 # recorded with their commands in PERSISTENT_TRAFFIC_SOURCE. Re-measure when the kernel changes.
-PERSISTENT_TRAFFIC_BYTES_PER_TOKEN = 2760872418
+PERSISTENT_TRAFFIC_BYTES_PER_TOKEN = 2739225546
 PERSISTENT_TRAFFIC_SOURCE = ("profiles/decode_persistent_config5.md: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
                              "over bench.py --steps 256, scaled by a 256 MiB copy in the same process")
 
